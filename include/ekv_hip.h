@@ -1,0 +1,202 @@
+/*
+ * ekv_hip.h -- C ABI of libekv_hip.so, the MI355X (gfx950) implementation of KVScope's
+ * audit / tile-share / ranking / block-table-view hot path.
+ *
+ * Every entry point takes raw device pointers, element strides, sizes and a hipStream_t
+ * (passed as void*; NULL is the null stream).  No entry point allocates device memory
+ * except the explicit memory helpers at the end, so the compute calls can run inside a
+ * captured HIP graph.  Every call returns an int status:
+ *
+ *   EKV_OK           0   success
+ *   EKV_EINVAL      -1   an argument is out of range (the Python layer raises ValueError)
+ *   EKV_ELAUNCH     -2   a HIP call or kernel launch failed (RuntimeError)
+ *   EKV_EUNSUPPORTED -3  the shape / dtype combination has no compiled kernel (ValueError)
+ *
+ * ekv_last_error() returns a message for the last failing call on the calling thread.
+ *
+ * Layout of the statistic planes (the layout the reference's pass and audit kernel write,
+ * runtime/audit_kernel.py:97-109 and observe/tile_shares.py:4-11):
+ *   float32 [2][layers][rows][width][cells]   plane 0 = tile max m, plane 1 = tile sum l
+ * with `cells` = query rows recorded per block.  Unwritten cells keep whatever the caller
+ * put there (the plane is NaN-filled once at allocation, runtime/audit_kernel.py:137).
+ */
+#ifndef EKV_HIP_H
+#define EKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EKV_OK 0
+#define EKV_EINVAL (-1)
+#define EKV_ELAUNCH (-2)
+#define EKV_EUNSUPPORTED (-3)
+
+/* element types of q / K */
+#define EKV_F32 0
+#define EKV_F16 1
+#define EKV_BF16 2
+#define EKV_FP8_E4M3 3 /* OCP e4m3fn, dequantised as k_scale * value */
+
+/* aggregates of the share normalisation (observe/tile_shares.py:55) */
+#define EKV_AGG_MEAN 0
+#define EKV_AGG_MAX 1
+
+const char *ekv_last_error(void);
+int ekv_abi_version(void);
+
+/*
+ * A1 + A10: the audit statistic of one attention layer.
+ * Replaces tile_lse_kernel and its launch, runtime/audit_kernel.py:34-109 and :224-265.
+ *
+ * For every row r with *flag != 0 and select[r] != 0, every tile of tile_blocks (= 2) blocks
+ * that starts before lens[r], and every query row q of the audited KV heads
+ * group_first .. group_first + groups - 1, the kernel stores
+ *     m = max_j s_j,   l = sum_j exp(s_j - m),   s_j = scale * k_scale * <q, k_j>
+ * over the tile's keys j < lens[r], into plane 0 / plane 1 at
+ *     lse[plane * lse_plane_stride + layer * lse_layer_stride + r * lse_row_stride
+ *         + b * cells + h * group_rows + q]                 (h = 0 .. groups - 1)
+ * for each block b of the tile with b * block_size < lens[r].  groups = 1 with
+ * group_first = layer % kv_heads is the reference's one-group-per-layer audit
+ * (runtime/audit_kernel.py:250); groups = kv_heads audits every KV head.
+ *
+ * q      : [tokens, q_heads, head_dim] with strides (q_stride_token, q_stride_head), row r's
+ *          query is token qrow[r]; its KV head h uses query heads h*group_rows .. +group_rows-1.
+ * keys   : element (blk, pos, h, dim) at blk*k_stride_block + pos*k_stride_pos + h*k_stride_head + dim
+ *          (the keys view kv_cache[:, 0] of a [blocks, 2, block, heads, dim] cache).
+ * table  : int32 [rows, >= width] with row stride table_stride; lens, qrow: int32 [rows];
+ *          select: uint8 [rows]; flag: uint32 device scalar.
+ * cycles : optional uint64 [cycles_rows]; when non-NULL every unit of work adds its
+ *          s_memtime duration to cycles[r] (r < cycles_rows), for the first audited head only
+ *          (the pass's timer, mlir_pass/lib/eKVTimer.cpp:1348-1387).
+ * chunk_tiles: tiles per work unit (0 = the library's default).
+ */
+int ekv_audit_tile_lse(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                       const void *keys, int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos,
+                       int64_t k_stride_head, float k_scale, const int32_t *table, int64_t table_stride,
+                       const int32_t *lens, const int32_t *qrow, const uint8_t *select,
+                       const uint32_t *flag, float *lse, int64_t lse_plane_stride,
+                       int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells,
+                       uint64_t *cycles, int32_t cycles_rows, float scale, int32_t layer,
+                       int32_t group_first, int32_t groups, int32_t group_rows, int32_t rows,
+                       int32_t width, int32_t block_size, int32_t tile_blocks, int32_t head_dim,
+                       int32_t chunk_tiles, void *stream);
+
+/*
+ * A4 + A5: exact per-block attention shares of the chosen rows, from the statistic planes.
+ * Replaces read_tile_rows + normalize_tile_lse (observe/tile_shares.py:129-173 and :58-103),
+ * computing on the device what the reference copies to the host and normalises with NumPy.
+ *
+ * For output row i the source row is row_ids[i] (row_ids NULL: row i), of row_blocks[i]
+ * blocks (row_blocks NULL: all `width`).  The statistic is read for layers 0 .. layers-1 and
+ * the `cells` query rows of each block:  u = m + log(l) - log(tile_blocks), a partial last tile's
+ * blocks regain log(tile_blocks / valid_in_tail), cells at b >= row_blocks are dropped, each
+ * (layer, query row) with a finite value is a softmax over the row's blocks, and the result
+ * is their mean (EKV_AGG_MEAN) or the renormalised per-block max (EKV_AGG_MAX).
+ * shares[i * shares_stride + b], float32, b < width: 0 beyond the row's blocks, all NaN for
+ * a row with no finite value.
+ */
+int ekv_tile_shares(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
+                    int64_t lse_row_stride, int32_t layers, int32_t cells, int32_t width,
+                    const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
+                    int32_t tile_blocks, int32_t aggregate, float *shares, int64_t shares_stride,
+                    void *stream);
+
+/*
+ * The same normalisation from u values already formed, u[layer][row][block][cell]
+ * (normalize_tile_lse's own input, observe/tile_shares.py:58-103).
+ */
+int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row_stride,
+                           int32_t layers, int32_t cells, int32_t width, const int32_t *row_blocks,
+                           int32_t nrows, int32_t tile_blocks, int32_t aggregate, float *shares,
+                           int64_t shares_stride, void *stream);
+
+/*
+ * A6 + A7: the `uniform` budget split and the per-row ranking, on the device.
+ * Replaces Controller._allocate's pin / budget rules (observe/controller.py:398-451) feeding
+ * allocate(..., "uniform") (observe/allocation.py:39-91).
+ *
+ * Rows with measured[r] != 0 (measured NULL: every row) and blocks[r] > 0 take part.
+ *  - pinned block of row r: pinned[r, b] != 0 when `pinned` is given (Request.pinned);
+ *    otherwise block 0, blocks >= max(0, n-1-recent_blocks), and blocks >= pin_from[r]
+ *    (pin_from NULL: none).
+ *  - released[r, b] != 0 (NULL: none) removes block b from the request (controller.py:425-431).
+ *  - budget >= 0 is used as given (allocate's budget); budget < 0 computes the controller's
+ *    max(floor, ceil(fraction * total)) in IEEE double, total = sum of blocks[r].
+ *  - free blocks are split by largest remainder in IEEE double, then each row keeps its quota
+ *    of open blocks by (share desc, block index asc).  Shares are max(score, 0) as float32.
+ * keep[r, b] (uint8, row stride keep_stride) is written for every r < rows, b < width: 1 for
+ * rows that do not take part and for b >= blocks[r], else pinned | chosen, 0 for released.
+ * summary (optional int64[6]): budget, total, floor (pinned blocks), status, requests, free.
+ * status != 0 means the budget could not hold the pinned blocks (allocate's ValueError).
+ * Explicit pinned / released masks need ekv_rank_uniform_ws; ekv_rank_uniform rejects them.
+ */
+int ekv_rank_uniform(const float *scores, int64_t scores_stride, const int32_t *blocks,
+                     const uint8_t *measured, const uint8_t *pinned, int64_t pinned_stride,
+                     const int32_t *pin_from, int32_t recent_blocks, const uint8_t *released,
+                     int64_t released_stride, int32_t rows, int32_t width, double fraction,
+                     int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                     void *stream);
+
+/*
+ * ekv_rank_uniform with a caller-owned device workspace of 2 * rows int32, where a first
+ * kernel counts each row's existing and pinned blocks when explicit masks are given.
+ */
+int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_t *blocks,
+                        const uint8_t *measured, const uint8_t *pinned, int64_t pinned_stride,
+                        const int32_t *pin_from, int32_t recent_blocks, const uint8_t *released,
+                        int64_t released_stride, int32_t rows, int32_t width, double fraction,
+                        int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                        int32_t *workspace, void *stream);
+
+/*
+ * A8: compact_block_table (runtime/block_view.py:36-56).
+ * keep'[r, b] = (keep[r, b] | b == 0 | b == n-1) & b < n,  n = ceil(seq_lens[r] / block_size).
+ * view_table row r = table row r stably partitioned: keep' entries first, the rest after them,
+ * each in original order (all `width` entries).  view_lens[r] = (sum keep' - 1) * block_size
+ * + seq_lens[r] - (n-1) * block_size for n > 0, else 0.
+ */
+int ekv_compact_view(const int32_t *table, int64_t table_stride, const int32_t *seq_lens,
+                     const uint8_t *keep, int64_t keep_stride, int32_t rows, int32_t width,
+                     int32_t block_size, int32_t *view_table, int64_t view_stride,
+                     int32_t *view_lens, void *stream);
+
+/*
+ * A8 + A9: DecodeView.build's keep composition fused with the compaction and the read
+ * counters (runtime/block_view.py:272-295 and :297-329).
+ * keep = committed | !live | audited[r] | !decoding[r], then & !released  (committed NULL:
+ * all ones; audited / decoding / released NULL: none / all decoding / none).
+ * counts (optional int64[5], accumulated): read, full, audit, untrimmed, expired blocks of
+ * decode rows, as DecodeView._count.  view_table and view_lens may be NULL (counts only, as
+ * DecodeView.skip needs).
+ */
+int ekv_build_view(const int32_t *table, int64_t table_stride, const int32_t *seq_lens,
+                   const uint8_t *committed, int64_t committed_stride, const uint8_t *released,
+                   int64_t released_stride, const uint8_t *audited, const uint8_t *decoding,
+                   int32_t live, int32_t rows, int32_t width, int32_t block_size,
+                   int32_t *view_table, int64_t view_stride, int32_t *view_lens, int64_t *counts,
+                   void *stream);
+
+/*
+ * Device memory, copies and IPC for the statistic planes.  They replace the ctypes calls
+ * into libcudart of runtime/audit.py:17-23, :55-60, runtime/audit_kernel.py:146-158 and
+ * observe/cuda.py:12-58.  These are not for hot loops.
+ */
+int ekv_malloc(void **ptr, size_t bytes);
+int ekv_free(void *ptr);
+int ekv_memset(void *ptr, int value, size_t bytes);
+int ekv_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int ekv_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int ekv_ipc_handle(const void *ptr, uint8_t handle[64]);
+int ekv_ipc_open(const uint8_t handle[64], void **ptr);
+int ekv_synchronize(void);
+int ekv_device_count(int *count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EKV_HIP_H */

@@ -1,0 +1,123 @@
+"""GPU parity of the share normalisation (ekv_normalize_tile_lse / ekv_tile_shares) with the oracle:
+the reference's known answers and random records with NaN, -inf, partial tails and rows past the
+width, within 1e-4 (observe/tile_shares.py:58-173 of the reference)."""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import lse_of
+from observe import tile_shares
+from observe.hip import Hip
+from oracle import tile_shares as ots
+
+pytestmark = pytest.mark.gpu
+SHARE_TOL = 1e-4
+
+
+def assert_close(got, want, tol=SHARE_TOL, what=""):
+    assert got.shape == want.shape
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"{what}: NaN rows differ"
+    err = np.nanmax(np.abs(np.nan_to_num(got - want))) if got.size else 0.0
+    print(f"{what}: max |d share| {err:.2e}", flush=True)
+    assert err <= tol, what
+
+
+def test_known_answers(known_answers):
+    for case in known_answers["tile_shares"]:
+        got = tile_shares.normalize_tile_lse(lse_of(case), np.array(case["row_blocks"]), case["tile_blocks"],
+                                             case["aggregate"])
+        assert got.dtype == np.float64
+        assert_close(got, np.array(case["expected"], dtype=np.float64), 1e-6, case["name"])
+
+
+def random_records(rng, layers, rows, width, cells, tile_blocks):
+    lse = rng.normal(0, 4, (layers, rows, width, cells)).astype(np.float32)
+    lse[rng.random(lse.shape) < 0.05] = np.nan  # unwritten cells
+    lse[rng.random(lse.shape) < 0.03] = -np.inf  # empty tiles
+    lse[:, 0] = np.nan  # a row without evidence
+    if rows > 2:
+        lse[:, 2, :, 1:] = np.nan  # a row whose other query rows have no data
+    row_blocks = rng.integers(0, width + 3, size=rows)  # partial tails and rows past the width
+    return lse, row_blocks
+
+
+@pytest.mark.parametrize("tile_blocks", [1, 2, 3, 4])
+@pytest.mark.parametrize("aggregate", ["mean", "max"])
+def test_random_records_match_the_oracle(tile_blocks, aggregate):
+    rng = np.random.default_rng(100 + tile_blocks)
+    for layers, rows, width, cells in ((1, 5, 7, 1), (3, 9, 33, 4), (32, 6, 512, 4), (2, 4, 130, 32), (4, 3, 64, 5)):
+        lse, row_blocks = random_records(rng, layers, rows, width, cells, tile_blocks)
+        got = tile_shares.normalize_tile_lse(lse, row_blocks, tile_blocks, aggregate)
+        want = ots.normalize(lse, row_blocks, tile_blocks, aggregate)
+        assert_close(got, want, what=f"{layers}x{rows}x{width}x{cells} T={tile_blocks} {aggregate}")
+        live = ~np.isnan(want).all(axis=1)
+        assert np.abs(got[live].sum(axis=1) - 1).max() < 1e-5
+
+
+def test_device_tensor_in_device_tensor_out():
+    rng = np.random.default_rng(7)
+    lse, row_blocks = random_records(rng, 2, 4, 40, 4, 2)
+    got = tile_shares.normalize_tile_lse(torch.from_numpy(lse).cuda(), torch.from_numpy(row_blocks), 2)
+    assert got.is_cuda and got.dtype == torch.float32
+    assert_close(got.cpu().numpy().astype(np.float64), ots.normalize(lse, row_blocks, 2), what="device in/out")
+
+
+def planes_on_device(planes):
+    return torch.from_numpy(np.ascontiguousarray(planes)).cuda()
+
+
+def test_fused_read_and_normalise_matches_reader_plus_oracle():
+    rng = np.random.default_rng(11)
+    table_layers, layers, rows, width, cells, tile = 6, 4, 10, 96, 4, 2
+    m = rng.normal(0, 3, (table_layers, rows, width, cells)).astype(np.float32)
+    l = rng.uniform(0.5, 30, (table_layers, rows, width, cells)).astype(np.float32)
+    l[rng.random(l.shape) < 0.02] = 0.0
+    m[:, 3] = np.nan
+    planes = np.stack([m, l])
+    dev = planes_on_device(planes)
+    row_ids = np.array([1, 2, 3, 7, 9])
+    row_blocks = np.array([96, 13, 50, 1, 95])
+    got = tile_shares.tile_shares(dev.data_ptr(), table_layers, layers, rows, width, cells,
+                                  torch.from_numpy(row_ids.astype(np.int32)).cuda(),
+                                  torch.from_numpy(row_blocks.astype(np.int32)).cuda(), tile)
+    torch.cuda.synchronize()
+    want = ots.normalize(ots.read_rows(planes, layers, row_ids, tile), row_blocks, tile)
+    assert_close(got.cpu().numpy().astype(np.float64), want, what="fused read + normalise")
+
+
+def test_host_reader_through_hip_equals_the_oracle_reader():
+    rng = np.random.default_rng(12)
+    planes = np.stack([rng.normal(0, 3, (3, 6, 4, 2)), rng.uniform(0.5, 9, (3, 6, 4, 2))]).astype(np.float32)
+    planes[1, 0, 0, 3, 1] = 0.0
+    dev = planes_on_device(planes)
+    hip = Hip()
+    chosen = np.array([1, 2, 5])
+    got = tile_shares.read_tile_rows(hip, dev.data_ptr(), 3, 2, 6, 4, 2, chosen, 2)
+    want = ots.read_rows(planes, 2, chosen, 2)
+    assert np.array_equal(got, want)
+    assert tile_shares.read_tile_lse(hip, dev.data_ptr(), 3, 2, 6, 4, 2, 2, 2)[0, 0, 3, 1] == -np.inf
+
+
+def test_device_share_source_reads_only_live_rows(tmp_path, monkeypatch):
+    # the controller-side source with the normalisation on the device answers like the reference's
+    # TileShareSource.read: NaN rows without evidence, rows of 0 blocks not read
+    monkeypatch.setenv("EKV_RUNTIME_DIR", str(tmp_path))
+    from runtime.audit_kernel import RecordingPlane
+
+    plane = RecordingPlane(4, 5, 8, 2, 16)
+    rng = np.random.default_rng(3)
+    planes = np.stack([rng.normal(0, 2, (4, 5, 8, 2)), rng.uniform(1, 5, (4, 5, 8, 2))]).astype(np.float32)
+    import ekv_hip
+
+    ekv_hip.h2d(plane.lse_address, planes.tobytes())
+    plane.attach([1111, 2222])  # two layers have caches
+    import os
+
+    entry = tile_shares.share_descriptor(os.getpid())
+    source = tile_shares.DeviceTileShareSource(Hip(), entry, os.getpid())
+    row_blocks = np.array([8, 0, 5, 3, 8])
+    got = source.read(4, row_blocks)
+    assert np.isnan(got[1]).all()
+    want = ots.normalize(ots.read_rows(planes, 2, np.array([0, 2, 3]), 2), row_blocks[[0, 2, 3]], 2)
+    assert_close(got[[0, 2, 3]], want, what="device share source")

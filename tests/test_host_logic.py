@@ -1,0 +1,73 @@
+"""Host-side logic of the drop-in modules that needs no device: DecodeView's controller-facing state
+(runtime/block_view.py:133-218), Request and allocate's argument rules (observe/allocation.py:31-76),
+the descriptor helpers."""
+
+import numpy as np
+import pytest
+
+from observe import allocation
+from observe.zero_touch import pub_path, read_json_lines
+from runtime.block_view import DecodeView
+
+
+class FakePlane:
+    def set(self, on):
+        pass
+
+    def select(self, audited, token_start):
+        pass
+
+
+def test_view_writes_validate_their_shapes():
+    view = DecodeView(rows=2, width=4, block_size=16)
+    with pytest.raises(ValueError):
+        view.write_row_controls(np.ones((2, 4)), np.zeros((2, 4), dtype=np.float32))
+    with pytest.raises(ValueError):
+        view.write_row_controls(np.ones((3, 4)))
+    with pytest.raises(ValueError):
+        view.write_audit_rows(np.array([True, False]))  # no plane to switch the statistic on
+    with pytest.raises(ValueError):
+        DecodeView(rows=2, width=4, block_size=16, prefill_audit=True)
+    with pytest.raises(ValueError):
+        DecodeView(rows=0, width=4, block_size=16)
+
+
+def test_release_rules_and_row_moves():
+    view = DecodeView(rows=2, width=4, block_size=16, audit=FakePlane())
+    ask = np.array([[1, 1, 1, 1], [0, 0, 0, 0]], dtype=np.uint8)
+    assert view.write_release(ask) == []  # before any audit
+    view.row_audited[0] = True
+    view.audited_blocks[0] = 4
+    assert view.write_release(ask) == [(0, 1), (0, 2)]  # never block 0 nor the last audited block
+    assert view.write_release(ask) == []
+    view.reassign_rows({1: 0, 0: 1}, [], [])
+    assert view.released[1].tolist() == [False, True, True, False]
+    view.reassign_rows({}, [1], [])
+    assert not view.released[1].any() and not view.row_audited[1] and view.audit_rows[1]
+
+
+def test_request_pins_and_shares():
+    r = allocation.Request(scores=np.array([0.0, 2.0, 2.0, -1.0]))
+    assert r.pinned_mask().tolist() == [True, False, False, True]
+    assert r.shares().tolist() == [0.0, 0.5, 0.5, 0.0]
+    assert allocation.Request(scores=np.zeros(4)).shares().tolist() == [0.25] * 4
+
+
+def test_allocate_argument_rules():
+    reqs = [allocation.Request(scores=np.ones(5)), allocation.Request(scores=np.ones(5))]
+    with pytest.raises(ValueError):
+        allocation.allocate(reqs, 3, "uniform")
+    with pytest.raises(ValueError):
+        allocation.allocate(reqs, -1, "uniform")
+    with pytest.raises(ValueError):
+        allocation.allocate([allocation.Request(scores=np.ones(4), weight=2.0), reqs[0]], 5, "uniform")
+    assert all(m.all() for m in allocation.allocate(reqs, 10, "uniform"))
+
+
+def test_descriptor_paths(tmp_path, monkeypatch):
+    monkeypatch.setenv("EKV_RUNTIME_DIR", str(tmp_path))
+    path = pub_path(42)
+    assert path == f"{tmp_path}/ekv_pass_42.json"
+    with open(path, "w") as f:
+        f.write('{"a": 1}\n\n{"b": 2}\n')
+    assert read_json_lines(path) == [{"a": 1}, {"b": 2}]
