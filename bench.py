@@ -1,0 +1,393 @@
+"""Benchmark of the audit / share / ranking / view hot path on one MI355X.
+
+Workload: the Llama-3-8B decode shape -- 128 rows with contexts U[512, 8192] tokens, 32 query /
+8 KV heads, head_dim 128, bf16, block size 16, a pool of 100k blocks per layer, 32 layers.  A step
+is one decode step's worth of the path: the audit kernel after each of the 32 layers (layer L reads
+KV group L mod 8 of its own cache; the caches rotate over 4 distinct pools so that the 144 MB a
+launch reads is never served by the 256 MB Infinity Cache), the share normalisation over the 32
+layers, the uniform ranking at budget 0.5 (first block and 4 newest pinned) and the block-table
+view build.  The step is captured once into a HIP graph and replayed (the launches are identical
+every step; the audit flag lives on the device).
+
+value = audited KV bytes (algorithmic, below) per step / step time.  Per audit launch:
+  B = sum_r L_r*d*2 (keys) + sum_r n_r*4 (table) + R*G*d*2 (queries) + R*8 (lengths, token)
+      + 2*sum_r n_r*G*4 (m and l cells written)
+roofline.achieved = B / the mean duration of an audit launch, timed with HIP events on the launch
+stream.  The CPU baseline is the oracle's PyTorch-CPU form of the audit on a bounded sample.
+
+Only one GPU is used: ``--gpus N`` with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sigmod-kvscope_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 32
+POOLS = 4
+FRACTION = 0.5
+RECENT = 4
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--chunk-tiles", type=int, default=0)
+    ap.add_argument("--profile-only", action="store_true", help="run the graph replays only (for rocprof)")
+    return ap.parse_args()
+
+
+def audit_bytes(batch, audited_heads: int = 1) -> int:
+    lens = batch.lens.astype("int64")
+    n = batch.blocks.astype("int64")
+    g, d = batch.group_rows, batch.head_dim
+    return int(
+        lens.sum() * d * 2 * audited_heads
+        + n.sum() * 4
+        + batch.rows * g * audited_heads * d * 2
+        + batch.rows * 8
+        + 2 * n.sum() * g * audited_heads * 4
+    )
+
+
+class Step:
+    """Preallocated buffers and the launches of one step."""
+
+    def __init__(self, batch, chunk_tiles: int):
+        import numpy as np
+        import torch
+
+        import ekv_hip
+        import workloads
+        from runtime.audit_kernel import RecordingPlane
+
+        self.ekv = ekv_hip
+        self.batch = batch
+        self.chunk = chunk_tiles
+        dev = "cuda"
+        self.pools = [workloads.device_pool(batch, torch.bfloat16, seed=batch.seed + 101 * p) for p in range(POOLS)]
+        self.keys = [pool[:, 0] for pool in self.pools]
+        qs = workloads.queries(batch, LAYERS)
+        self.q = [torch.from_numpy(qs[layer]).to(torch.bfloat16).to(dev) for layer in range(LAYERS)]
+        self.table = torch.from_numpy(batch.table).to(dev)
+        self.lens = torch.from_numpy(batch.lens).to(dev)
+        self.blocks = torch.from_numpy(batch.blocks.astype(np.int32)).to(dev)
+        self.plane = RecordingPlane(LAYERS, batch.rows, batch.width, batch.group_rows, batch.block_size)
+        self.plane._copy_to_device(self.plane._flag_dev, np.array([1], dtype=np.uint32))
+        self.plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
+        R, W = batch.rows, batch.width
+        self.shares = torch.empty(R, W, dtype=torch.float32, device=dev)
+        self.keep = torch.empty(R, W, dtype=torch.uint8, device=dev)
+        self.summary = torch.zeros(6, dtype=torch.int64, device=dev)
+        self.view = torch.zeros(R, W, dtype=torch.int32, device=dev)
+        self.view_lens = torch.zeros(R, dtype=torch.int32, device=dev)
+        self.counts = torch.zeros(5, dtype=torch.int64, device=dev)
+        self.scale = batch.head_dim ** -0.5
+
+    def audit(self, layer: int, stream: int) -> None:
+        b, p = self.batch, self.plane
+        plane_stride, layer_stride, row_stride = p.strides
+        q, keys = self.q[layer], self.keys[layer % POOLS]
+        self.ekv.call(
+            "ekv_audit_tile_lse",
+            q.data_ptr(), self.ekv.BF16, q.stride(0), q.stride(1),
+            keys.data_ptr(), self.ekv.BF16, keys.stride(0), keys.stride(1), keys.stride(2), 1.0,
+            self.table.data_ptr(), self.table.stride(0), self.lens.data_ptr(), p._token.data_ptr(),
+            p._select.data_ptr(), p._flag_dev,
+            p.lse_address, plane_stride, layer_stride, row_stride, p.cells, 0, 0,
+            self.scale, layer, layer % b.kv_heads, 1, b.group_rows,
+            b.rows, b.width, b.block_size, 2, b.head_dim, self.chunk, stream,
+        )
+
+    def shares_rank_view(self, stream: int) -> None:
+        b, p = self.batch, self.plane
+        plane_stride, layer_stride, row_stride = p.strides
+        self.ekv.call(
+            "ekv_tile_shares", p.lse_address, plane_stride, layer_stride, row_stride, LAYERS, p.cells, b.width,
+            0, self.blocks.data_ptr(), b.rows, 2, self.ekv.AGG_MEAN, self.shares.data_ptr(), b.width, stream,
+        )
+        self.rank_view(stream)
+
+    def rank_view(self, stream: int) -> None:
+        b = self.batch
+        self.ekv.call(
+            "ekv_rank_uniform", self.shares.data_ptr(), b.width, self.blocks.data_ptr(), 0, 0, 0, 0, RECENT, 0, 0,
+            b.rows, b.width, FRACTION, -1, self.keep.data_ptr(), b.width, self.summary.data_ptr(), stream,
+        )
+        self.ekv.call(
+            "ekv_build_view", self.table.data_ptr(), b.width, self.lens.data_ptr(), self.keep.data_ptr(), b.width,
+            0, 0, 0, 0, 1, b.rows, b.width, b.block_size, self.view.data_ptr(), b.width, self.view_lens.data_ptr(),
+            self.counts.data_ptr(), stream,
+        )
+
+    def run(self, stream: int) -> None:
+        for layer in range(LAYERS):
+            self.audit(layer, stream)
+        self.shares_rank_view(stream)
+
+
+def time_events(fn, repeats: int, stream) -> list[float]:
+    """Durations (ms) of ``fn`` bracketed by events on ``stream``."""
+    import torch
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    for i in range(repeats):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def copy_peak_gbs() -> float:
+    """Bandwidth of a plain device copy of 4 GB (read + write bytes / time): the measured peak."""
+    import torch
+
+    n = 1 << 29  # 4 GiB of float64... per buffer 4 GiB
+    src = torch.empty(n, dtype=torch.float64, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    stream = torch.cuda.current_stream()
+    ms = sorted(time_events(lambda: dst.copy_(src), 10, stream))[5]
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * n * 8 / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(step: Step, bound_s: float) -> dict:
+    """The oracle's PyTorch-CPU audit on a bounded sample of the step's layers (all 128 rows each)."""
+    import numpy as np
+    import torch
+
+    from oracle import audit as oracle_audit
+    import workloads
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    b = step.batch
+    planes = oracle_audit.new_planes(LAYERS, b.rows, b.width, b.group_rows)
+    done, busy = 0, 0.0
+    host = {}
+    for layer in range(LAYERS):
+        pool, group = layer % POOLS, layer % b.kv_heads
+        if (pool, group) not in host:
+            keys, table = workloads.host_keys(b, step.pools[pool], heads=[group])
+            host[(pool, group)] = (torch.from_numpy(keys).to(torch.bfloat16), table)
+        keys, table = host[(pool, group)]
+        q = step.q[layer].cpu()
+        t0 = time.perf_counter()
+        oracle_audit.tile_lse_torch(planes, q, keys, table, b.lens, np.arange(b.rows), np.ones(b.rows), layer,
+                                    step.scale, b.block_size, b.group_rows, group, key_head=0)
+        busy += time.perf_counter() - t0
+        done += 1
+        if busy >= bound_s:
+            break
+    # the sample's records agree with the device's (same layers)
+    got = step.plane.read_planes()[:, :done]
+    live = ~np.isnan(planes[0, :done])
+    err = float(np.abs(got[0][live] - planes[0, :done][live]).max())
+    return {
+        "value": round(done * audit_bytes(b) / busy / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"audit of {done} of the 32 layers (all 128 rows, one KV group each) with oracle.audit.tile_lse_torch, "
+                  f"{busy:.1f} s; tile max agrees with the GPU to {err:.1e}",
+    }
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import workloads
+
+    torch.cuda.set_device(0)
+    batch = workloads.config2_batch()
+    step = Step(batch, args.chunk_tiles)
+    stream = torch.cuda.current_stream()
+    handle = int(stream.cuda_stream)
+
+    # eager reference of one step, then the captured graph; every replay must reproduce it
+    step.run(handle)
+    torch.cuda.synchronize()
+    eager = (step.shares.clone(), step.keep.clone(), step.view.clone(), step.view_lens.clone())
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step.run(int(side.cuda_stream))
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.run(int(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        now = (step.shares, step.keep, step.view, step.view_lens)
+        for a, b in zip(eager, now):
+            if not torch.equal(a, b) and not (a.is_floating_point() and torch.equal(torch.nan_to_num(a), torch.nan_to_num(b))):
+                raise RuntimeError("a graph replay differs from the eager step")
+
+    if args.profile_only:
+        # a plain copy of known size first, to scale the memory counters of the kernels that follow
+        calib_bytes = 256 << 20
+        src = torch.ones(calib_bytes // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        for _ in range(args.warmup + args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_only": True, "steps": args.steps, "calibration_copy_bytes": calib_bytes}))
+        return
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    # mean duration of an audit launch: a graph of the 32 launches of a step, replayed and timed
+    # with events on the stream it runs on, divided by the launches
+    audit_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(audit_graph):
+        capture = int(torch.cuda.current_stream().cuda_stream)
+        for layer in range(LAYERS):
+            step.audit(layer, capture)
+    for _ in range(3):
+        audit_graph.replay()
+    torch.cuda.synchronize()
+    reps = max(10, args.steps // 2)
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(reps):
+        audit_graph.replay()
+    a1.record(stream)
+    torch.cuda.synchronize()
+    audit_ms = a0.elapsed_time(a1) / (reps * LAYERS)
+    # the other stages of the step
+    shares_ms = float(np.median(time_events(lambda: step.ekv.call(
+        "ekv_tile_shares", step.plane.lse_address, *step.plane.strides, LAYERS, step.plane.cells, batch.width, 0,
+        step.blocks.data_ptr(), batch.rows, 2, step.ekv.AGG_MEAN, step.shares.data_ptr(), batch.width, handle),
+        20, stream)))
+    view_ms = float(np.median(time_events(lambda: step.rank_view(handle), 20, stream)))
+
+    b_launch = audit_bytes(batch)
+    achieved = b_launch / (audit_ms * 1e-3) / 1e9
+    value = LAYERS * b_launch / (ms_per_step * 1e-3) / 1e9
+
+    # the every-KV-head audit (1.14 GB of keys per launch): same kernel, all 8 groups per launch
+    from runtime.audit_kernel import RecordingPlane
+
+    all_plane = RecordingPlane(1, batch.rows, batch.width, batch.group_rows, batch.block_size, kv_heads=batch.kv_heads)
+    all_plane._copy_to_device(all_plane._flag_dev, np.array([1], dtype=np.uint32))
+    all_plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
+    all_ms = float(np.median(time_events(
+        lambda: all_plane.launch(0, step.table, step.lens, step.q[0], step.keys[0], step.scale,
+                                 chunk_tiles=args.chunk_tiles), 10, stream)))
+    all_gbs = audit_bytes(batch, batch.kv_heads) / (all_ms * 1e-3) / 1e9
+
+    # the view-build configuration: ranking + compaction of 1024 rows x up to 8192 blocks
+    c4 = workloads.config4()
+    s4 = torch.from_numpy(c4["shares"]).cuda()
+    n4 = torch.from_numpy(c4["blocks"]).cuda()
+    t4 = torch.from_numpy(c4["table"]).cuda()
+    l4 = torch.from_numpy(c4["seq_lens"]).cuda()
+    k4 = torch.empty_like(s4, dtype=torch.uint8)
+    v4 = torch.empty_like(t4)
+    vl4 = torch.empty_like(l4)
+    sm4 = torch.zeros(6, dtype=torch.int64, device="cuda")
+
+    def view_build_c4():
+        step.ekv.call("ekv_rank_uniform", s4.data_ptr(), 8192, n4.data_ptr(), 0, 0, 0, 0, 0, 0, 0, 1024, 8192, 0.5,
+                      -1, k4.data_ptr(), 8192, sm4.data_ptr(), handle)
+        step.ekv.call("ekv_compact_view", t4.data_ptr(), 8192, l4.data_ptr(), k4.data_ptr(), 8192, 1024, 8192, 16,
+                      v4.data_ptr(), 8192, vl4.data_ptr(), handle)
+
+    view_build_c4()
+    c4_ms = float(np.median(time_events(view_build_c4, 20, stream)))
+
+    peak = copy_peak_gbs()
+    out = {
+        "metric": "audit KV GB/s (% HBM peak) at Llama-3-8B decode shape; view build us",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,1) bf16 keys and queries, seeded tables and lengths",
+        "config": {
+            "workload": "Llama-3-8B decode audit step: 128 rows, L~U[512,8192], 32q/8kv heads, d=128, bf16, "
+                        "block 16, 32 layers (one KV group each, 4 rotating 100k-block pools), shares + uniform "
+                        "ranking at 0.5 + view build, HIP-graph replay",
+            "rows": batch.rows,
+            "layers": LAYERS,
+            "audited_tokens": int(batch.lens.sum()),
+            "audit_bytes_per_launch": b_launch,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "ekv_audit_tile_lse (one KV group)",
+            "mean_launch_us": round(audit_ms * 1e3, 2),
+            "measured_copy_peak_gbs": round(peak, 1),
+            "frac_of_measured_peak": round(achieved / peak, 4),
+        },
+        "stages_us": {
+            "audit_per_layer": round(audit_ms * 1e3, 2),
+            "shares_32_layers": round(shares_ms * 1e3, 2),
+            "rank_and_view": round(view_ms * 1e3, 2),
+        },
+        "every_kv_head_audit": {"bytes_per_launch": audit_bytes(batch, batch.kv_heads), "us": round(all_ms * 1e3, 2),
+                                "gbs": round(all_gbs, 1), "frac": round(all_gbs / HBM_PEAK_GBS, 4)},
+        "view_build_us": {"llama3_step_128_rows": round(view_ms * 1e3, 2),
+                          "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2)},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -87,3 +87,37 @@ def true_block_shares(q: np.ndarray, k: np.ndarray, scale: float, block_size: in
     p = p.mean(axis=0)
     n_blocks = -(-len(p) // block_size)
     return np.pad(p, (0, n_blocks * block_size - len(p))).reshape(n_blocks, block_size).sum(axis=1)
+
+
+def tile_lse_torch(planes, q, keys, table, lens, qrow, select, layer, scale, block_size, group_rows, group,
+                   key_head=None, tile_blocks=2):
+    """The same statistic with PyTorch on the host CPU, float32 as the reference's kernel accumulates,
+    for the CPU baseline: ``keys`` a CPU tensor ``[blocks, block_size, heads, dim]`` (any float dtype),
+    ``q`` a CPU tensor ``[tokens, q_heads, dim]``; one KV group; ``planes`` a NumPy block as above."""
+    import torch
+
+    kh = group if key_head is None else key_head
+    width = planes.shape[3]
+    tile_tokens = tile_blocks * block_size
+    flat = keys[:, :, kh, :].reshape(-1, keys.shape[-1])  # [blocks * block_size, dim]
+    for r in range(planes.shape[2]):
+        if select[r] == 0:
+            continue
+        length = int(min(max(int(lens[r]), 0), width * block_size))
+        if length == 0:
+            continue
+        n_blocks = -(-length // block_size)
+        pos = torch.arange(length)
+        rows_of = torch.from_numpy(table[r, :n_blocks].astype("int64"))[pos // block_size] * block_size + pos % block_size
+        k = flat.index_select(0, rows_of).float()
+        qg = q[int(qrow[r]), group * group_rows : (group + 1) * group_rows].float()
+        s = (qg @ k.T) * scale
+        n_tiles = -(-length // tile_tokens)
+        padded = torch.full((group_rows, n_tiles * tile_tokens), float("-inf"))
+        padded[:, :length] = s
+        t = padded.view(group_rows, n_tiles, tile_tokens)
+        m = t.amax(dim=2)
+        total = torch.exp(t - m[:, :, None]).sum(dim=2)
+        tile_of_block = torch.arange(n_blocks) // tile_blocks
+        planes[0, layer, r, :n_blocks, :group_rows] = m[:, tile_of_block].T.numpy()
+        planes[1, layer, r, :n_blocks, :group_rows] = total[:, tile_of_block].T.numpy()

@@ -4,16 +4,18 @@
 // RecordingPlane.launch, runtime/audit_kernel.py:224-265.
 //
 // Design (gfx950, wave64):
-//  * Work list.  A unit is (row, run of `chunk_tiles` tiles, audited KV head).  Every workgroup
-//    builds the per-row unit offsets in LDS from lens/select (a block scan over the rows), so
-//    the launch needs no host-side knowledge of the lengths, no scratch memory and no second
-//    kernel; it is identical on every step and can be captured in a graph.  Waves walk the
-//    units grid-stride, so only live tiles are visited (the reference's grid is rows x width
-//    tiles with early exits).
+//  * Work list.  The live tiles of the selected rows, times the audited KV heads, form one
+//    flat list; wave w of the grid takes the w-th equal contiguous slice of it (split-K over
+//    the rows' tiles, crossing row boundaries), so every wave does the same amount of work
+//    whatever the length mix.  Every workgroup builds the per-row tile offsets in LDS from
+//    lens/select with a block scan, so the launch needs no host-side knowledge of the lengths,
+//    no scratch memory and no second kernel; it is identical on every step and can be captured
+//    in a graph.  The grid is the number of workgroups the GPU holds at once.
 //  * Loads.  One token's key row of one head is `row_bytes` contiguous bytes; LPT lanes load
 //    it with 16-byte loads, TPI = 64 / LPT tokens per wave instruction.  A chunk is NL such
 //    instructions; chunks are double-buffered so one chunk's loads are in flight while the
-//    previous one is reduced.
+//    previous one is reduced (the prefetch is unconditional inside the loop so that the
+//    compiler's wait counts let it stay in flight).
 //  * Dots.  Each lane multiplies its 16-byte slice with the matching slice of the (padded)
 //    query group kept in registers (v_dot2 for 16-bit / fp8->bf16 keys, FMA for fp32), then a
 //    transpose reduction over the LPT lanes of a token leaves VF complete scores per lane,
@@ -21,6 +23,8 @@
 //  * Timer.  With a cycles buffer each unit adds its s_memtime duration to cycles[row] with a
 //    vector 64-bit atomic (the pass's per-row timer, mlir_pass/lib/eKVTimer.cpp:1348-1387).
 #include <math.h>
+
+#include <mutex>
 
 #include "ekv_common.hpp"
 
@@ -31,7 +35,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kTileBlocks = 2;  // TILE_BLOCKS, runtime/audit_kernel.py:31
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxRows = 16000;  // LDS holds one int per row (64 KB per workgroup)
+constexpr int kMaxRows = 6000;  // LDS holds two ints per row and 16 KB of staged records
 
 enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
 
@@ -56,7 +60,7 @@ struct Params {
   uint64_t *cycles;
   int32_t cycles_rows;
   float scale;  // scale * k_scale
-  int32_t group_first, groups, group_rows, rows, width, block_size, chunk_tiles, nsub;
+  int32_t group_first, groups, group_rows, rows, width, block_size, chunk_tiles, nsub, nsub_log2;
 };
 
 template <int MODE, int HEAD_DIM, int NL, int GP>
@@ -175,27 +179,25 @@ __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
   const int rows = p.rows;
   const int bs = p.block_size;
   const int tile_tokens = kTileBlocks * bs;
-  const int chunk = p.chunk_tiles;
 
-  // ---- per-row unit counts and their exclusive scan (every workgroup) -------------------
+  // ---- per-row live tile counts and their exclusive scan (every workgroup) -------------
   const int per = (rows + kThreads - 1) / kThreads;
   const int r0 = threadIdx.x * per;
   const int r1 = min(r0 + per, rows);
-  auto units_of = [&](int r) -> int {
+  auto tiles_of = [&](int r) -> int {
     if (p.select[r] == 0) return 0;  // runtime/audit_kernel.py:65
     const int len = min(max(p.lens[r], 0), p.width * bs);
-    const int tiles = (len + tile_tokens - 1) / tile_tokens;
-    return (tiles + chunk - 1) / chunk;
+    return (len + tile_tokens - 1) / tile_tokens;
   };
   int local = 0;
-  for (int r = r0; r < r1; ++r) local += units_of(r);
-  int total_units = 0;
-  int base = block_exclusive_scan<kThreads>(local, s_scan, total_units);
+  for (int r = r0; r < r1; ++r) local += tiles_of(r);
+  int total_tiles = 0;
+  int base = block_exclusive_scan<kThreads>(local, s_scan, total_tiles);
   for (int r = r0; r < r1; ++r) {
     s_off[r] = base;
-    base += units_of(r);
+    base += tiles_of(r);
   }
-  if (threadIdx.x == 0) s_off[rows] = total_units;
+  if (threadIdx.x == 0) s_off[rows] = total_tiles;
   __syncthreads();
 
   const int lane = lane_id();
@@ -204,28 +206,31 @@ __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
   const int nwaves = gridDim.x * kWaves;
   const int nsub = p.nsub;
   const int G = p.group_rows;
-  const int all_units = total_units * p.groups;
-
-  // the wave index is uniform across the wave; say so, so that the unit, row and chunk
+  // the wave index is uniform across the wave; say so, so that the slice, row and tile
   // arithmetic and the block-table reads stay scalar
   const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
-  for (int u = wave_id; u < all_units; u += nwaves) {
-    const int h = u % p.groups;
-    const int bu = u / p.groups;
-    int lo = 0, hi = rows;  // largest row with s_off[row] <= bu
+  const long long all = (long long)total_tiles * p.groups;
+  long long u = all * wave_id / nwaves;
+  const long long u_end = all * (wave_id + 1) / nwaves;
+
+  while (u < u_end) {
+    const int h = (int)(u / total_tiles);
+    const int t = (int)(u - (long long)h * total_tiles);
+    int lo = 0, hi = rows;  // the row holding flat tile t: largest row with s_off[row] <= t
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= bu) lo = mid; else hi = mid;
+      if (s_off[mid] <= t) lo = mid; else hi = mid;
     }
     const int row = lo;
-    const int unit_in_row = bu - s_off[row];
+    const long long seg_end = min(u_end, (long long)(h + 1) * total_tiles);  // this head's part
+    const int t_stop = (int)min((long long)s_off[row + 1], seg_end - (long long)h * total_tiles);
+    const int tile_begin = t - s_off[row];
+    const int tile_end = t_stop - s_off[row];
+    u += t_stop - t;
     const uint64_t t_start = __builtin_amdgcn_s_memtime();
 
     const int len = min(max(p.lens[row], 0), p.width * bs);
     const int nblocks = (len + bs - 1) / bs;
-    const int tiles = (len + tile_tokens - 1) / tile_tokens;
-    const int tile_begin = unit_in_row * chunk;
-    const int tile_end = min(tile_begin + chunk, tiles);
     const int g = p.group_first + h;  // KV head
     const int32_t *trow = p.table + (int64_t)row * p.table_stride;
 
@@ -255,15 +260,18 @@ __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
 #pragma unroll
     for (int e = 0; e < HPL; ++e) { m_run[e] = -INFINITY; l_run[e] = 0.0f; }
 
-    // Loads are not predicated: a token past the row's end still lies in a block the row owns
-    // (or in its first block when the tile's second block does not exist), so every address is
-    // inside the key cache; its score is masked to -inf in reduce_chunk.
+    // Block ids come from a register holding one id per lane for a window of 64 blocks (read
+    // with readlane), so the pipelined loop issues no table load whose wait would drain the key
+    // loads in flight.  Loads are not predicated: a token past the row's end still lies in a
+    // block the row owns (or in its first block when the tile's second block does not exist),
+    // so every address is inside the key cache; its score is masked to -inf in reduce_chunk.
+    int ids = 0, ids_base = 0;
     auto load_chunk = [&](u32x4 (&D)[NL], int z) {
       const int tile = z / nsub;
       const int c = z - tile * nsub;
       const int b0 = tile * kTileBlocks;
-      const int id0 = trow[b0];
-      const int id1 = (b0 + 1 < nblocks) ? trow[b0 + 1] : id0;
+      const int id0 = __builtin_amdgcn_readlane(ids, b0 - ids_base);
+      const int id1 = (b0 + 1 < nblocks) ? __builtin_amdgcn_readlane(ids, b0 + 1 - ids_base) : id0;
       const char *base0 = p.keys + (int64_t)id0 * p.k_stride_block + lane_off;
       const char *base1 = p.keys + (int64_t)id1 * p.k_stride_block + lane_off;
 #pragma unroll
@@ -341,17 +349,316 @@ __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
       }
     };
 
-    const int z_end = tile_end * nsub;
-    int z = tile_begin * nsub;
-    u32x4 A[NL], B[NL];
-    load_chunk(A, z);
-    while (true) {
-      if (z + 1 < z_end) load_chunk(B, z + 1);
-      reduce_chunk(A, z);
-      if (++z >= z_end) break;
-      if (z + 1 < z_end) load_chunk(A, z + 1);
-      reduce_chunk(B, z);
-      if (++z >= z_end) break;
+    // Windows of 32 tiles (the 64 block ids one register holds); inside a window two chunks are
+    // in flight: the loop always prefetches and the tail drains.
+    constexpr int kWindowTiles = kWave / kTileBlocks;
+    for (int w0 = tile_begin; w0 < tile_end; w0 += kWindowTiles) {
+      const int w1 = min(w0 + kWindowTiles, tile_end);
+      ids_base = w0 * kTileBlocks;
+      ids = ids_base + lane < nblocks ? trow[ids_base + lane] : 0;
+      const int z_end = w1 * nsub;
+      int z = w0 * nsub;
+      u32x4 A[NL], B[NL];
+      load_chunk(A, z);
+      while (z + 2 < z_end) {
+        load_chunk(B, z + 1);
+        reduce_chunk(A, z);
+        load_chunk(A, z + 2);
+        reduce_chunk(B, z + 1);
+        z += 2;
+      }
+      if (z + 1 < z_end) {
+        load_chunk(B, z + 1);
+        reduce_chunk(A, z);
+        reduce_chunk(B, z + 1);
+      } else {
+        reduce_chunk(A, z);
+      }
+    }
+
+    if (p.cycles != nullptr && h == 0 && row < p.cycles_rows && lane == 0) {
+      const uint64_t t_end = __builtin_amdgcn_s_memtime();
+      atomicAdd((unsigned long long *)(p.cycles + row), (unsigned long long)(t_end - t_start));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// MFMA form for 16-bit keys (and fp8 keys widened to bf16): S^T = K * Q^T on
+// v_mfma_f32_16x16x32_{bf16,f16}.  A = keys (M = 16 tokens of one block, K = 32 dims),
+// B = the query group (N = 16 query rows, zero past group_rows), C = scores.  Lane l holds
+// A[token l % 16][dims of piece l / 16] and B[dims of piece l / 16][query row l % 16]; the 16-byte
+// dim pieces are permuted identically in A and B (piece 4s + l / 16 feeds k-step s), so each wave
+// load reads 64 contiguous bytes of each of 16 tokens.  C gives lane l the scores of tokens
+// 4 (l / 16) + i of query row l % 16, so a query row's max / sum over a 32-token chunk is a local
+// reduction of 8 values and two butterfly steps.
+// ---------------------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int MODE, int HEAD_DIM>
+struct MfmaShape {
+  static constexpr bool kFp8 = MODE == kModeFp8Bf16;
+  static constexpr int kKBytes = kFp8 ? 1 : 2;
+  static constexpr int kSteps = HEAD_DIM / 32;                   // k-steps of 32 dims
+  static constexpr int kLoads = kFp8 ? kSteps / 2 : kSteps;      // 16-byte key loads per M-tile
+  static constexpr int kChunk = 32;                              // tokens per chunk: two M-tiles
+};
+
+template <int MODE>
+__device__ __forceinline__ f32x4_t mfma_step(const u32x4 a, const u32x4 b, f32x4_t c) {
+  if constexpr (MODE == kModeF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// 16 fp8 values (one 16-byte load) -> two bf16x8 operands (dims 0..7 and 8..15 of the piece)
+__device__ __forceinline__ void widen_fp8(const u32x4 k, u32x4 &lo, u32x4 &hi) {
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w[2 * e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)k[e], 1.0f, false));
+    w[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)k[e], 1.0f, true));
+  }
+  lo = (u32x4){w[0], w[1], w[2], w[3]};
+  hi = (u32x4){w[4], w[5], w[6], w[7]};
+}
+
+// NT loads the keys with the nontemporal hint (they are read once).
+//
+// Per wave, two chunks are in flight.  A chunk's reduction is split: the MFMAs are the only
+// readers of the load buffer, so the next chunk's loads are issued right after them and the
+// softmax part overlaps with them.  The per-tile records are staged in LDS and written once per
+// window with coalesced stores, so no conditional global store sits between a load and its wait.
+constexpr int kMaxGroupRows = 16;
+constexpr int kWindowTiles = kWave / kTileBlocks;  // tiles whose block ids one register holds
+constexpr int kStageFloats = kWindowTiles * 2 * kMaxGroupRows;  // per wave: [tile][plane][row]
+
+template <int MODE, int HEAD_DIM, bool NT>
+__global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p) {
+  using S = MfmaShape<MODE, HEAD_DIM>;
+  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = S::kChunk;
+
+  extern __shared__ int s_mem[];  // [rows + 1] tile offsets, [rows] clipped lengths
+  __shared__ int s_scan[kWaves];
+  __shared__ float s_stage[kWaves][kStageFloats];
+  int *s_off = s_mem;
+  int *s_len = s_mem + p.rows + 1;
+
+  if (*p.flag == 0u) return;  // the audit flag, runtime/audit_kernel.py:64
+
+  const int rows = p.rows;
+  const int bs = p.block_size;
+  const int tile_tokens = kTileBlocks * bs;
+
+  // ---- per-row live tiles: one read of select / lens, then a block scan ------------------
+  const int per = (rows + kThreads - 1) / kThreads;
+  const int r0 = threadIdx.x * per;
+  const int r1 = min(r0 + per, rows);
+  int local = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int len = min(max(p.lens[r], 0), p.width * bs);
+    const int tiles = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
+    s_len[r] = len;
+    s_off[r] = tiles;
+    local += tiles;
+  }
+  int total_tiles = 0;
+  int base = block_exclusive_scan<kThreads>(local, s_scan, total_tiles);
+  for (int r = r0; r < r1; ++r) {
+    const int tiles = s_off[r];
+    s_off[r] = base;
+    base += tiles;
+  }
+  if (threadIdx.x == 0) s_off[rows] = total_tiles;
+  __syncthreads();
+
+  const int lane = lane_id();
+  const int n = lane & 15;   // A: token of the M-tile; B / C: query row
+  const int c = lane >> 4;   // dim piece within a k-step; C: token quad
+  const int nwaves = gridDim.x * kWaves;
+  const int nsub = p.nsub;   // chunks per tile
+  const int G = p.group_rows;
+  float *stage = s_stage[threadIdx.x / kWave];
+  const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
+  const long long all = (long long)total_tiles * p.groups;
+  long long u = all * wave_id / nwaves;
+  const long long u_end = all * (wave_id + 1) / nwaves;
+
+  while (u < u_end) {
+    const int h = (int)(u / total_tiles);
+    const int t = (int)(u - (long long)h * total_tiles);
+    int lo = 0, hi = rows;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int row = lo;
+    const long long seg_end = min(u_end, (long long)(h + 1) * total_tiles);
+    const int t_stop = (int)min((long long)s_off[row + 1], seg_end - (long long)h * total_tiles);
+    const int tile_begin = t - s_off[row];
+    const int tile_end = t_stop - s_off[row];
+    u += t_stop - t;
+    const uint64_t t_start = __builtin_amdgcn_s_memtime();
+
+    const int len = s_len[row];
+    const int nblocks = (len + bs - 1) / bs;
+    const int g = p.group_first + h;  // KV head
+    const int32_t *trow = p.table + (int64_t)row * p.table_stride;
+
+    // B operand: query row n of the group, the dims k-step s reads (zero past group_rows)
+    u32x4 qb[KS];
+    {
+      const char *qrow = p.q + (int64_t)p.qrow[row] * p.q_stride_token + (int64_t)(g * G + n) * p.q_stride_head;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        // 16-bit keys: piece 4s + c (8 dims); fp8 keys: 16-dim piece 4(s/2) + c, half s % 2
+        const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
+        qb[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+    const int64_t lane_off = (int64_t)n * p.k_stride_pos + (int64_t)g * p.k_stride_head + c * 16;
+    float *cell_row = p.lse + (int64_t)row * p.row_stride + h * G;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    int ids = 0, ids_base = 0, w0 = 0;
+    // chunk z: tokens 32 (z % nsub) .. + 32 of tile z / nsub, two M-tiles of 16 tokens; an M-tile lies in
+    // one block (16 divides the block size), whose id comes from the window register
+    auto load_chunk = [&](u32x4 (&D)[2 * NLD], int z) {
+      const int tile = z >> p.nsub_log2;
+      const int off = (z & (nsub - 1)) * CH;  // token offset in the tile
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int tpos = off + 16 * mt;
+        const int b = tile * kTileBlocks + tpos / bs;
+        // past the row the tile's first block stands in (in the cache; the scores are masked)
+        const int id = __builtin_amdgcn_readlane(ids, (b < nblocks ? b : tile * kTileBlocks) - ids_base);
+        const char *src = p.keys + (int64_t)id * p.k_stride_block + lane_off + (int64_t)(tpos % bs) * p.k_stride_pos;
+#pragma unroll
+        for (int s = 0; s < NLD; ++s) {
+          const u32x4 *at = (const u32x4 *)(src + 64 * s);
+          D[mt * NLD + s] = NT ? __builtin_nontemporal_load(at) : *at;
+        }
+      }
+    };
+
+    // the MFMAs of a chunk: scores of tokens 16 mt + 4 c + i for query row n in sc[4 mt + i]
+    auto mma_chunk = [&](const u32x4 (&D)[2 * NLD], f32x4_t (&acc)[2]) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (S::kFp8) {
+#pragma unroll
+          for (int s = 0; s < NLD; ++s) {
+            u32x4 lo4, hi4;
+            widen_fp8(D[mt * NLD + s], lo4, hi4);
+            acc[mt] = mfma_step<kModeBF16>(lo4, qb[2 * s], acc[mt]);
+            acc[mt] = mfma_step<kModeBF16>(hi4, qb[2 * s + 1], acc[mt]);
+          }
+        } else {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[mt * NLD + s], qb[s], acc[mt]);
+        }
+      }
+    };
+
+    auto softmax_chunk = [&](const f32x4_t (&acc)[2], int z) {
+      const int tile = z >> p.nsub_log2;
+      const int sub = z & (nsub - 1);
+      const int tok0 = tile * tile_tokens + sub * CH;
+      float sc[8];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = tok0 + 16 * mt + 4 * c + i;
+          sc[4 * mt + i] = tok < len ? acc[mt][i] * p.scale : -INFINITY;
+        }
+      float mx = sc[0];
+#pragma unroll
+      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, sc[k]);
+      mx = fmaxf(mx, shfl_xor(mx, 16));
+      mx = fmaxf(mx, shfl_xor(mx, 32));
+      // exponents are <= 0 (a score minus a max); v_exp_f32 gives 0 for -inf and for underflow
+      float sum = 0.0f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sum += __builtin_amdgcn_exp2f((sc[k] - mx) * kLog2e);
+      }
+      sum += shfl_xor(sum, 16);
+      sum += shfl_xor(sum, 32);
+      const float M = fmaxf(m_run, mx);
+      if (M != -INFINITY) {
+        const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f((m_run - M) * kLog2e);
+        const float bb = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f((mx - M) * kLog2e);
+        l_run = a + bb;
+        m_run = M;
+      }
+      if (sub == nsub - 1) {  // the tile is complete: stage its record
+        if (c == 0) {
+          stage[((tile - w0) * 2 + 0) * kMaxGroupRows + n] = m_run;
+          stage[((tile - w0) * 2 + 1) * kMaxGroupRows + n] = l_run;
+        }
+        m_run = -INFINITY;
+        l_run = 0.0f;
+      }
+    };
+
+    for (w0 = tile_begin; w0 < tile_end; w0 += kWindowTiles) {
+      const int w1 = min(w0 + kWindowTiles, tile_end);
+      ids_base = w0 * kTileBlocks;
+      ids = ids_base + lane < nblocks ? trow[ids_base + lane] : 0;
+      const int z_end = w1 * nsub;
+      int z = w0 * nsub;
+      u32x4 A[2 * NLD], B[2 * NLD];
+      f32x4_t acc[2];
+      if (z + 1 == z_end) {
+        load_chunk(A, z);
+        mma_chunk(A, acc);
+        softmax_chunk(acc, z);
+      } else {
+        load_chunk(A, z);
+        load_chunk(B, z + 1);
+        while (z + 3 < z_end) {  // steady state: every load unconditional
+          mma_chunk(A, acc);
+          load_chunk(A, z + 2);
+          softmax_chunk(acc, z);
+          mma_chunk(B, acc);
+          load_chunk(B, z + 3);
+          softmax_chunk(acc, z + 1);
+          z += 2;
+        }
+        if (z + 2 < z_end) {
+          mma_chunk(A, acc);
+          load_chunk(A, z + 2);
+          softmax_chunk(acc, z);
+          mma_chunk(B, acc);
+          softmax_chunk(acc, z + 1);
+          mma_chunk(A, acc);
+          softmax_chunk(acc, z + 2);
+        } else {
+          mma_chunk(A, acc);
+          softmax_chunk(acc, z);
+          mma_chunk(B, acc);
+          softmax_chunk(acc, z + 1);
+        }
+      }
+      // the window's records into every block of its tiles that the row reaches,
+      // runtime/audit_kernel.py:97-109 (a wave reads only what it staged itself)
+      __builtin_amdgcn_wave_barrier();
+      const int b0 = w0 * kTileBlocks;
+      const int nb = min(w1 * kTileBlocks, nblocks) - b0;
+      for (int e = lane; e < nb * G; e += kWave) {
+        const int b = e / G, q = e - b * G;
+        float *cell = cell_row + (int64_t)(b0 + b) * p.cells + q;
+        cell[0] = stage[((b >> 1) * 2 + 0) * kMaxGroupRows + q];
+        cell[p.plane_stride] = stage[((b >> 1) * 2 + 1) * kMaxGroupRows + q];
+      }
+      __builtin_amdgcn_wave_barrier();
     }
 
     if (p.cycles != nullptr && h == 0 && row < p.cycles_rows && lane == 0) {
@@ -397,6 +704,27 @@ KernelFn pick_hd(int hd, int nl, int gp) {
   return nullptr;
 }
 
+constexpr bool kMfmaNontemporal = true;
+
+template <int MODE>
+KernelFn pick_mfma_hd(int hd) {
+  switch (hd) {
+    case 64: return tile_lse_mfma_kernel<MODE, 64, kMfmaNontemporal>;
+    case 128: return tile_lse_mfma_kernel<MODE, 128, kMfmaNontemporal>;
+    case 256: return tile_lse_mfma_kernel<MODE, 256, kMfmaNontemporal>;
+  }
+  return nullptr;
+}
+
+KernelFn pick_mfma(int mode, int hd) {
+  switch (mode) {
+    case kModeF16: return pick_mfma_hd<kModeF16>(hd);
+    case kModeBF16: return pick_mfma_hd<kModeBF16>(hd);
+    case kModeFp8Bf16: return pick_mfma_hd<kModeFp8Bf16>(hd);
+  }
+  return nullptr;
+}
+
 KernelFn pick(int mode, int hd, int nl, int gp) {
   switch (mode) {
     case kModeF32: return pick_hd<kModeF32>(hd, nl, gp);
@@ -405,6 +733,28 @@ KernelFn pick(int mode, int hd, int nl, int gp) {
     case kModeFp8Bf16: return pick_hd<kModeFp8Bf16>(hd, nl, gp);
   }
   return nullptr;
+}
+
+// Workgroups of `fn` one compute unit holds at once with `lds` bytes of dynamic LDS (cached).
+int resident_blocks(KernelFn fn, size_t lds) {
+  struct Entry {
+    KernelFn fn;
+    size_t lds;
+    int blocks;
+  };
+  static Entry cache[64];
+  static int used = 0;
+  static std::mutex lock;
+  std::lock_guard<std::mutex> guard(lock);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == fn && cache[i].lds == lds) return cache[i].blocks;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), kThreads, lds) !=
+          hipSuccess ||
+      n < 1)
+    n = 2;
+  if (used < 64) cache[used++] = Entry{fn, lds, n};
+  return n;
 }
 
 int dtype_bytes(int dtype) {
@@ -466,17 +816,29 @@ extern "C" int ekv_audit_tile_lse(
   const int lpt = row_bytes / 16;
   const int tpi = kWave / lpt;
   const int tile_tokens = kTileBlocks * block_size;
-  // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
-  // instruction must sit inside one block, and a chunk inside one tile.
-  if (block_size % tpi != 0)
-    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: block size %d is below the %d tokens of one load",
-                block_size, tpi);
-  const int nl = tile_tokens / tpi >= 8 ? 8 : tile_tokens / tpi;
-  const int gp = group_rows <= 4 ? 4 : (group_rows <= 8 ? 8 : 16);
-  KernelFn fn = pick(mode, head_dim, nl, gp);
+  // 16-bit and fp8 keys use the MFMA form when a 32-token chunk fits the tile; otherwise (fp32
+  // keys, block size 8) the dot products run on the VALU.
+  const bool use_mfma = mode != kModeF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
+                        tile_tokens % 32 == 0;
+  KernelFn fn = nullptr;
+  int nsub = 1;
+  if (use_mfma) {
+    fn = pick_mfma(mode, head_dim);
+    nsub = tile_tokens / 32;
+  } else {
+    // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
+    // instruction must sit inside one block, and a chunk inside one tile.
+    if (block_size % tpi != 0)
+      return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: block size %d is below the %d tokens of one load",
+                  block_size, tpi);
+    const int nl = tile_tokens / tpi >= 8 ? 8 : tile_tokens / tpi;
+    const int gp = group_rows <= 4 ? 4 : (group_rows <= 8 ? 8 : 16);
+    fn = pick(mode, head_dim, nl, gp);
+    nsub = tile_tokens / (nl * tpi);
+  }
   if (fn == nullptr)
-    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, %d loads, group %d",
-                kv_dtype, head_dim, nl, gp);
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, block size %d",
+                kv_dtype, head_dim, block_size);
   // 16-byte loads of key rows and query slices
   const uint64_t kaddr = (uint64_t)keys | (uint64_t)(k_stride_block * kbytes) |
                          (uint64_t)(k_stride_pos * kbytes) | (uint64_t)(k_stride_head * kbytes);
@@ -511,16 +873,21 @@ extern "C" int ekv_audit_tile_lse(
   p.rows = rows;
   p.width = width;
   p.block_size = block_size;
-  p.chunk_tiles = chunk_tiles > 0 ? chunk_tiles : 4;
-  p.nsub = tile_tokens / (nl * tpi);
+  p.chunk_tiles = chunk_tiles > 0 ? chunk_tiles : 1;
+  p.nsub = nsub;
+  p.nsub_log2 = 0;
+  while ((1 << p.nsub_log2) < nsub) ++p.nsub_log2;
 
-  const int64_t max_tiles = (width + kTileBlocks - 1) / kTileBlocks;
-  const int64_t max_units = (int64_t)rows * ((max_tiles + p.chunk_tiles - 1) / p.chunk_tiles) * groups;
-  int64_t blocks = (max_units + kWaves - 1) / kWaves;
-  const int64_t cap = (int64_t)cu_count() * 4;
+  // One resident wave per slot the GPU has: the work list is split evenly over the grid, so a
+  // second round of workgroups would only add a tail.  chunk_tiles bounds the grid for small
+  // batches (at least that many tiles per wave).
+  const size_t lds = (size_t)(use_mfma ? 2 * rows + 1 : rows + 1) * sizeof(int);
+  const int64_t max_tiles = (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks) * groups;
+  const int64_t min_per_wave = p.chunk_tiles;
+  int64_t blocks = (max_tiles + min_per_wave * kWaves - 1) / (min_per_wave * kWaves);
+  const int64_t cap = (int64_t)cu_count() * resident_blocks(fn, lds);
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  const size_t lds = (size_t)(rows + 1) * sizeof(int);
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), lds, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_audit_tile_lse launch");
 }

@@ -6,12 +6,13 @@
 // renormalised per-block max).  The reference copies the planes to the host and does this in
 // float64 NumPy; here it runs in float32 on the planes where the audit kernel wrote them.
 //
-// One workgroup per output row.  Phase 1: wave w takes layers w, w + waves, ...; for each it
-// streams the row's [width][cells] records (coalesced: consecutive lanes read consecutive
-// cells) and keeps an online (max, sum of exp) per lane, which a butterfly over the lanes of
-// the same query row turns into the (layer, query row) peak and total, kept in LDS.  Phase 2:
-// each thread owns blocks and sums their shares over layers and query rows in a fixed order,
-// so the result is deterministic (no atomics).
+// One workgroup of 16 waves per output row.  Phase 1: wave w takes layers w, w + 16, ...; for
+// each it streams the row's [width][cells] records (coalesced: consecutive lanes read
+// consecutive cells, 8 elements' loads in flight per lane before any is used) and keeps an
+// online (max, sum of exp) per lane, which a butterfly over the lanes of the same query row
+// turns into the (layer, query row) peak and total, kept in LDS.  Phase 2: each thread owns
+// blocks and sums their shares over layers and query rows in a fixed order (8 records loaded
+// ahead), so the result is deterministic (no atomics).
 #include <math.h>
 
 #include "ekv_common.hpp"
@@ -19,7 +20,8 @@
 namespace ekv {
 namespace shares {
 
-constexpr int kThreads = 512;
+constexpr int kThreads = 1024;
+constexpr int kBatch = 8;  // loads in flight per lane
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
@@ -38,16 +40,11 @@ struct Params {
 
 __device__ __forceinline__ bool finite(float x) { return __builtin_isfinite(x); }
 
-// log weight of block b of one record, or NaN when the record carries none
-// (n is the row's length in blocks, which may exceed the width: the tail rule uses it unclipped)
-__device__ __forceinline__ float weight_log(const Params &p, const float *mrow, const float *lrow,
-                                           int64_t idx, int b, int n) {
-  float u;
-  if (p.from_u) {
-    u = mrow[idx];
-  } else {
-    u = mrow[idx] + __logf(lrow[idx]) - p.log_tile;
-  }
+// log weight of block b of one record (m and l as loaded, or u itself when from_u), NaN when the
+// record carries none.  n is the row's length in blocks, which may exceed the width: the tail
+// rule uses it unclipped.
+__device__ __forceinline__ float weight_of(const Params &p, float m, float l, int b, int n) {
+  float u = p.from_u ? m : m + __logf(l) - p.log_tile;
   // a partial last tile gives its weight back to the blocks that exist, tile_shares.py:84-87
   const int T = p.tile_blocks;
   const int tail_start = (n / T) * T;
@@ -93,15 +90,28 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
     const float *lrow = p.from_u ? nullptr : p.l + layer * p.layer_stride + (int64_t)src_row * p.row_stride;
     float mx = -INFINITY, sum = 0.0f;
     if (q < cells) {
-      for (int64_t e = lane; e < span; e += kWave) {
-        const int b = (int)(e / CP);
-        const float u = weight_log(p, mrow, lrow, (int64_t)b * cells + q, b, n_row);
-        if (finite(u)) {
-          if (u > mx) {
-            sum = sum * __expf(mx - u) + 1.0f;
-            mx = u;
-          } else {
-            sum += __expf(u - mx);
+      for (int64_t e0 = lane; e0 < span; e0 += (int64_t)kWave * kBatch) {
+        float mv[kBatch], lv[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int64_t e = e0 + (int64_t)k * kWave;
+          const int64_t idx = e < span ? (e / CP) * cells + q : 0;
+          mv[k] = mrow[idx];
+          lv[k] = p.from_u ? 0.0f : lrow[idx];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int64_t e = e0 + (int64_t)k * kWave;
+          if (e >= span) break;
+          const int b = (int)(e / CP);
+          const float u = weight_of(p, mv[k], lv[k], b, n_row);
+          if (finite(u)) {
+            if (u > mx) {
+              sum = sum * __expf(mx - u) + 1.0f;
+              mx = u;
+            } else {
+              sum += __expf(u - mx);
+            }
           }
         }
       }
@@ -132,16 +142,28 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   // ---- phase 2: per-block shares, summed (or maxed) in a fixed order -----------------------
   const bool use_max = p.aggregate == EKV_AGG_MAX;
   float local_total = 0.0f;
+  const int records = p.layers * cells;  // (layer, query row) pairs, in a fixed order
   for (int b = threadIdx.x; b < p.width; b += kThreads) {
     float acc = 0.0f;
     if (b < n) {
-      for (int layer = 0; layer < p.layers; ++layer) {
-        const float *mrow = p.m + layer * p.layer_stride + (int64_t)src_row * p.row_stride;
-        const float *lrow = p.from_u ? nullptr : p.l + layer * p.layer_stride + (int64_t)src_row * p.row_stride;
-        for (int c = 0; c < cells; ++c) {
+      for (int r0 = 0; r0 < records; r0 += kBatch) {
+        float mv[kBatch], lv[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int rec = r0 + k < records ? r0 + k : 0;
+          const int layer = rec / cells, c = rec - layer * cells;
+          const int64_t at = layer * p.layer_stride + (int64_t)src_row * p.row_stride + (int64_t)b * cells + c;
+          mv[k] = p.m[at];
+          lv[k] = p.from_u ? 0.0f : p.l[at];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int rec = r0 + k;
+          if (rec >= records) break;
+          const int layer = rec / cells, c = rec - layer * cells;
           const float pk = peak[layer * CP + c];
           if (!finite(pk)) continue;
-          const float u = weight_log(p, mrow, lrow, (int64_t)b * cells + c, b, n_row);
+          const float u = weight_of(p, mv[k], lv[k], b, n_row);
           const float share = finite(u) ? __expf(u - pk) * inv_total[layer * CP + c] : 0.0f;
           acc = use_max ? fmaxf(acc, share) : acc + share;
         }

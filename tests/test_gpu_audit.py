@@ -241,7 +241,9 @@ def test_records_give_the_true_share(kind):
 
 def test_timer_accumulates_per_row_cycles():
     # rows with planted work (lengths 512 * (r + 1)); the accumulator only grows, unselected rows stay 0,
-    # and the per-launch cycles of a row follow its work (tests/_row_cycles_check.py:61-69, 120-163)
+    # and the per-launch cycles of a row follow its work (tests/_row_cycles_check.py:61-69, 120-163).
+    # As the reference's check keeps one program per SM so that a duration is its own work and not
+    # co-residency, the launch asks for at least 16 tiles per wave (about one wave per compute unit).
     rows, bs, hkv, hq, d = 16, 16, 8, 32, 128
     lens = np.array([512 * (r + 1) for r in range(rows)], dtype=np.int32)
     n = (lens + bs - 1) // bs
@@ -264,7 +266,7 @@ def test_timer_accumulates_per_row_cycles():
     assert (prev == 0).all()
     deltas = []
     for _ in range(16):
-        record(plane, 0, table_t, lens_t, q, pool[:, 0], d**-0.5, select=select, chunk_tiles=1)
+        record(plane, 0, table_t, lens_t, q, pool[:, 0], d**-0.5, select=select, chunk_tiles=16)
         cur = plane.read_cycles()
         assert (cur >= prev).all(), "the accumulator decreased"
         deltas.append((cur - prev).astype(np.float64))

@@ -95,3 +95,20 @@ def test_all_heads_mode_stacks_the_groups():
     stacked = np.concatenate(one, axis=-1)
     assert np.array_equal(np.isnan(stacked), np.isnan(every))
     assert np.nanmax(np.abs(stacked - every)) == 0.0
+
+
+def test_torch_cpu_form_matches_the_numpy_oracle():
+    import torch
+
+    batch, kv, q = workloads.config1()
+    scale = batch.head_dim ** -0.5
+    a = audit.new_planes(1, batch.rows, batch.width, batch.group_rows)
+    b = audit.new_planes(1, batch.rows, batch.width, batch.group_rows)
+    audit.tile_lse(a, q, kv[:, 0], batch.table, batch.lens, np.arange(4), np.ones(4), 1, 0, scale, batch.block_size,
+                   batch.group_rows, [1])
+    audit.tile_lse_torch(b, torch.from_numpy(q), torch.from_numpy(kv[:, 0].copy()), batch.table, batch.lens,
+                         np.arange(4), np.ones(4), 0, scale, batch.block_size, batch.group_rows, 1)
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    live = ~np.isnan(a[0])
+    assert np.abs(a[0][live] - b[0][live]).max() < 1e-4
+    assert np.abs(np.log(a[1][live]) - np.log(b[1][live])).max() < 1e-4
