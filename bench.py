@@ -153,19 +153,34 @@ def time_events(fn, repeats: int, stream) -> list[float]:
 
 
 def copy_peak_gbs() -> float:
-    """Bandwidth of a plain device copy of 4 GB (read + write bytes / time): the measured peak."""
+    """Measured streaming peak: a 1 GiB -> 1 GiB float32 negation (the counter calibration
+    kernel), read + write bytes / median time."""
     import torch
 
-    n = 1 << 29  # 4 GiB of float64... per buffer 4 GiB
-    src = torch.empty(n, dtype=torch.float64, device="cuda").normal_()
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
-        dst.copy_(src)
+        torch.neg(src, out=dst)
     stream = torch.cuda.current_stream()
-    ms = sorted(time_events(lambda: dst.copy_(src), 10, stream))[5]
+    ms = sorted(time_events(lambda: torch.neg(src, out=dst), 11, stream))[5]
     del src, dst
     torch.cuda.empty_cache()
-    return 2 * n * 8 / (ms * 1e-3) / 1e9
+    return 2 * n * 4 / (ms * 1e-3) / 1e9
+
+
+def profiled_traffic() -> int | None:
+    """HBM bytes per audit launch from the committed FETCH_SIZE / WRITE_SIZE summary of this
+    workload (scaled by the calibration kernel), or None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "tile_lse_llama3_decode_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        return None
+    return None
 
 
 def cpu_baseline(step: Step, bound_s: float) -> dict:
@@ -180,33 +195,33 @@ def cpu_baseline(step: Step, bound_s: float) -> dict:
     torch.set_num_threads(threads)
     b = step.batch
     planes = oracle_audit.new_planes(LAYERS, b.rows, b.width, b.group_rows)
-    done, busy = 0, 0.0
     host = {}
-    for layer in range(LAYERS):
-        pool, group = layer % POOLS, layer % b.kv_heads
-        if (pool, group) not in host:
-            keys, table = workloads.host_keys(b, step.pools[pool], heads=[group])
-            host[(pool, group)] = (torch.from_numpy(keys).to(torch.bfloat16), table)
-        keys, table = host[(pool, group)]
-        q = step.q[layer].cpu()
-        t0 = time.perf_counter()
-        oracle_audit.tile_lse_torch(planes, q, keys, table, b.lens, np.arange(b.rows), np.ones(b.rows), layer,
-                                    step.scale, b.block_size, b.group_rows, group, key_head=0)
-        busy += time.perf_counter() - t0
-        done += 1
-        if busy >= bound_s:
-            break
+    launches, busy = 0, 0.0
+    while busy < bound_s:  # whole passes over the 32 layers until the bound
+        for layer in range(LAYERS):
+            pool, group = layer % POOLS, layer % b.kv_heads
+            if (pool, group) not in host:
+                keys, table = workloads.host_keys(b, step.pools[pool], heads=[group])
+                host[(pool, group)] = (torch.from_numpy(keys).to(torch.bfloat16), table)
+            keys, table = host[(pool, group)]
+            q = step.q[layer].cpu()
+            t0 = time.perf_counter()
+            oracle_audit.tile_lse_torch(planes, q, keys, table, b.lens, np.arange(b.rows), np.ones(b.rows), layer,
+                                        step.scale, b.block_size, b.group_rows, group, key_head=0)
+            busy += time.perf_counter() - t0
+            launches += 1
     # the sample's records agree with the device's (same layers)
-    got = step.plane.read_planes()[:, :done]
-    live = ~np.isnan(planes[0, :done])
-    err = float(np.abs(got[0][live] - planes[0, :done][live]).max())
+    got = step.plane.read_planes()
+    live = ~np.isnan(planes[0])
+    err = float(np.abs(got[0][live] - planes[0][live]).max())
     return {
-        "value": round(done * audit_bytes(b) / busy / 1e9, 3),
+        "value": round(launches * audit_bytes(b) / busy / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"audit of {done} of the 32 layers (all 128 rows, one KV group each) with oracle.audit.tile_lse_torch, "
-                  f"{busy:.1f} s; tile max agrees with the GPU to {err:.1e}",
+        "sample": f"{launches // LAYERS} passes over the 32 layer launches of the step (all 128 rows, one KV group "
+                  f"each) with oracle.audit.tile_lse_torch (gather, matmul, tile max / sum exp), {busy:.1f} s of "
+                  f"audit time; tile max agrees with the GPU to {err:.1e}",
     }
 
 
@@ -251,12 +266,13 @@ def main() -> None:
                 raise RuntimeError("a graph replay differs from the eager step")
 
     if args.profile_only:
-        # a plain copy of known size first, to scale the memory counters of the kernels that follow
+        # a plain streaming kernel of known size first (one read and one write of 256 MiB, the
+        # only negation in the run), to scale the memory counters of the kernels that follow
         calib_bytes = 256 << 20
         src = torch.ones(calib_bytes // 4, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
         for _ in range(args.warmup + args.steps):
@@ -329,16 +345,25 @@ def main() -> None:
     vl4 = torch.empty_like(l4)
     sm4 = torch.zeros(6, dtype=torch.int64, device="cuda")
 
-    def view_build_c4():
+    def rank_c4():
         step.ekv.call("ekv_rank_uniform", s4.data_ptr(), 8192, n4.data_ptr(), 0, 0, 0, 0, 0, 0, 0, 1024, 8192, 0.5,
                       -1, k4.data_ptr(), 8192, sm4.data_ptr(), handle)
+
+    def compact_c4():
         step.ekv.call("ekv_compact_view", t4.data_ptr(), 8192, l4.data_ptr(), k4.data_ptr(), 8192, 1024, 8192, 16,
                       v4.data_ptr(), 8192, vl4.data_ptr(), handle)
 
+    def view_build_c4():
+        rank_c4()
+        compact_c4()
+
     view_build_c4()
     c4_ms = float(np.median(time_events(view_build_c4, 20, stream)))
+    c4_rank_ms = float(np.median(time_events(rank_c4, 20, stream)))
+    c4_compact_ms = float(np.median(time_events(compact_c4, 20, stream)))
 
     peak = copy_peak_gbs()
+    traffic = profiled_traffic()
     out = {
         "metric": "audit KV GB/s (% HBM peak) at Llama-3-8B decode shape; view build us",
         "value": round(value, 2),
@@ -367,9 +392,11 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "ekv_audit_tile_lse (one KV group)",
             "mean_launch_us": round(audit_ms * 1e3, 2),
+            "traffic_source": "profiles/tile_lse_llama3_decode_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                              "scaled by a 256 MiB streaming kernel)",
             "measured_copy_peak_gbs": round(peak, 1),
             "frac_of_measured_peak": round(achieved / peak, 4),
         },
@@ -381,7 +408,9 @@ def main() -> None:
         "every_kv_head_audit": {"bytes_per_launch": audit_bytes(batch, batch.kv_heads), "us": round(all_ms * 1e3, 2),
                                 "gbs": round(all_gbs, 1), "frac": round(all_gbs / HBM_PEAK_GBS, 4)},
         "view_build_us": {"llama3_step_128_rows": round(view_ms * 1e3, 2),
-                          "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2)},
+                          "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2),
+                          "config_1024x8192_rank": round(c4_rank_ms * 1e3, 2),
+                          "config_1024x8192_compact": round(c4_compact_ms * 1e3, 2)},
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu:

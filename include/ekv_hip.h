@@ -49,7 +49,7 @@ const char *ekv_last_error(void);
 int ekv_abi_version(void);
 
 /*
- * A1 + A10: the audit statistic of one attention layer.
+ * The audit statistic of one attention layer.
  * Replaces tile_lse_kernel and its launch, runtime/audit_kernel.py:34-109 and :224-265.
  *
  * For every row r with *flag != 0 and select[r] != 0, every tile of tile_blocks (= 2) blocks
@@ -72,7 +72,9 @@ int ekv_abi_version(void);
  * cycles : optional uint64 [cycles_rows]; when non-NULL every unit of work adds its
  *          s_memtime duration to cycles[r] (r < cycles_rows), for the first audited head only
  *          (the pass's timer, mlir_pass/lib/eKVTimer.cpp:1348-1387).
- * chunk_tiles: tiles per work unit (0 = the library's default).
+ * chunk_tiles: the fewest tiles one wavefront takes (0 = 1).  The live tiles of all selected rows
+ *          form one list split into equal contiguous slices, one per wavefront of a grid the GPU
+ *          holds at once; a larger value shrinks the grid for small batches.
  */
 int ekv_audit_tile_lse(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
                        const void *keys, int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos,
@@ -86,7 +88,7 @@ int ekv_audit_tile_lse(const void *q, int q_dtype, int64_t q_stride_token, int64
                        int32_t chunk_tiles, void *stream);
 
 /*
- * A4 + A5: exact per-block attention shares of the chosen rows, from the statistic planes.
+ * Exact per-block attention shares of the chosen rows, from the statistic planes.
  * Replaces read_tile_rows + normalize_tile_lse (observe/tile_shares.py:129-173 and :58-103),
  * computing on the device what the reference copies to the host and normalises with NumPy.
  *
@@ -115,7 +117,7 @@ int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row
                            int64_t shares_stride, void *stream);
 
 /*
- * A6 + A7: the `uniform` budget split and the per-row ranking, on the device.
+ * The `uniform` budget split and the per-row ranking, on the device.
  * Replaces Controller._allocate's pin / budget rules (observe/controller.py:398-451) feeding
  * allocate(..., "uniform") (observe/allocation.py:39-91).
  *
@@ -153,7 +155,7 @@ int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_
                         int32_t *workspace, void *stream);
 
 /*
- * A8: compact_block_table (runtime/block_view.py:36-56).
+ * compact_block_table (runtime/block_view.py:36-56).
  * keep'[r, b] = (keep[r, b] | b == 0 | b == n-1) & b < n,  n = ceil(seq_lens[r] / block_size).
  * view_table row r = table row r stably partitioned: keep' entries first, the rest after them,
  * each in original order (all `width` entries).  view_lens[r] = (sum keep' - 1) * block_size
@@ -165,7 +167,7 @@ int ekv_compact_view(const int32_t *table, int64_t table_stride, const int32_t *
                      int32_t *view_lens, void *stream);
 
 /*
- * A8 + A9: DecodeView.build's keep composition fused with the compaction and the read
+ * DecodeView.build's keep composition fused with the compaction and the read
  * counters (runtime/block_view.py:272-295 and :297-329).
  * keep = committed | !live | audited[r] | !decoding[r], then & !released  (committed NULL:
  * all ones; audited / decoding / released NULL: none / all decoding / none).

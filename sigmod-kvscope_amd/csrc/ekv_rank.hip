@@ -10,7 +10,9 @@
 // operands), and the `free - sum(floor)` leftover blocks go to the rows ranked first by
 // (-(exact_i - floor_i), i).  That is O(rows) work per workgroup and needs no second kernel.
 // The row then keeps its quota of open blocks by (share desc, block index asc), found by an
-// 8-bit radix select over order-preserving keys in LDS and a prefix count of the tied keys.
+// 8-bit radix select over order-preserving keys (a row's keys stay in registers, block
+// tid + 512 i in slot i of thread tid; 256-bin LDS histograms, scanned by one wave) and a
+// ballot / scan count of the tied keys before each block.
 //
 // Keys.  The reference ranks `max(s, 0) / total` in float64 with a stable argsort.  For float32
 // scores this order equals the order of max(s, 0) itself: distinct float32 values differ by at
@@ -29,7 +31,10 @@ namespace ekv {
 namespace rank {
 
 constexpr int kThreads = 512;
-constexpr int kMaxWidth = 12288;  // 5 bytes of LDS per block
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxPer = 24;                  // blocks per thread, block tid + kThreads i
+constexpr int kMaxWidth = kThreads * kMaxPer;  // 12288: a row lives in registers
+constexpr int kRowRegs = 4;                  // rows per thread whose open count stays in registers
 constexpr uint32_t kClosed = 0xFFFFFFFFu;  // key of a block that is not open
 
 struct Params {
@@ -106,34 +111,72 @@ __global__ __launch_bounds__(256) void count_kernel(const Params p, int32_t *cou
   }
 }
 
+// Sum of N values over the workgroup in one pass (every thread receives the sums).
+template <int N>
+__device__ __forceinline__ void block_sums(long long (&v)[N], long long (*scratch)[kWaves]) {
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    v[j] = wave_sum_i64(v[j]);
+    if (lane_id() == 0) scratch[j][wave] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    long long s = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += scratch[j][w];
+    v[j] = s;
+  }
+  __syncthreads();
+}
+
+// PER: blocks per thread (the row's width is at most kThreads * PER)
+template <int PER>
 __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
-  extern __shared__ uint32_t s_keys[];  // [width] keys, then [width] keep bytes
-  __shared__ long long s_red64[kThreads / kWave];
-  __shared__ int s_red[kThreads / kWave];
-  __shared__ int s_scan[kThreads / kWave];
-  __shared__ int s_hist[256];
+  constexpr int kPer = PER;
+  __shared__ long long s_red[5][kWaves];
+  __shared__ int s_hist[2][256];
+  __shared__ int s_count[kPer * kWaves];  // equal keys per (load, wave), then their exclusive scan
+  __shared__ int s_scan[kWaves];
   __shared__ int s_digit, s_krem;
-  uint8_t *s_keep = (uint8_t *)(s_keys + p.width);
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
 
   // ---- totals over every row: controller.py:435-437, allocation.py:57-67 -----------------
-  long long total = 0, floor_pins = 0, sizes = 0, open_total = 0, nreq = 0;
-  for (int r = tid; r < p.rows; r += kThreads) {
+  // the open blocks of the first kRowRegs * kThreads rows stay in registers for the quota pass
+  long long open_reg[kRowRegs];
+  long long t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
+#pragma unroll
+  for (int i = 0; i < kRowRegs; ++i) {
+    const int r = tid + i * kThreads;
+    open_reg[i] = -1;  // not taking part
+    if (r < p.rows) {
+      const RowInfo ri = row_info(p, r);
+      if (ri.part) {
+        t5[0] += ri.n;
+        t5[1] += ri.pinned;
+        t5[2] += ri.exist;
+        t5[3] += ri.exist - ri.pinned;
+        t5[4] += 1;
+        open_reg[i] = ri.exist - ri.pinned;
+      }
+    }
+  }
+  for (int r = tid + kRowRegs * kThreads; r < p.rows; r += kThreads) {
     const RowInfo ri = row_info(p, r);
     if (!ri.part) continue;
-    total += ri.n;
-    floor_pins += ri.pinned;
-    sizes += ri.exist;
-    open_total += ri.exist - ri.pinned;
-    nreq += 1;
+    t5[0] += ri.n;
+    t5[1] += ri.pinned;
+    t5[2] += ri.exist;
+    t5[3] += ri.exist - ri.pinned;
+    t5[4] += 1;
   }
-  total = block_sum<kThreads>(total, s_red64);
-  floor_pins = block_sum<kThreads>(floor_pins, s_red64);
-  sizes = block_sum<kThreads>(sizes, s_red64);
-  open_total = block_sum<kThreads>(open_total, s_red64);
-  nreq = block_sum<kThreads>(nreq, s_red64);
+  block_sums(t5, s_red);
+  const long long total = t5[0], floor_pins = t5[1], sizes = t5[2], open_total = t5[3], nreq = t5[4];
 
   long long budget = p.budget_in;
   if (budget < 0) {
@@ -159,119 +202,157 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     return;
   }
 
+  // ---- the row's blocks: scores and masks into registers (block tid + kThreads i) -----------
+  const float *srow = p.scores + (int64_t)row * p.scores_stride;
+  float sv[kPer];
+  uint32_t exist_bits = 0, pin_bits = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = tid + i * kThreads;
+    const bool in = b < me.n;
+    sv[i] = in ? srow[b] : 0.0f;
+    exist_bits |= (in && exists(p, row, b)) ? (1u << i) : 0u;
+    pin_bits |= (in && is_pinned(p, me, row, b)) ? (1u << i) : 0u;
+  }
+
   // ---- this row's quota: largest remainder in IEEE double, allocation.py:79-86 ---------------
   const long long my_open = me.exist - me.pinned;
-  long long quota = 0;
-  if (keep_all) {
-    quota = my_open;
-  } else {
-    const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
-    const long long my_floor = (long long)my_exact;
-    const double my_frac = my_exact - (double)my_floor;
-    long long floors = 0, ahead = 0;
-    for (int r = tid; r < p.rows; r += kThreads) {
-      const RowInfo ri = row_info(p, r);
-      if (!ri.part) continue;
-      const long long open = ri.exist - ri.pinned;
+  const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
+  const long long my_floor = (long long)my_exact;
+  const double my_frac = my_exact - (double)my_floor;
+  // [0] floors, [1] rows ahead in the leftover order, [2..4] has NaN / +inf / positive score,
+  // then [0] (in the second reduction) open blocks
+  long long q5[5] = {0, 0, 0, 0, 0};
+  if (!keep_all) {
+    auto visit = [&](int r, long long open) {
       const double exact = open_total > 0 ? (double)(free_blocks * open) / (double)open_total : 0.0;
       const long long fl = (long long)exact;
       const double frac = exact - (double)fl;
-      floors += fl;
-      ahead += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
+      q5[0] += fl;
+      q5[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
+    };
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i)
+      if (open_reg[i] >= 0) visit(tid + i * kThreads, open_reg[i]);
+    for (int r = tid + kRowRegs * kThreads; r < p.rows; r += kThreads) {
+      const RowInfo ri = row_info(p, r);
+      if (ri.part) visit(r, ri.exist - ri.pinned);
     }
-    floors = block_sum<kThreads>(floors, s_red64);
-    ahead = block_sum<kThreads>(ahead, s_red64);
-    const long long leftover = free_blocks - floors;
-    quota = my_floor + (ahead < leftover ? 1 : 0);
   }
-
-  // ---- key mode of the row's shares: allocation.py:46-52 over the existing blocks -----------
-  const float *srow = p.scores + (int64_t)row * p.scores_stride;
-  int has_nan = 0, has_inf = 0, has_pos = 0;
-  for (int b = tid; b < me.n; b += kThreads) {
-    if (!exists(p, row, b)) continue;
-    const float s = srow[b];
-    has_nan |= __builtin_isnan(s) ? 1 : 0;
-    has_inf |= (__builtin_isinf(s) && s > 0.0f) ? 1 : 0;
-    has_pos |= s > 0.0f ? 1 : 0;
+  // key mode of the row's shares: allocation.py:46-52 over the existing blocks
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    if (!((exist_bits >> i) & 1u)) continue;
+    const float s = sv[i];
+    q5[2] |= __builtin_isnan(s) ? 1 : 0;
+    q5[3] |= (__builtin_isinf(s) && s > 0.0f) ? 1 : 0;
+    q5[4] |= s > 0.0f ? 1 : 0;
   }
-  has_nan = block_sum<kThreads>(has_nan, s_red);
-  has_inf = block_sum<kThreads>(has_inf, s_red);
-  has_pos = block_sum<kThreads>(has_pos, s_red);
-  const int mode = has_nan ? 0 : (has_inf ? 2 : (has_pos ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
+  block_sums(q5, s_red);
+  long long quota;
+  if (keep_all) {
+    quota = my_open;
+  } else {
+    const long long leftover = free_blocks - q5[0];
+    quota = my_floor + (q5[1] < leftover ? 1 : 0);
+  }
+  const int mode = q5[2] ? 0 : (q5[3] ? 2 : (q5[4] ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
 
-  // ---- keys of the open blocks, and the pinned / released part of the keep row -------------
-  int open_count = 0;
-  for (int b = tid; b < p.width; b += kThreads) {
-    uint32_t key = kClosed;
-    uint8_t k = 1;
-    if (b < me.n) {
-      if (!exists(p, row, b)) {
-        k = 0;
-      } else if (!is_pinned(p, me, row, b)) {
-        k = 0;  // decided below
-        const float s = srow[b];
-        if (mode == 1) key = s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
-        else if (mode == 2) key = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
-        else key = 0u;
-        ++open_count;
-      }
+  // ---- keys of the open blocks (order-preserving, larger first), kClosed elsewhere ----------
+  uint32_t key[kPer];
+  long long open_count[1] = {0};
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    key[i] = kClosed;
+    if (((exist_bits & ~pin_bits) >> i) & 1u) {
+      const float s = sv[i];
+      if (mode == 1) key[i] = s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
+      else if (mode == 2) key[i] = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
+      else key[i] = 0u;
+      open_count[0] += 1;
     }
-    s_keys[b] = key;
-    s_keep[b] = k;
   }
-  open_count = block_sum<kThreads>(open_count, s_red);
-  // (block_sum ends with a barrier, so the LDS rows are complete)
+  block_sums(open_count, s_red);
 
-  if (quota >= open_count) {
-    for (int b = tid; b < me.n; b += kThreads)
-      if (s_keys[b] != kClosed) s_keep[b] = 1;
+  // keep: blocks past the row's end 1, released 0, pinned 1, open blocks decided here
+  uint32_t open_keep = 0;
+  if (quota >= open_count[0]) {
+    open_keep = ~0u;
   } else if (quota > 0) {
-    // radix select of the quota-th largest key, 8 bits at a time from the top
+    // radix select of the quota-th largest key, 8 bits at a time from the top; the histogram is
+    // double-buffered so that clearing the next one needs no extra barrier
     uint32_t prefix = 0, mask = 0;
     int k_rem = (int)quota;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      if (tid < 256) s_hist[tid] = 0;
+    if (tid < 256) s_hist[0][tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      int *hist = s_hist[pass & 1];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (key[i] != kClosed && (key[i] & mask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255], 1);
+      if (tid < 256) s_hist[(pass & 1) ^ 1][tid] = 0;
       __syncthreads();
-      for (int b = tid; b < me.n; b += kThreads) {
-        const uint32_t key = s_keys[b];
-        if (key != kClosed && (key & mask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255], 1);
-      }
-      __syncthreads();
-      // thread t looks at digit 255 - t: an inclusive scan gives the count of digits >= it
-      const int h = tid < 256 ? s_hist[255 - tid] : 0;
-      int scan_total;
-      const int before = block_exclusive_scan<kThreads>(h, s_scan, scan_total);
-      if (tid < 256 && before < k_rem && before + h >= k_rem) {
-        s_digit = 255 - tid;
-        s_krem = k_rem - before;
+      if (wave == 0) {
+        // lane l holds digits 255 - 4l .. 252 - 4l; a scan over the lanes counts the keys above
+        int c[4], s4 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = hist[255 - 4 * lane - j];
+          s4 += c[j];
+        }
+        const int inc = wave_inclusive_scan(s4);
+        int acc = inc - s4;
+        if (acc < k_rem && inc >= k_rem) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (acc < k_rem && acc + c[j] >= k_rem) {
+              s_digit = 255 - 4 * lane - j;
+              s_krem = k_rem - acc;
+            }
+            acc += c[j];
+          }
+        }
       }
       __syncthreads();
       prefix |= (uint32_t)s_digit << shift;
       mask |= 255u << shift;
       k_rem = s_krem;
-      __syncthreads();
     }
     // keep every key above the threshold and the first k_rem equal keys by block index
-    const int chunk = (me.n + kThreads - 1) / kThreads;
-    const int b0 = tid * chunk, b1 = min(b0 + chunk, me.n);
-    int eq = 0;
-    for (int b = b0; b < b1; ++b) eq += s_keys[b] == prefix ? 1 : 0;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int eq_rank[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint64_t eq = __ballot(key[i] == prefix);
+      eq_rank[i] = __popcll(eq & below);
+      if (lane == 0) s_count[i * kWaves + wave] = __popcll(eq);
+    }
+    __syncthreads();
+    const int v = tid < kPer * kWaves ? s_count[tid] : 0;
     int eq_total;
-    int rank_eq = block_exclusive_scan<kThreads>(eq, s_scan, eq_total);
-    for (int b = b0; b < b1; ++b) {
-      const uint32_t key = s_keys[b];
-      if (key == kClosed) continue;
-      if (key > prefix) {
-        s_keep[b] = 1;
-      } else if (key == prefix) {
-        if (rank_eq < k_rem) s_keep[b] = 1;
-        ++rank_eq;
-      }
+    const int excl = block_exclusive_scan<kThreads>(v, s_scan, eq_total);
+    if (tid < kPer * kWaves) s_count[tid] = excl;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const bool kept = key[i] != kClosed &&
+                        (key[i] > prefix || (key[i] == prefix && s_count[i * kWaves + wave] + eq_rank[i] < k_rem));
+      open_keep |= kept ? (1u << i) : 0u;
     }
   }
-  __syncthreads();
-  for (int b = tid; b < p.width; b += kThreads) keep_row[b] = s_keep[b];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = tid + i * kThreads;
+    if (b >= p.width) continue;
+    uint8_t k;
+    if (b >= me.n) k = 1;
+    else if (!((exist_bits >> i) & 1u)) k = 0;
+    else if ((pin_bits >> i) & 1u) k = 1;
+    else k = (open_keep >> i) & 1u;
+    keep_row[b] = k;
+  }
 }
 
 }  // namespace rank
@@ -331,7 +412,14 @@ extern "C" int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, c
     if (rc != EKV_OK) return rc;
     p.counts = workspace;
   }
-  const size_t lds = (size_t)width * sizeof(uint32_t) + (size_t)width;
-  hipLaunchKernelGGL(rank::rank_kernel, dim3(rows), dim3(rank::kThreads), lds, (hipStream_t)stream, p);
+  const int per = (width + rank::kThreads - 1) / rank::kThreads;
+  if (per <= 4)
+    hipLaunchKernelGGL(rank::rank_kernel<4>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
+  else if (per <= 8)
+    hipLaunchKernelGGL(rank::rank_kernel<8>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
+  else if (per <= 16)
+    hipLaunchKernelGGL(rank::rank_kernel<16>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(rank::rank_kernel<24>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_rank_uniform launch");
 }

@@ -6,13 +6,24 @@
 // renormalised per-block max).  The reference copies the planes to the host and does this in
 // float64 NumPy; here it runs in float32 on the planes where the audit kernel wrote them.
 //
+// Algebra.  exp(u - c) = l * t * exp(m - c) / T, with t = T / valid on a partial last tile and 1
+// elsewhere.  The 1/T cancels in every softmax, so with the weight w = l * t the softmax of a
+// (layer, query row) record over its blocks is w_b exp(m_b - M) / sum w exp(m - M) for any M,
+// and no logarithm is taken.  M = the largest m of the record keeps every term at most w (l is
+// a sum of at most T * block_size exponentials no larger than 1).  u is finite -- the block
+// carries weight -- iff m is finite and 0 < l < inf.  With u planes (ekv_normalize_tile_lse),
+// m = u and l = 1.
+//
 // One workgroup of 16 waves per output row.  Phase 1: wave w takes layers w, w + 16, ...; for
-// each it streams the row's [width][cells] records (coalesced: consecutive lanes read
-// consecutive cells, 8 elements' loads in flight per lane before any is used) and keeps an
-// online (max, sum of exp) per lane, which a butterfly over the lanes of the same query row
-// turns into the (layer, query row) peak and total, kept in LDS.  Phase 2: each thread owns
-// blocks and sums their shares over layers and query rows in a fixed order (8 records loaded
-// ahead), so the result is deterministic (no atomics).
+// each it streams the row's [width][cells] records (coalesced; when the cells come in 16-byte
+// quads, as for a group of 4 query rows, a lane loads a block's quad at once; 8 loads of each
+// plane in flight per lane) and keeps a running (max m, sum w exp(m - max)) per cell, which a
+// butterfly over the lanes holding the same cells turns into the record's peak and total, kept
+// in LDS.  Phase 2: the row's blocks x layer groups are spread over all 16 waves; each thread
+// sums (or maxes) its block's shares over its layers and query rows in a fixed order, and the
+// group partials are combined in LDS in a fixed order, so the result is deterministic (no
+// atomics) and the same on every call.
+#include <limits.h>
 #include <math.h>
 
 #include "ekv_common.hpp"
@@ -21,8 +32,8 @@ namespace ekv {
 namespace shares {
 
 constexpr int kThreads = 1024;
-constexpr int kBatch = 8;  // loads in flight per lane
 constexpr int kWaves = kThreads / kWave;
+constexpr int kBatch = 8;  // quads (or cells) of each plane in flight per lane
 constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
 
@@ -32,27 +43,38 @@ struct Params {
   int64_t layer_stride, row_stride;
   int32_t layers, cells, cells_pow2, width;
   const int32_t *row_ids, *row_blocks;
-  float log_tile;  // log(tile_blocks)
   int32_t tile_blocks, aggregate, from_u;
   float *shares;
   int64_t shares_stride;
 };
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ bool finite(float x) { return __builtin_isfinite(x); }
 
-// log weight of block b of one record (m and l as loaded, or u itself when from_u), NaN when the
-// record carries none.  n is the row's length in blocks, which may exceed the width: the tail
-// rule uses it unclipped.
-__device__ __forceinline__ float weight_of(const Params &p, float m, float l, int b, int n) {
-  float u = p.from_u ? m : m + __logf(l) - p.log_tile;
-  // a partial last tile gives its weight back to the blocks that exist, tile_shares.py:84-87
-  const int T = p.tile_blocks;
-  const int tail_start = (n / T) * T;
-  if ((n % T) != 0 && b >= tail_start) u += __logf((float)T / (float)max(n - tail_start, 1));
-  return u;
-}
+// The row's weight rule.  n is the row's length in blocks, which may exceed the width: the tail
+// rule uses it unclipped (tile_shares.py:84-87).
+struct RowWeight {
+  int tail_start;   // first block of a partial last tile (INT_MAX when the last tile is whole)
+  float tail_mult;  // T / blocks in that tile
+  bool from_u;
 
-// merge two (max, sum exp(x - max)) pairs
+  __device__ RowWeight(const Params &p, int n) {
+    const int T = p.tile_blocks;
+    const int whole = (n / T) * T;
+    tail_start = n != whole ? whole : INT_MAX;
+    tail_mult = n != whole ? (float)T / (float)(n - whole) : 1.0f;
+    from_u = p.from_u != 0;
+  }
+  // w of block b's record from its two plane values; 0 when the record carries no weight
+  __device__ __forceinline__ float operator()(float m, float l, int b) const {
+    const float lw = from_u ? 1.0f : l;
+    const bool carries = finite(m) && lw > 0.0f && lw < INFINITY;
+    return carries ? (b >= tail_start ? lw * tail_mult : lw) : 0.0f;
+  }
+};
+
+// merge two (max, sum w exp(m - max)) pairs
 __device__ __forceinline__ void merge(float &m, float &s, float m2, float s2) {
   const float M = fmaxf(m, m2);
   if (M == -INFINITY) return;
@@ -62,8 +84,27 @@ __device__ __forceinline__ void merge(float &m, float &s, float m2, float s2) {
   s = a + b;
 }
 
+// running (max, sum) after a batch of N (m, w) pairs (w = 0: no weight)
+template <int N>
+__device__ __forceinline__ void absorb(float &mx, float &sum, const float (&m)[N], const float (&w)[N]) {
+  float bm = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < N; ++k) bm = w[k] > 0.0f ? fmaxf(bm, m[k]) : bm;
+  if (bm > mx) {
+    sum *= __expf(mx - bm);  // mx = -inf: sum is 0 and stays 0
+    mx = bm;
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) sum += w[k] > 0.0f ? w[k] * __expf(m[k] - mx) : 0.0f;
+}
+
+// VEC: the cells of a block come in 16-byte quads (cells a multiple of 4, cells / 4 a power of
+// two, 16-byte aligned planes and strides), so one lane loads a quad with one instruction and
+// quad e of a (layer, row) record is at 4 e.  Otherwise every cell is loaded on its own.
+template <bool VEC>
 __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   extern __shared__ float s_stats[];  // [layers][cells_pow2] peak, then [layers][cells_pow2] 1/total
+  __shared__ float s_part[kThreads];  // per (layer group, block) partial shares
   __shared__ float s_red[kWaves];
   __shared__ int s_contrib;
 
@@ -71,61 +112,106 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   const int src_row = p.row_ids != nullptr ? p.row_ids[out_row] : out_row;
   const int n_row = p.row_blocks != nullptr ? max(p.row_blocks[out_row], 0) : p.width;
   const int n = min(n_row, p.width);  // blocks with records
-  const int CP = p.cells_pow2;
+  const int CP = p.cells_pow2, cp_log2 = __builtin_ctz(CP);
   const int cells = p.cells;
+  const RowWeight weight(p, n_row);
+  const int64_t row_base = (int64_t)src_row * p.row_stride;
+  const float *lplane = weight.from_u ? p.m : p.l;  // never read through when from_u
   float *peak = s_stats;
   float *inv_total = s_stats + p.layers * CP;
   if (threadIdx.x == 0) s_contrib = 0;
   __syncthreads();
 
+  const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int q = lane & (CP - 1);  // every element a lane visits has this query row (CP divides 64)
-  const int64_t span = (int64_t)n * CP;
+  const int wave = tid / kWave;
 
   // ---- phase 1: peak and total of every (layer, query row) ------------------------------
   int contrib = 0;
-  for (int layer = wave; layer < p.layers; layer += kWaves) {
-    const float *mrow = p.m + layer * p.layer_stride + (int64_t)src_row * p.row_stride;
-    const float *lrow = p.from_u ? nullptr : p.l + layer * p.layer_stride + (int64_t)src_row * p.row_stride;
-    float mx = -INFINITY, sum = 0.0f;
-    if (q < cells) {
-      for (int64_t e0 = lane; e0 < span; e0 += (int64_t)kWave * kBatch) {
-        float mv[kBatch], lv[kBatch];
+  if constexpr (VEC) {
+    const int QP = cells >> 2, qp_log2 = __builtin_ctz(QP);  // quads per block, dividing 64
+    const int slot = lane & (QP - 1);  // the quad of the block every element of this lane is in
+    const int quads = n * QP;
+    for (int layer = wave; layer < p.layers; layer += kWaves) {
+      const int64_t base = layer * p.layer_stride + row_base;
+      const f32x4_t *mq = reinterpret_cast<const f32x4_t *>(p.m + base);
+      const f32x4_t *lq = reinterpret_cast<const f32x4_t *>(lplane + base);
+      float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int e0 = lane; e0 < quads; e0 += kWave * kBatch) {
+        f32x4_t mv[kBatch], lv[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-          const int64_t e = e0 + (int64_t)k * kWave;
-          const int64_t idx = e < span ? (e / CP) * cells + q : 0;
-          mv[k] = mrow[idx];
-          lv[k] = p.from_u ? 0.0f : lrow[idx];
+          const int at = e0 + k * kWave < quads ? e0 + k * kWave : 0;
+          mv[k] = mq[at];
+          lv[k] = weight.from_u ? mv[k] : lq[at];
         }
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int64_t e = e0 + (int64_t)k * kWave;
-          if (e >= span) break;
-          const int b = (int)(e / CP);
-          const float u = weight_of(p, mv[k], lv[k], b, n_row);
-          if (finite(u)) {
-            if (u > mx) {
-              sum = sum * __expf(mx - u) + 1.0f;
-              mx = u;
-            } else {
-              sum += __expf(u - mx);
-            }
+        for (int j = 0; j < 4; ++j) {
+          float m[kBatch], w[kBatch];
+#pragma unroll
+          for (int k = 0; k < kBatch; ++k) {
+            const int e = e0 + k * kWave;
+            m[k] = mv[k][j];
+            w[k] = e < quads ? weight(mv[k][j], lv[k][j], e >> qp_log2) : 0.0f;
           }
+          absorb(mx[j], sum[j], m, w);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        for (int msk = QP; msk < kWave; msk <<= 1) {
+          const float m2 = shfl_xor(mx[j], msk);
+          const float s2 = shfl_xor(sum[j], msk);
+          merge(mx[j], sum[j], m2, s2);
+        }
+      }
+      if (lane < QP) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = 4 * slot + j;
+          const bool has = mx[j] != -INFINITY;
+          peak[layer * CP + c] = has ? mx[j] : NAN;
+          inv_total[layer * CP + c] = has ? 1.0f / sum[j] : 0.0f;
+          contrib += has ? 1 : 0;
         }
       }
     }
-    for (int msk = CP; msk < kWave; msk <<= 1) {
-      const float m2 = shfl_xor(mx, msk);
-      const float s2 = shfl_xor(sum, msk);
-      merge(mx, sum, m2, s2);
-    }
-    if (lane < CP) {
-      const bool has = lane < cells && mx != -INFINITY;
-      peak[layer * CP + lane] = has ? mx : NAN;
-      inv_total[layer * CP + lane] = has ? 1.0f / sum : 0.0f;
-      contrib += has ? 1 : 0;
+  } else {
+    const int q = lane & (CP - 1);  // every element a lane visits has this query row (CP divides 64)
+    const int span = n * CP;
+    for (int layer = wave; layer < p.layers; layer += kWaves) {
+      const float *mrow = p.m + layer * p.layer_stride + row_base;
+      const float *lrow = lplane + layer * p.layer_stride + row_base;
+      float mx = -INFINITY, sum = 0.0f;
+      if (q < cells) {
+        for (int e0 = lane; e0 < span; e0 += kWave * kBatch) {
+          float m[kBatch], w[kBatch];
+#pragma unroll
+          for (int k = 0; k < kBatch; ++k) {
+            const int e = e0 + k * kWave;
+            const int idx = e < span ? (e >> cp_log2) * cells + q : 0;
+            m[k] = mrow[idx];
+            w[k] = weight.from_u ? m[k] : lrow[idx];
+          }
+#pragma unroll
+          for (int k = 0; k < kBatch; ++k) {
+            const int e = e0 + k * kWave;
+            w[k] = e < span ? weight(m[k], w[k], e >> cp_log2) : 0.0f;
+          }
+          absorb(mx, sum, m, w);
+        }
+      }
+      for (int msk = CP; msk < kWave; msk <<= 1) {
+        const float m2 = shfl_xor(mx, msk);
+        const float s2 = shfl_xor(sum, msk);
+        merge(mx, sum, m2, s2);
+      }
+      if (lane < CP) {
+        const bool has = lane < cells && mx != -INFINITY;
+        peak[layer * CP + lane] = has ? mx : NAN;
+        inv_total[layer * CP + lane] = has ? 1.0f / sum : 0.0f;
+        contrib += has ? 1 : 0;
+      }
     }
   }
   contrib = wave_sum_int(contrib);
@@ -135,50 +221,95 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
 
   float *out = p.shares + (int64_t)out_row * p.shares_stride;
   if (contributors == 0) {  // no evidence about the row, tile_shares.py:103
-    for (int b = threadIdx.x; b < p.width; b += kThreads) out[b] = NAN;
+    for (int b = tid; b < p.width; b += kThreads) out[b] = NAN;
     return;
   }
 
-  // ---- phase 2: per-block shares, summed (or maxed) in a fixed order -----------------------
+  // ---- phase 2: per-block shares, summed (or maxed) over (layer, query row) in a fixed order
   const bool use_max = p.aggregate == EKV_AGG_MAX;
-  float local_total = 0.0f;
-  const int records = p.layers * cells;  // (layer, query row) pairs, in a fixed order
-  for (int b = threadIdx.x; b < p.width; b += kThreads) {
+  // block b's shares over layers [l0, l1)
+  auto shares_of = [&](int b, int l0, int l1) -> float {
     float acc = 0.0f;
-    if (b < n) {
-      for (int r0 = 0; r0 < records; r0 += kBatch) {
-        float mv[kBatch], lv[kBatch];
+    const int64_t block_base = row_base + (int64_t)b * cells;
+    if constexpr (VEC) {
+      const int QP = cells >> 2, qp_log2 = __builtin_ctz(QP);
+      const int r_end = l1 * QP;  // quad rq = (layer rq / QP, cells 4 (rq % QP) ..)
+      for (int r0 = l0 * QP; r0 < r_end; r0 += kBatch) {
+        f32x4_t mv[kBatch], lv[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-          const int rec = r0 + k < records ? r0 + k : 0;
-          const int layer = rec / cells, c = rec - layer * cells;
-          const int64_t at = layer * p.layer_stride + (int64_t)src_row * p.row_stride + (int64_t)b * cells + c;
-          mv[k] = p.m[at];
-          lv[k] = p.from_u ? 0.0f : p.l[at];
+          const int rq = r0 + k < r_end ? r0 + k : r0;
+          const int64_t at = (rq >> qp_log2) * p.layer_stride + block_base + 4 * (rq & (QP - 1));
+          mv[k] = *reinterpret_cast<const f32x4_t *>(p.m + at);
+          lv[k] = weight.from_u ? mv[k] : *reinterpret_cast<const f32x4_t *>(lplane + at);
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-          const int rec = r0 + k;
-          if (rec >= records) break;
+          const int rq = r0 + k;
+          if (rq >= r_end) break;
+          const int stat = (rq >> qp_log2) * CP + 4 * (rq & (QP - 1));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float w = weight(mv[k][j], lv[k][j], b);  // > 0 only where phase 1 found a peak
+            const float share = w > 0.0f ? w * __expf(mv[k][j] - peak[stat + j]) * inv_total[stat + j] : 0.0f;
+            acc = use_max ? fmaxf(acc, share) : acc + share;
+          }
+        }
+      }
+    } else {
+      const int r_end = l1 * cells;  // record r = (layer r / cells, cell r % cells)
+      for (int r0 = l0 * cells; r0 < r_end; r0 += kBatch) {
+        float mv[kBatch], lv[kBatch];
+        int stat[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int rec = r0 + k < r_end ? r0 + k : r0;
           const int layer = rec / cells, c = rec - layer * cells;
-          const float pk = peak[layer * CP + c];
-          if (!finite(pk)) continue;
-          const float u = weight_of(p, mv[k], lv[k], b, n_row);
-          const float share = finite(u) ? __expf(u - pk) * inv_total[layer * CP + c] : 0.0f;
+          const int64_t at = layer * p.layer_stride + block_base + c;
+          stat[k] = layer * CP + c;
+          mv[k] = p.m[at];
+          lv[k] = weight.from_u ? mv[k] : lplane[at];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          if (r0 + k >= r_end) break;
+          const float w = weight(mv[k], lv[k], b);
+          const float share = w > 0.0f ? w * __expf(mv[k] - peak[stat[k]]) * inv_total[stat[k]] : 0.0f;
           acc = use_max ? fmaxf(acc, share) : acc + share;
         }
       }
     }
-    if (use_max) {
-      local_total += acc;
-      out[b] = acc;
-    } else {
-      out[b] = acc / (float)contributors;
+    return acc;
+  };
+
+  // the row's n blocks (rounded up to whole waves) times LG layer groups fill the workgroup
+  const int NC = ((n + kWave - 1) / kWave) * kWave;
+  const int LG = NC >= kThreads ? 1 : min(kThreads / NC, p.layers);
+  float local_total = 0.0f;
+  if (LG > 1) {
+    const int g = tid / NC, col = tid - g * NC;
+    float acc = 0.0f;
+    if (g < LG && col < n) acc = shares_of(col, g * p.layers / LG, (g + 1) * p.layers / LG);
+    s_part[tid] = acc;  // = s_part[g * NC + col]
+    __syncthreads();
+    for (int b = tid; b < p.width; b += kThreads) {
+      float v = 0.0f;
+      if (b < n) {
+        for (int h = 0; h < LG; ++h) v = use_max ? fmaxf(v, s_part[h * NC + b]) : v + s_part[h * NC + b];
+      }
+      local_total += v;
+      out[b] = use_max ? v : v / (float)contributors;
+    }
+  } else {
+    for (int b = tid; b < p.width; b += kThreads) {
+      const float v = b < n ? shares_of(b, 0, p.layers) : 0.0f;
+      local_total += v;
+      out[b] = use_max ? v : v / (float)contributors;
     }
   }
-  if (use_max) {
+  if (use_max) {  // renormalise the per-block max, tile_shares.py:97-100
     const float total = block_sum<kThreads>(local_total, s_red);
-    for (int b = threadIdx.x; b < p.width; b += kThreads) out[b] = total > 0.0f ? out[b] / total : 0.0f;
+    for (int b = tid; b < p.width; b += kThreads) out[b] = total > 0.0f ? out[b] / total : 0.0f;
   }
 }
 
@@ -190,16 +321,23 @@ int launch(Params p, int nrows, void *stream) {
                 p.tile_blocks, nrows);
   if (p.aggregate != EKV_AGG_MEAN && p.aggregate != EKV_AGG_MAX)
     return fail(EKV_EINVAL, "tile shares: unknown aggregate %d", p.aggregate);
+  if ((int64_t)p.width * kMaxCells > INT_MAX)
+    return fail(EKV_EUNSUPPORTED, "tile shares: width %d too large", p.width);
   int cp = 1;
   while (cp < p.cells) cp <<= 1;
   p.cells_pow2 = cp;
   if ((int64_t)p.layers * cp > kMaxStats)
     return fail(EKV_EUNSUPPORTED, "tile shares: %d layers x %d cells exceed the %d statistics kept per row",
                 p.layers, cp, kMaxStats);
-  p.log_tile = logf((float)p.tile_blocks);
   if (nrows == 0) return EKV_OK;
   const size_t lds = (size_t)2 * p.layers * cp * sizeof(float);
-  hipLaunchKernelGGL(shares_kernel, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
+  const bool aligned = ((uintptr_t)p.m % 16) == 0 && (p.from_u || ((uintptr_t)p.l % 16) == 0) &&
+                       p.layer_stride % 4 == 0 && p.row_stride % 4 == 0;
+  const bool vec = aligned && p.cells % 4 == 0 && cp == p.cells;  // cells / 4 a power of two
+  if (vec)
+    hipLaunchKernelGGL(shares_kernel<true>, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(shares_kernel<false>, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "tile shares launch");
 }
 

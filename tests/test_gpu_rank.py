@@ -90,6 +90,23 @@ def test_controller_rule_with_released_blocks_and_audit_length():
         assert int(summary[0]) == budget
 
 
+@pytest.mark.parametrize("width", [1, 2048, 2049, 4097, 8193, 12288])
+def test_every_row_layout_width(width):
+    # a row lives in registers, 4, 8, 16 or 24 blocks per thread
+    rng = np.random.default_rng(width)
+    rows = 6
+    blocks = np.array([width, 1, 0, width // 2 + 1, width, max(width - 3, 1)], dtype=np.int32)
+    shares = rng.dirichlet(np.full(width, 0.1), size=rows).astype(np.float32)
+    shares[4, : width // 3] = 0.25  # long runs of equal shares
+    for fraction, recent in ((0.2, 4), (0.5, 0), (0.8, 2)):
+        keep, summary = uniform_keep_rows(torch.from_numpy(shares).cuda(), torch.from_numpy(blocks).cuda(),
+                                          torch.ones(rows, dtype=torch.bool, device="cuda"), fraction,
+                                          recent_blocks=recent)
+        want, budget = oc.keep_rows(shares, blocks, np.ones(rows), fraction, recent, 0)
+        assert np.array_equal(keep.cpu().numpy(), want), (width, fraction)
+        assert int(summary[0]) == budget
+
+
 @pytest.mark.parametrize("recent", [0, 4])
 def test_view_build_config_full_size(recent):
     c = workloads.config4()

@@ -48,6 +48,20 @@ def test_random_batches_whole_rows():
         assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens)
 
 
+@pytest.mark.parametrize("width", [1, 63, 2048, 2049, 4097, 8192, 8193, 12288, 12289, 30001])
+def test_every_row_layout_width(width):
+    # the kernel keeps 4, 8, 16 or 24 entries per thread and goes by 12288-entry segments beyond
+    rng = np.random.default_rng(width)
+    rows = 5
+    table = rng.integers(0, 2**31 - 1, size=(rows, width), dtype=np.int64).astype(np.int32)
+    lens = np.array([0, 1, width * BLOCK, width * BLOCK + 100, max(width * BLOCK // 3, 1)], dtype=np.int32)
+    keep = rng.random((rows, width)) < np.array([0.5, 0.1, 0.9, 0.3, 0.5])[:, None]
+    view, view_lens = compact_block_table(torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(),
+                                          torch.from_numpy(keep).cuda(), BLOCK)
+    want_view, want_lens = obv.compact(table, lens, keep, BLOCK)
+    assert np.array_equal(view.cpu().numpy(), want_view) and np.array_equal(view_lens.cpu().numpy(), want_lens)
+
+
 def test_view_build_config_full_size():
     c = workloads.config4()
     rng = np.random.default_rng(44)
