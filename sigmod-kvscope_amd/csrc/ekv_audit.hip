@@ -404,7 +404,20 @@ struct MfmaShape {
   static constexpr int kSteps = HEAD_DIM / 32;                   // k-steps of 32 dims
   static constexpr int kLoads = kFp8 ? kSteps / 2 : kSteps;      // 16-byte key loads per M-tile
   static constexpr int kChunk = 32;                              // tokens per chunk: two M-tiles
+  static constexpr int kRowBytes = HEAD_DIM * kKBytes;           // one token's key row of one head
+  static constexpr int kPieces = kRowBytes / 16;                 // 16-byte pieces of a row
+  static constexpr int kTPI = kWave / kPieces;                   // whole rows per load instruction
+  static constexpr int kSwzDiv = kPieces >= 16 ? 1 : 16 / kPieces;
+  static constexpr int kSwzMask = (kPieces >= 16 ? 16 : kPieces) - 1;
+  static_assert(kTPI * kLoads == 16, "an M-tile is kLoads instructions of whole rows");
 };
+
+// LDS slot of piece pc of M-tile row t: the pieces of a row are permuted so that the 16 rows
+// an MFMA operand read takes at one piece index fall in 16 different 16-byte bank columns
+template <class S>
+__device__ __forceinline__ int tr_slot(int t, int pc) {
+  return t * S::kPieces + (pc ^ ((t / S::kSwzDiv) & S::kSwzMask));
+}
 
 template <int MODE>
 __device__ __forceinline__ f32x4_t mfma_step(const u32x4 a, const u32x4 b, f32x4_t c) {
@@ -430,6 +443,13 @@ __device__ __forceinline__ void widen_fp8(const u32x4 k, u32x4 &lo, u32x4 &hi) {
 
 // NT loads the keys with the nontemporal hint (they are read once).
 //
+// Loads.  A load instruction reads whole key rows (16 lanes x 16 bytes for a 256-byte row, 4
+// rows per instruction), the coalesced form: DRAM serves it at the streaming rate whatever the
+// head's offset in the token, where 64-byte pieces of 16 rows per instruction run up to 35%
+// slower for some heads.  The MFMA wants a token per lane instead, so each 16-row M-tile goes
+// through a per-wave LDS buffer (written in load order, read in operand order, both free of
+// bank conflicts by the slot permutation tr_slot).
+//
 // Per wave, two chunks are in flight.  A chunk's reduction is split: the MFMAs are the only
 // readers of the load buffer, so the next chunk's loads are issued right after them and the
 // softmax part overlaps with them.  The per-tile records are staged in LDS and written once per
@@ -446,27 +466,31 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
   extern __shared__ int s_mem[];  // [rows + 1] tile offsets, [rows] clipped lengths
   __shared__ int s_scan[kWaves];
   __shared__ float s_stage[kWaves][kStageFloats];
+  __shared__ u32x4 s_tr[kWaves][16 * S::kPieces];  // one M-tile of key rows per wave
   int *s_off = s_mem;
   int *s_len = s_mem + p.rows + 1;
-
-  if (*p.flag == 0u) return;  // the audit flag, runtime/audit_kernel.py:64
 
   const int rows = p.rows;
   const int bs = p.block_size;
   const int tile_tokens = kTileBlocks * bs;
 
   // ---- per-row live tiles: one read of select / lens, then a block scan ------------------
+  // the audit flag (runtime/audit_kernel.py:64) is read together with the rows' lengths, so
+  // that the prologue waits for memory once
+  const bool on = *p.flag != 0u;
+#pragma unroll 4
+  for (int r = threadIdx.x; r < rows; r += kThreads) {
+    const int len = min(max(p.lens[r], 0), p.width * bs);
+    s_len[r] = len;
+    s_off[r] = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
+  }
+  if (!on) return;
+  __syncthreads();
   const int per = (rows + kThreads - 1) / kThreads;
   const int r0 = threadIdx.x * per;
   const int r1 = min(r0 + per, rows);
   int local = 0;
-  for (int r = r0; r < r1; ++r) {
-    const int len = min(max(p.lens[r], 0), p.width * bs);
-    const int tiles = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
-    s_len[r] = len;
-    s_off[r] = tiles;
-    local += tiles;
-  }
+  for (int r = r0; r < r1; ++r) local += s_off[r];
   int total_tiles = 0;
   int base = block_exclusive_scan<kThreads>(local, s_scan, total_tiles);
   for (int r = r0; r < r1; ++r) {
@@ -484,6 +508,9 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
   const int nsub = p.nsub;   // chunks per tile
   const int G = p.group_rows;
   float *stage = s_stage[threadIdx.x / kWave];
+  u32x4 *tr = s_tr[threadIdx.x / kWave];
+  const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
+  const int piece = lane % S::kPieces;
   const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
   const long long all = (long long)total_tiles * p.groups;
   long long u = all * wave_id / nwaves;
@@ -521,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
         qb[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
       }
     }
-    const int64_t lane_off = (int64_t)n * p.k_stride_pos + (int64_t)g * p.k_stride_head + c * 16;
+    const int64_t lane_off = (int64_t)row_in * p.k_stride_pos + (int64_t)g * p.k_stride_head + piece * 16;
     float *cell_row = p.lse + (int64_t)row * p.row_stride + h * G;
     float m_run = -INFINITY, l_run = 0.0f;
 
@@ -539,29 +566,35 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
         const int id = __builtin_amdgcn_readlane(ids, (b < nblocks ? b : tile * kTileBlocks) - ids_base);
         const char *src = p.keys + (int64_t)id * p.k_stride_block + lane_off + (int64_t)(tpos % bs) * p.k_stride_pos;
 #pragma unroll
-        for (int s = 0; s < NLD; ++s) {
-          const u32x4 *at = (const u32x4 *)(src + 64 * s);
-          D[mt * NLD + s] = NT ? __builtin_nontemporal_load(at) : *at;
+        for (int j = 0; j < NLD; ++j) {  // rows j * TPI .. + TPI of the M-tile
+          const u32x4 *at = (const u32x4 *)(src + (int64_t)(j * S::kTPI) * p.k_stride_pos);
+          D[mt * NLD + j] = NT ? __builtin_nontemporal_load(at) : *at;
         }
       }
     };
 
     // the MFMAs of a chunk: scores of tokens 16 mt + 4 c + i for query row n in sc[4 mt + i]
-    auto mma_chunk = [&](const u32x4 (&D)[2 * NLD], f32x4_t (&acc)[2]) {
+    auto mma_chunk = [&](const u32x4 (&L)[2 * NLD], f32x4_t (&acc)[2]) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
+        // the M-tile through LDS: row n's piece 4 s + c is operand s of this lane
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) tr[tr_slot<S>(j * S::kTPI + row_in, piece)] = L[mt * NLD + j];
+        u32x4 D[NLD];
+#pragma unroll
+        for (int s = 0; s < NLD; ++s) D[s] = tr[tr_slot<S>(n, 4 * s + c)];
         acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (S::kFp8) {
 #pragma unroll
           for (int s = 0; s < NLD; ++s) {
             u32x4 lo4, hi4;
-            widen_fp8(D[mt * NLD + s], lo4, hi4);
+            widen_fp8(D[s], lo4, hi4);
             acc[mt] = mfma_step<kModeBF16>(lo4, qb[2 * s], acc[mt]);
             acc[mt] = mfma_step<kModeBF16>(hi4, qb[2 * s + 1], acc[mt]);
           }
         } else {
 #pragma unroll
-          for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[mt * NLD + s], qb[s], acc[mt]);
+          for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[s], qb[s], acc[mt]);
         }
       }
     };
