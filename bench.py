@@ -49,17 +49,85 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
-def audit_bytes(batch, audited_heads: int = 1) -> int:
+def audit_bytes(batch, audited_heads: int = 1, key_bytes: int = 2, query_bytes: int = 2) -> int:
     lens = batch.lens.astype("int64")
     n = batch.blocks.astype("int64")
     g, d = batch.group_rows, batch.head_dim
     return int(
-        lens.sum() * d * 2 * audited_heads
+        lens.sum() * d * key_bytes * audited_heads
         + n.sum() * 4
-        + batch.rows * g * audited_heads * d * 2
+        + batch.rows * g * audited_heads * d * query_bytes
         + batch.rows * 8
         + 2 * n.sum() * g * audited_heads * 4
     )
+
+
+def graph_launch_us(launches, count: int, reps: int) -> float:
+    """Mean duration (us) of one of the ``count`` launches that ``launches(stream)`` makes, from a
+    HIP graph of them replayed ``reps`` times and timed with events on the replay stream."""
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launches(int(torch.cuda.current_stream().cuda_stream))
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * count)
+
+
+def other_audit_shapes() -> dict:
+    """The audit kernel on the skewed long-context mix and on the 256-row fp8 full step (per-row
+    timer on): one KV group per launch, layers rotating over pools larger than the Infinity Cache."""
+    import numpy as np
+    import torch
+
+    import workloads
+    from runtime.audit_kernel import RecordingPlane
+
+    out = {}
+    # skewed mix: 8 rows of 131072 tokens + 120 Zipf(1.2) rows on [1024, 4096], bf16, 2 pools
+    b3 = workloads.config3_batch()
+    pools = [workloads.device_pool(b3, torch.bfloat16, seed=b3.seed + i) for i in range(2)]
+    q3 = torch.from_numpy(workloads.queries(b3, 8)).to(torch.bfloat16).cuda()
+    plane = RecordingPlane(8, b3.rows, b3.width, b3.group_rows, b3.block_size)
+    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    plane.select(np.ones(b3.rows, bool), np.arange(b3.rows))
+    t3, l3 = torch.from_numpy(b3.table).cuda(), torch.from_numpy(b3.lens).cuda()
+    us = graph_launch_us(lambda s: [plane.launch(layer, t3, l3, q3[layer], pools[layer % 2][:, 0],
+                                                 b3.head_dim ** -0.5, stream=s) for layer in range(8)], 8, 10)
+    bytes3 = audit_bytes(b3)
+    out["skewed_long_context_bf16"] = {"bytes_per_launch": bytes3, "us": round(us, 2),
+                                       "gbs": round(bytes3 / us / 1e3, 1), "frac": round(bytes3 / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del pools, q3, plane
+    torch.cuda.empty_cache()
+    # full step: 256 rows of U[2048, 32768] tokens, block 32, fp8 keys with a per-tensor scale, 32 layers
+    b5 = workloads.config5_batch()
+    fp8 = torch.float8_e4m3fn
+    pools = [workloads.device_pool(b5, fp8, seed=b5.seed + i) for i in range(2)]
+    q5 = torch.from_numpy(workloads.queries(b5, LAYERS)).to(torch.bfloat16).cuda()
+    plane = RecordingPlane(LAYERS, b5.rows, b5.width, b5.group_rows, b5.block_size, timer=True)
+    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    plane.select(np.ones(b5.rows, bool), np.arange(b5.rows))
+    t5, l5 = torch.from_numpy(b5.table).cuda(), torch.from_numpy(b5.lens).cuda()
+    k_scale = b5.extra["k_scale"]
+    us = graph_launch_us(lambda s: [plane.launch(layer, t5, l5, q5[layer], pools[layer % 2][:, 0],
+                                                 b5.head_dim ** -0.5, k_scale=k_scale, stream=s)
+                                    for layer in range(LAYERS)], LAYERS, 5)
+    bytes5 = audit_bytes(b5, key_bytes=1)
+    out["full_step_fp8_256_rows"] = {"bytes_per_launch": bytes5, "us_per_layer": round(us, 2),
+                                     "ms_per_step": round(us * LAYERS / 1e3, 3), "gbs": round(bytes5 / us / 1e3, 1),
+                                     "frac": round(bytes5 / us / 1e3 / HBM_PEAK_GBS, 4), "timer": True}
+    del pools, q5, plane
+    torch.cuda.empty_cache()
+    return out
 
 
 class Step:
@@ -362,6 +430,7 @@ def main() -> None:
     c4_rank_ms = float(np.median(time_events(rank_c4, 20, stream)))
     c4_compact_ms = float(np.median(time_events(compact_c4, 20, stream)))
 
+    others = other_audit_shapes()
     peak = copy_peak_gbs()
     traffic = profiled_traffic()
     out = {
@@ -407,6 +476,7 @@ def main() -> None:
         },
         "every_kv_head_audit": {"bytes_per_launch": audit_bytes(batch, batch.kv_heads), "us": round(all_ms * 1e3, 2),
                                 "gbs": round(all_gbs, 1), "frac": round(all_gbs / HBM_PEAK_GBS, 4)},
+        "other_audit_shapes": others,
         "view_build_us": {"llama3_step_128_rows": round(view_ms * 1e3, 2),
                           "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2),
                           "config_1024x8192_rank": round(c4_rank_ms * 1e3, 2),

@@ -103,7 +103,10 @@ def call(name: str, *args) -> None:
 
 
 def stream_handle(stream=None) -> int:
-    """The raw hipStream_t of ``stream`` (default: torch's current stream on the current device)."""
+    """The raw hipStream_t of ``stream``: a torch stream, a raw handle (int) as is, or by default
+    torch's current stream on the current device."""
+    if isinstance(stream, int):
+        return stream
     import torch
 
     s = torch.cuda.current_stream() if stream is None else stream

@@ -138,26 +138,63 @@ def test_every_kv_head_mode():
 
 
 def test_long_rows_with_heavy_hitters():
+    # the whole skewed mix: 8 rows of 131072 tokens and 120 Zipf rows, 0.5% planted heavy hitters
     batch = workloads.config3_batch()
-    long_rows = [r for r in range(batch.rows) if batch.lens[r] == 131072][:2]
-    short_rows = [r for r in range(batch.rows) if batch.lens[r] != 131072][:6]
-    rows = sorted(long_rows + short_rows)
     pool = workloads.device_pool(batch, torch.bfloat16, seed=batch.seed)
     q = torch.from_numpy(workloads.queries(batch, 1)[0]).to(torch.bfloat16).cuda()
     workloads.plant_heavy_hitters(batch, pool, q)
-    select = np.zeros(batch.rows, bool)
-    select[rows] = True
     plane = RecordingPlane(1, batch.rows, batch.width, batch.group_rows, batch.block_size)
     flag(plane)
     scale = batch.head_dim ** -0.5
     got = record(plane, 0, torch.from_numpy(batch.table).cuda(), torch.from_numpy(batch.lens).cuda(), q,
-                 pool[:, 0], scale, select=select)
-    keys, table = workloads.host_keys(batch, pool, rows=rows, heads=[0])
+                 pool[:, 0], scale)
+    keys, table = workloads.host_keys(batch, pool, heads=[0])
+    del pool
+    torch.cuda.empty_cache()
     want = oa.new_planes(1, batch.rows, batch.width, batch.group_rows)
-    oa.tile_lse(want, q.float().cpu().numpy(), keys, table, batch.lens, np.arange(batch.rows), select, 1, 0, scale,
+    every = np.ones(batch.rows)
+    oa.tile_lse(want, q.float().cpu().numpy(), keys, table, batch.lens, np.arange(batch.rows), every, 1, 0, scale,
                 batch.block_size, batch.group_rows, [0], key_heads=[0])
     assert_parity(got, want, "long rows + heavy hitters")
-    del pool
+
+
+def test_full_step_fp8_with_timer():
+    # the 256-row full step: 32 layers over two fp8 pools (block 32, a per-tensor scale), the per-row
+    # timer on.  Every layer writes exactly the cells of the rows' blocks, two layers match the oracle
+    # in full, and every row's cycle counter grows with every step.
+    batch = workloads.config5_batch()
+    layers, rows, G, bs = 32, batch.rows, batch.group_rows, batch.block_size
+    fp8 = torch.float8_e4m3fn
+    k_scale = batch.extra["k_scale"]
+    pools = [workloads.device_pool(batch, fp8, seed=batch.seed + i) for i in range(2)]
+    q = torch.from_numpy(workloads.queries(batch, layers)).to(torch.bfloat16).cuda()
+    plane = RecordingPlane(layers, rows, batch.width, G, bs, timer=True)
+    flag(plane)
+    plane.select(np.ones(rows, bool), np.arange(rows))
+    table, lens = torch.from_numpy(batch.table).cuda(), torch.from_numpy(batch.lens).cuda()
+    scale = batch.head_dim ** -0.5
+
+    def step():
+        for layer in range(layers):
+            plane.launch(layer, table, lens, q[layer], pools[layer % 2][:, 0], scale, k_scale=k_scale)
+        torch.cuda.synchronize()
+
+    step()
+    first = plane.read_cycles()
+    step()
+    second = plane.read_cycles()
+    assert (first[:rows] > 0).all() and (second[:rows] > first[:rows]).all(), "a row's cycles did not grow"
+    got = plane.read_planes()
+    written = np.arange(batch.width)[None, :] < batch.blocks[:, None]  # [rows, width]
+    for layer in range(layers):
+        assert np.array_equal(~np.isnan(got[0, layer]), np.repeat(written[:, :, None], G, axis=2)), layer
+    for layer in (0, 13):
+        keys, table_c = workloads.host_keys(batch, pools[layer % 2], heads=[layer % batch.kv_heads])
+        want = oa.new_planes(1, rows, batch.width, G)
+        oa.tile_lse(want, q[layer].float().cpu().numpy(), keys, table_c, batch.lens, np.arange(rows), np.ones(rows),
+                    1, 0, scale, bs, G, [layer % batch.kv_heads], k_scale=k_scale, key_heads=[0])
+        assert_parity(got[:, layer : layer + 1], want, f"fp8 full step, layer {layer}")
+    del pools
     torch.cuda.empty_cache()
 
 
