@@ -183,6 +183,30 @@ int ekv_build_view(const int32_t *table, int64_t table_stride, const int32_t *se
                    void *stream);
 
 /*
+ * SGLang's key-value index list compaction, the token-granular form of the view.
+ * Replaces plan_kernel, gather_kernel and SlotCompactor.compact, runtime/sglang_compact.py:22-167.
+ *
+ * Request r reads slots[indptr[r] .. indptr[r + 1]) (int32 offsets, slots of slot_bytes = 4 or
+ * 8 bytes).  Each block_tokens consecutive entries form a block.  Row r keeps block b when
+ *     b < blocks_r and (b == 0 or b == blocks_r - 1 or whole_r or (r < n_real and keep[r][b]))
+ * with whole_r = !active or r >= n_real or (audit != NULL and r < n_real and audit[r]); a row
+ * has at most `width` blocks.  The call writes table[r][k] (the k-th kept block), lens[r] (the
+ * new length: kept blocks times block_tokens less the unfilled part of the last block, 0 for an
+ * empty row), new_indptr[0 .. n_rows] (their running sum) and out[0 .. new_indptr[n_rows]) (the
+ * kept entries in order), and adds to counts[0..4] (when non-NULL) the real rows' blocks read,
+ * blocks a full read would read, blocks read by audited rows, blocks read by rows that kept every
+ * token while the policy is live, and blocks read while it is not.  `entries` is indptr[n_rows],
+ * which the host knows.  With write_back, new_indptr is copied into indptr and the new list into
+ * slots[0 .. new total) in place (entries past the new total keep their old values).  No host
+ * synchronisation; n_rows <= 6000.
+ */
+int ekv_compact_slots(int32_t *indptr, void *slots, int32_t slot_bytes, const uint8_t *keep,
+                      int64_t keep_stride, const uint8_t *audit, int32_t active, int32_t n_real,
+                      int32_t n_rows, int32_t width, int32_t block_tokens, int64_t entries,
+                      int32_t *new_indptr, int32_t *lens, int32_t *table, int64_t table_stride,
+                      void *out, int64_t *counts, int32_t write_back, void *stream);
+
+/*
  * Device memory, copies and IPC for the statistic planes.  They replace the ctypes calls
  * into libcudart of runtime/audit.py:17-23, :55-60, runtime/audit_kernel.py:146-158 and
  * observe/cuda.py:12-58.  These are not for hot loops.

@@ -51,6 +51,9 @@ _SIGNATURES: dict[str, list] = {
     "ekv_build_view": [
         _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p,
     ],
+    "ekv_compact_slots": [
+        _p, _p, _i32, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _p, _p, _i32, _p,
+    ],
     "ekv_malloc": [ctypes.POINTER(ctypes.c_void_p), _sz],
     "ekv_free": [_p],
     "ekv_memset": [_p, ctypes.c_int, _sz],
