@@ -155,6 +155,25 @@ int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_
                         int32_t *workspace, void *stream);
 
 /*
+ * The `sum` budget split: allocate(requests, budget, "sum"), observe/allocation.py:55-123.
+ *
+ * Row r is a request of blocks[r] blocks (at most width) with float64 scores, weight weights[r]
+ * (NULL: 1.0) and pinned blocks pinned[r][b] (NULL: the first and the last).  Its shares are
+ * max(s, 0) / total (NumPy's float64 sum, reproduced in its order) or 1 / n when total <= 0.  The
+ * call keeps every pinned block and the free = budget - pinned unpinned blocks of highest
+ * weight * share, ties to the newer block, then the earlier request; every block when budget >=
+ * the blocks of all rows.  keep[r][b] is 1 or 0, and 1 past the row's blocks.  summary (int64[6],
+ * may be NULL): budget, blocks of all rows, pinned blocks, status (1: the budget is below the
+ * pinned blocks -- the reference raises ValueError -- and every block is kept), requests, free.
+ * workspace: ekv_rank_sum_workspace(rows) bytes of device memory the call may overwrite.
+ */
+size_t ekv_rank_sum_workspace(int32_t rows);
+int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blocks, const double *weights,
+                 const uint8_t *pinned, int64_t pinned_stride, int32_t rows, int32_t width, int64_t budget,
+                 uint8_t *keep, int64_t keep_stride, int64_t *summary, void *workspace, size_t workspace_bytes,
+                 void *stream);
+
+/*
  * compact_block_table (runtime/block_view.py:36-56).
  * keep'[r, b] = (keep[r, b] | b == 0 | b == n-1) & b < n,  n = ceil(seq_lens[r] / block_size).
  * view_table row r = table row r stably partitioned: keep' entries first, the rest after them,

@@ -51,6 +51,8 @@ _SIGNATURES: dict[str, list] = {
     "ekv_build_view": [
         _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p,
     ],
+    "ekv_rank_sum_workspace": [_i32],
+    "ekv_rank_sum": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p, _sz, _p],
     "ekv_compact_slots": [
         _p, _p, _i32, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _p, _p, _i32, _p,
     ],
@@ -81,7 +83,12 @@ def load() -> ctypes.CDLL:
     for name, args in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_char_p if name == "ekv_last_error" else ctypes.c_int
+        if name == "ekv_last_error":
+            fn.restype = ctypes.c_char_p
+        elif name.endswith("_workspace"):
+            fn.restype = ctypes.c_size_t
+        else:
+            fn.restype = ctypes.c_int
     _lib = lib
     return lib
 

@@ -3,9 +3,11 @@
 Each request scores each of its blocks by the share of its attention on the block.  ``uniform``
 gives every request the same fraction of its unpinned blocks, each ranked by its own shares:
 the free budget is split by largest remainder in IEEE double and each request keeps its quota of
-open blocks by (share descending, block index ascending).  The split and the ranking run on the
-GPU (``ekv_rank_uniform``); pinned blocks (by default the first and the last) always count
-against the budget, and a budget below them is an error.
+open blocks by (share descending, block index ascending) (``ekv_rank_uniform``).  ``sum`` keeps the
+free budget's unpinned blocks of highest weight * share over all requests, a tie going to the newer
+block, then the earlier request (``ekv_rank_sum``, float64 shares with NumPy's totals).  Pinned
+blocks (by default the first and the last) always count against the budget, and a budget below
+them is an error.
 
 The device ranks float32 shares.  For float32 scores that order is exactly the reference's stable
 argsort of the float64 ``shares()``; float64 scores are rounded to float32 first.
@@ -68,9 +70,75 @@ def allocate(requests: Sequence[Request], budget: int, objective: Objective = "s
         raise ValueError(f"the {objective} objective does not use request weights")
     if objective == "uniform":
         return _uniform_on_device(requests, pinned, budget)
-    if objective in ("sum", "maxmin"):
+    if objective == "sum":
+        return _sum_on_device(requests, pinned, budget)
+    if objective == "maxmin":
         raise NotImplementedError(f"the {objective} objective has no device implementation in this build")
     raise ValueError(f"unknown objective {objective!r}")
+
+
+def _padded(requests: Sequence[Request], pinned: list[np.ndarray]):
+    """Scores (float64), pins and block counts of the requests as [rows, width] device tensors."""
+    rows = len(requests)
+    sizes = [len(r.scores) for r in requests]
+    width = max(max(sizes, default=1), 1)
+    scores = np.zeros((rows, width), dtype=np.float64)
+    pins = np.zeros((rows, width), dtype=np.uint8)
+    for i, (req, pin) in enumerate(zip(requests, pinned)):
+        scores[i, : sizes[i]] = np.asarray(req.scores, dtype=np.float64)
+        pins[i, : sizes[i]] = pin
+    return (torch.from_numpy(scores).cuda(), torch.from_numpy(pins).cuda(),
+            torch.tensor(sizes, dtype=torch.int32).cuda(), sizes)
+
+
+def _sum_on_device(requests: Sequence[Request], pinned: list[np.ndarray], budget: int) -> list[np.ndarray]:
+    scores, pins, blocks, sizes = _padded(requests, pinned)
+    weights = torch.tensor([float(r.weight) for r in requests], dtype=torch.float64).cuda()
+    keep = sum_keep(scores, blocks, weights=weights, pinned=pins, budget=budget)[0].cpu().numpy()
+    return [keep[i, : sizes[i]].astype(bool) for i in range(len(requests))]
+
+
+def sum_keep(
+    scores: torch.Tensor,
+    blocks: torch.Tensor,
+    *,
+    budget: int,
+    weights: torch.Tensor | None = None,
+    pinned: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The ``sum`` keep mask ``uint8[rows, width]`` on the device (observe/allocation.py:94-123) and
+    the int64 summary (budget, blocks, pinned, status, requests, free).
+
+    ``scores`` float64 [rows, width] (float32 is widened, exactly); ``blocks`` int32 [rows];
+    ``weights`` float64 [rows] (default 1.0); ``pinned`` a uint8 / bool mask (default: the first
+    and the last block of each row)."""
+    if scores.dtype == torch.float32:
+        scores = scores.double()
+    if scores.dtype != torch.float64 or scores.stride(1) != 1:
+        raise ValueError("scores must be float64 (or float32) with contiguous rows")
+    rows, width = int(scores.shape[0]), int(scores.shape[1])
+    if blocks.dtype != torch.int32 or blocks.shape != (rows,):
+        raise ValueError("blocks must be int32 [rows]")
+    if weights is not None and (weights.dtype != torch.float64 or weights.shape != (rows,)):
+        raise ValueError("weights must be float64 [rows]")
+    if pinned is not None and (pinned.dtype not in (torch.uint8, torch.bool) or pinned.stride(-1) != 1):
+        raise ValueError("pinned must be a uint8 / bool mask with contiguous rows")
+    if budget < 0:
+        raise ValueError("the budget cannot be negative")
+    if out is None:
+        out = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
+    summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
+    need = int(ekv_hip.load().ekv_rank_sum_workspace(rows))
+    workspace = torch.empty(need, dtype=torch.uint8, device=scores.device)
+    ekv_hip.call(
+        "ekv_rank_sum", scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(weights),
+        ekv_hip.ptr(pinned), pinned.stride(0) if pinned is not None else 0, rows, width, int(budget),
+        out.data_ptr(), out.stride(0), summary.data_ptr(), workspace.data_ptr(), need,
+        ekv_hip.stream_handle(stream),
+    )
+    return out, summary
 
 
 def _uniform_on_device(requests: Sequence[Request], pinned: list[np.ndarray], budget: int) -> list[np.ndarray]:

@@ -11,7 +11,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 
 def declared() -> set[str]:
     text = open(HEADER).read()
-    return set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s*(ekv_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s*(ekv_\w+)\s*\(", text, re.M))
 
 
 def test_header_declares_the_hot_path():

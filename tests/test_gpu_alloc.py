@@ -1,0 +1,89 @@
+"""GPU `sum` split (ekv_rank_sum through allocate and sum_keep) bit-exact against the oracle:
+the reference test's tied integer scores with weights, explicit pins, float64 scores, rows past
+NumPy's 8192-value reduction run, and the view-build configuration at full size
+(observe/allocation.py:55-123 and tests/test_allocation.py:170-250 of the reference)."""
+
+import numpy as np
+import pytest
+import torch
+
+import workloads
+from cases import random_requests
+from observe import allocation
+from oracle import allocation as oa
+
+pytestmark = pytest.mark.gpu
+
+
+def same(got, want):
+    return len(got) == len(want) and all(np.array_equal(a, b) for a, b in zip(got, want))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_sum_with_ties_and_weights(seed):
+    rng = np.random.default_rng(seed)
+    reqs = []
+    for _ in range(int(rng.integers(1, 9))):
+        n = int(rng.integers(3, 40))
+        scores = rng.integers(0, 4, size=n).astype(float)  # many equal scores, so many ties
+        reqs.append(allocation.Request(scores=scores, weight=float(rng.choice([1.0, 2.0, 0.5]))))
+    total = sum(len(r.scores) for r in reqs)
+    must = sum(int(r.pinned_mask().sum()) for r in reqs)
+    budget = int(rng.integers(must, max(total, must + 1)))
+    got = allocation.allocate(reqs, budget, "sum")
+    want = oa.allocate_sum([r.scores for r in reqs], [r.pinned_mask() for r in reqs], [r.weight for r in reqs], budget)
+    assert same(got, want)
+
+
+def test_sum_float64_scores_and_explicit_pins():
+    rng = np.random.default_rng(3)
+    for trial in range(60):
+        scores, pinned = random_requests(rng, int(rng.integers(1, 7)), 50, ties=trial % 2 == 0)
+        scores = [s.astype(np.float64) * (1 + 1e-9 * rng.random(len(s))) for s in scores]  # not float32 values
+        weights = [float(rng.choice([1.0, 3.0, 0.25])) for _ in scores]
+        total = sum(len(s) for s in scores)
+        must = sum(int(p.sum()) for p in pinned)
+        budget = int(rng.integers(must, max(total, must + 1)))
+        reqs = [allocation.Request(scores=s, weight=w, pinned=p) for s, w, p in zip(scores, weights, pinned)]
+        assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, weights, budget)), trial
+
+
+def test_sum_rows_past_one_reduction_run():
+    # rows of more than 8192 blocks: NumPy's total adds two runs' pairwise sums
+    rng = np.random.default_rng(8)
+    scores = [rng.random(n) * rng.choice([1e-3, 1.0, 7.0]) for n in (8191, 8192, 8193, 12288, 9000)]
+    pinned = [oa.default_pins(len(s)) for s in scores]
+    weights = [1.0, 2.0, 0.5, 1.0, 1.5]
+    total = sum(len(s) for s in scores)
+    for frac in (0.1, 0.5, 0.9):
+        budget = int(frac * total)
+        reqs = [allocation.Request(scores=s, weight=w) for s, w in zip(scores, weights)]
+        assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, weights, budget)), frac
+
+
+def test_sum_view_build_configuration():
+    # 1024 rows of U[1, 8192] blocks with Dirichlet(0.1) float32 shares: budgets 0.2 / 0.5 / 0.8
+    c = workloads.config4()
+    shares, blocks = c["shares"], c["blocks"]
+    sizes = blocks.tolist()
+    total = int(blocks.sum())
+    scores = [shares[r, : sizes[r]] for r in range(len(sizes))]
+    pinned = [oa.default_pins(n) for n in sizes]
+    s_dev, b_dev = torch.from_numpy(shares).cuda(), torch.from_numpy(blocks).cuda()
+    for frac in (0.2, 0.5, 0.8):
+        budget = int(np.ceil(frac * total))
+        keep, summary = allocation.sum_keep(s_dev, b_dev, budget=budget)
+        got = keep.cpu().numpy()
+        want = oa.allocate_sum(scores, pinned, [1.0] * len(sizes), budget)
+        bad = sum(int((got[r, : sizes[r]].astype(bool) != want[r]).sum()) for r in range(len(sizes)))
+        print(f"sum at {frac}: budget {budget}, kept {sum(int(w.sum()) for w in want)}, mismatched {bad}", flush=True)
+        assert bad == 0 and int(summary[0]) == budget and int(summary[3]) == 0
+
+
+def test_sum_summary_flags_a_budget_below_the_pins():
+    scores = torch.ones(2, 5, dtype=torch.float64, device="cuda")
+    blocks = torch.tensor([5, 5], dtype=torch.int32, device="cuda")
+    keep, summary = allocation.sum_keep(scores, blocks, budget=3)  # 4 pinned blocks
+    assert int(summary[3]) == 1 and int(summary[2]) == 4
+    with pytest.raises(ValueError):
+        allocation.allocate([allocation.Request(scores=np.ones(5))] * 2, 3, "sum")

@@ -91,3 +91,125 @@ def test_float32_scores_rank_like_their_float64_shares():
         ref = np.argsort(-oa.shares(s), kind="stable")
         key = np.lexsort((np.arange(n), -np.maximum(s, 0).astype(np.float64)))
         assert np.array_equal(ref, key)
+
+
+# ---- sum and maxmin --------------------------------------------------------------------------
+
+def plain_sum(scores, pinned, weights, budget):
+    """Every unpinned block sorted by weighted share, newer blocks first on ties, then earlier requests."""
+    kept = [p.copy() for p in pinned]
+    cells = [(w * oa.shares(s)[b], b, i) for i, (s, p, w) in enumerate(zip(scores, pinned, weights))
+             for b in np.flatnonzero(~p)]
+    cells.sort(key=lambda c: (-c[0], -c[1], c[2]))
+    for _gain, b, i in cells[: budget - sum(int(p.sum()) for p in pinned)]:
+        kept[i][b] = True
+    return kept
+
+
+def plain_maxmin(scores, pinned, budget):
+    """The level bisected with one search per request, then the rest spent on the lowest request."""
+    sh = [oa.shares(s) for s in scores]
+    order = [np.flatnonzero(~p)[np.argsort(-sh[i][~p], kind="stable")] for i, p in enumerate(pinned)]
+    base = [float(sh[i][p].sum()) for i, p in enumerate(pinned)]
+    prefix = [np.cumsum(sh[i][order[i]]) for i in range(len(scores))]
+    free = budget - sum(int(p.sum()) for p in pinned)
+
+    def counts_at(level):
+        out = []
+        for i in range(len(scores)):
+            need = level - base[i]
+            out.append(0 if need <= 1e-12 else min(int(np.searchsorted(prefix[i], need - 1e-12)) + 1, len(order[i])))
+        return out
+
+    low, high = 0.0, 1.0
+    for _ in range(60):
+        mid = (low + high) / 2
+        if sum(counts_at(mid)) <= free:
+            low = mid
+        else:
+            high = mid
+    counts = counts_at(low)
+    kept = [p.copy() for p in pinned]
+    for i, k in enumerate(counts):
+        kept[i][order[i][:k]] = True
+    leftover = free - sum(counts)
+    while leftover > 0:
+        open_rows = [i for i in range(len(scores)) if counts[i] < len(order[i])]
+        if not open_rows:
+            break
+        i = min(open_rows, key=lambda r: (base[r] + (float(prefix[r][counts[r] - 1]) if counts[r] else 0.0), r))
+        kept[i][order[i][counts[i]]] = True
+        counts[i] += 1
+        leftover -= 1
+    return kept
+
+
+def sum_case(rng, requests):
+    scores, weights, pinned = [], [], []
+    for _ in range(requests):
+        n = int(rng.integers(3, 40))
+        scores.append(rng.integers(0, 4, size=n).astype(float))  # many equal scores, so many ties
+        weights.append(float(rng.choice([1.0, 2.0, 0.5])))
+        pinned.append(pins(n))
+    total = sum(len(s) for s in scores)
+    must = sum(int(p.sum()) for p in pinned)
+    return scores, weights, pinned, int(rng.integers(must, max(total, must + 1)))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_sum_equals_the_plain_sort_including_ties(seed):
+    rng = np.random.default_rng(seed)
+    scores, weights, pinned, budget = sum_case(rng, int(rng.integers(1, 9)))
+    got, want = oa.allocate_sum(scores, pinned, weights, budget), plain_sum(scores, pinned, weights, budget)
+    assert all(np.array_equal(a, b) for a, b in zip(got, want))
+
+
+def test_sum_maximises_the_weighted_share_by_brute_force():
+    rng = np.random.default_rng(5)
+    for _ in range(40):
+        scores, pinned = random_requests(rng, 3, 6, ties=bool(rng.random() < 0.5))
+        weights = [float(rng.choice([1.0, 2.0, 0.5])) for _ in scores]
+        total = sum(len(s) for s in scores)
+        must = sum(int(p.sum()) for p in pinned)
+        budget = int(rng.integers(must, total + 1))
+        kept = oa.allocate_sum(scores, pinned, weights, budget)
+        cells = [(w * oa.shares(s)[b]) for s, p, w in zip(scores, pinned, weights) for b in np.flatnonzero(~p)]
+        free = min(budget - must, len(cells))
+        best = max((sum(c) for c in itertools.combinations(cells, free)), default=0.0)
+        got = sum(w * oa.shares(s)[b] for s, p, w, k in zip(scores, pinned, weights, kept) for b in np.flatnonzero(~p & k))
+        assert sum(int(k.sum()) for k in kept) == min(budget, total)
+        assert got >= best - 1e-12
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_maxmin_equals_the_plain_search(seed):
+    rng = np.random.default_rng(seed)
+    scores, pinned = random_requests(rng, int(rng.integers(1, 9)), 40)
+    total = sum(len(s) for s in scores)
+    must = sum(int(p.sum()) for p in pinned)
+    budget = int(rng.integers(must, max(total, must + 1)))
+    got, want = oa.allocate_maxmin(scores, pinned, budget), plain_maxmin(scores, pinned, budget)
+    assert all(np.array_equal(a, b) for a, b in zip(got, want))
+
+
+def test_maxmin_raises_the_lowest_share_by_brute_force():
+    # the smallest retained share is the largest any split of the budget reaches
+    rng = np.random.default_rng(9)
+    for _ in range(30):
+        scores = [rng.dirichlet(np.full(int(rng.integers(3, 6)), 0.5)) for _ in range(3)]
+        pinned = [pins(len(s)) for s in scores]
+        total = sum(len(s) for s in scores)
+        must = sum(int(p.sum()) for p in pinned)
+        budget = int(rng.integers(must, total + 1))
+        kept = oa.allocate_maxmin(scores, pinned, budget)
+        got = min(float(oa.shares(s)[k].sum()) for s, k in zip(scores, kept))
+        best = 0.0
+        opened = [np.flatnonzero(~p) for p in pinned]
+        free = budget - must
+        for split in itertools.product(*[range(len(o) + 1) for o in opened]):
+            if sum(split) > free:
+                continue
+            level = min(float(oa.shares(s)[p].sum()) + np.sort(oa.shares(s)[o])[::-1][:k].sum()
+                        for s, p, o, k in zip(scores, pinned, opened, split))
+            best = max(best, level)
+        assert got >= best - 1e-9
