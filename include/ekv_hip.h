@@ -174,6 +174,19 @@ int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blo
                  void *stream);
 
 /*
+ * The `maxmin` budget split: allocate(requests, budget, "maxmin"), observe/allocation.py:55-76 and
+ * :126-166.  Rows, shares, pins, keep and summary as ekv_rank_sum (no weights).  The call raises
+ * the lowest retained share (pinned shares plus the kept open blocks, each request's open blocks
+ * taken in stable descending share order) by the reference's 60-step bisection of the level, then
+ * gives the leftover one block at a time to the request of the lowest (retained share, index).
+ * rows <= 8192.  workspace: ekv_rank_maxmin_workspace(rows, width) bytes of device memory.
+ */
+size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width);
+int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *blocks, const uint8_t *pinned,
+                    int64_t pinned_stride, int32_t rows, int32_t width, int64_t budget, uint8_t *keep,
+                    int64_t keep_stride, int64_t *summary, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * compact_block_table (runtime/block_view.py:36-56).
  * keep'[r, b] = (keep[r, b] | b == 0 | b == n-1) & b < n,  n = ceil(seq_lens[r] / block_size).
  * view_table row r = table row r stably partitioned: keep' entries first, the rest after them,

@@ -16,9 +16,22 @@
 // recomputed in each pass), then among the blocks at the threshold by a select over
 // (block desc, request asc) (four passes).  All state lives in a caller-provided workspace that a
 // kernel clears first, so the launches need no host synchronisation and no memset.
+//
+// maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
+// the lowest request first (observe/allocation.py:126-166).  Per request: the pinned shares' NumPy
+// sum (base), its open blocks in stable descending share order (a segmented radix sort over the
+// same order-preserving keys) and their running float64 totals, added in that order as
+// np.cumsum does.  The 60-step bisection of the level runs in one workgroup: a request's count at
+// a level is min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the
+// shifted-by-2r comparison NumPy's single search makes, and every request keeps the bracket of
+// positions its count can still take, so later steps search a few entries.  The leftover goes one
+// block at a time to the request of the lowest (retained, index), found by a workgroup argmin.
 #pragma clang fp contract(off)
 
+#include <limits.h>
 #include <math.h>
+
+#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "ekv_common.hpp"
 
@@ -343,6 +356,223 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
   }
 }
 
+// ---- maxmin --------------------------------------------------------------------------------
+constexpr int kBisectThreads = 1024;
+constexpr int kRowsPerThread = 8;  // rows a bisection thread keeps in registers
+constexpr int kMaxMaxminRows = kBisectThreads * kRowsPerThread;
+
+struct MaxminRow {
+  double base;  // NumPy's sum of the pinned shares
+  int open, counts;
+};
+
+struct MaxminParams {
+  Params p;
+  MaxminRow *mrow;
+  unsigned long long *keys_in, *keys_out;
+  int32_t *vals_in, *vals_out;
+  double *prefix;
+  int32_t *offsets;
+};
+
+// per request, one wave: the base, the sort keys of the open blocks (0 elsewhere), the offsets
+__global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
+  __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
+  __shared__ double s_leaf[kMaxLeaves];
+  __shared__ unsigned short s_pin[kMaxWidth];  // the pinned blocks, in order
+  const Params &p = m.p;
+  const int r = blockIdx.x;
+  const int lane = lane_id();
+  const RowStat st = p.row_stat[r];
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int npin = 0;
+  for (int b0 = 0; b0 < st.n; b0 += kWave) {
+    const int b = b0 + lane;
+    const bool pin = b < st.n && pinned_at(p, r, b, st.n);
+    const uint64_t mask = __ballot(pin);
+    if (pin) s_pin[npin + __popcll(mask & below)] = (unsigned short)b;
+    npin += __popcll(mask);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const double base = numpy_sum([&](int k) { return share_of(p, st, r, s_pin[k]); }, npin, s_start, s_len, s_leaf);
+  const int64_t row0 = (int64_t)r * p.width;
+  for (int b = lane; b < p.width; b += kWave) {
+    unsigned long long key = 0ull;
+    if (b < st.n && !pinned_at(p, r, b, st.n)) key = gain_key(share_of(p, st, r, b));
+    m.keys_in[row0 + b] = key;
+    m.vals_in[row0 + b] = b;
+  }
+  if (lane == 0) {
+    MaxminRow mr;
+    mr.base = base;
+    mr.open = st.open;
+    mr.counts = 0;
+    m.mrow[r] = mr;
+    m.offsets[r] = (int32_t)row0;
+    if (r == p.rows - 1) m.offsets[p.rows] = (int32_t)(row0 + p.width);
+  }
+}
+
+// per request, one thread: the running totals of the open shares in sorted order (np.cumsum)
+__global__ __launch_bounds__(kThreads) void mm_prefix_kernel(const MaxminParams m) {
+  const Params &p = m.p;
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= p.rows) return;
+  const RowStat st = p.row_stat[r];
+  const int open = st.open;
+  const int64_t row0 = (int64_t)r * p.width;
+  double acc = 0.0;
+  for (int i0 = 0; i0 < open; i0 += 8) {
+    double v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = i0 + k < open ? share_of(p, st, r, m.vals_out[row0 + i0 + k]) : 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (i0 + k >= open) break;
+      acc = (i0 + k == 0) ? v[k] : acc + v[k];
+      m.prefix[row0 + i0 + k] = acc;
+    }
+  }
+}
+
+// the level's bisection and the leftover, one workgroup
+__global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminParams m) {
+  __shared__ long long s_red[kBisectThreads / kWave];
+  __shared__ double s_best[kBisectThreads / kWave];
+  __shared__ int s_best_row[kBisectThreads / kWave];
+  const Params &p = m.p;
+  const State *s = p.state;
+  if (s->mode != kSelect || s->error) return;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const long long free_blocks = s->free_blocks;
+  double base[kRowsPerThread];
+  int open[kRowsPerThread], lo[kRowsPerThread], hi[kRowsPerThread], mid_pos[kRowsPerThread];
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int r = tid + j * kBisectThreads;
+    const bool in = r < p.rows;
+    base[j] = in ? m.mrow[r].base : 0.0;
+    open[j] = in ? m.mrow[r].open : 0;
+    lo[j] = 0;
+    hi[j] = open[j];
+  }
+  // count of request r at a level: its position among its shifted totals, from the bracket
+  auto count_at = [&](int j, double level, int &pos) -> int {
+    const int r = tid + j * kBisectThreads;
+    const double need = level - base[j];
+    const double shift = 2.0 * (double)r;
+    const double q = (need - 1e-12) + shift;
+    const double *pre = m.prefix + (int64_t)r * p.width;
+    int a = lo[j], b = hi[j];
+    while (a < b) {  // first position whose shifted total is >= q
+      const int c = (a + b) >> 1;
+      if (pre[c] + shift < q) a = c + 1; else b = c;
+    }
+    pos = a;
+    return need <= 1e-12 ? 0 : min(a + 1, open[j]);
+  };
+  double low = 0.0, high = 1.0;
+  for (int it = 0; it < 60; ++it) {
+    const double mid = (low + high) / 2;
+    long long local = 0;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j)
+      if (tid + j * kBisectThreads < p.rows) local += count_at(j, mid, mid_pos[j]);
+    const long long total = block_sum<kBisectThreads>(local, s_red);
+    const bool up = total <= free_blocks;
+    if (up) low = mid; else high = mid;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      if (tid + j * kBisectThreads >= p.rows) continue;
+      if (up) lo[j] = mid_pos[j]; else hi[j] = mid_pos[j];
+    }
+  }
+  // counts at the final level, then the leftover to the lowest (retained, index) first
+  int counts[kRowsPerThread];
+  double retained[kRowsPerThread];
+  long long used = 0;
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int r = tid + j * kBisectThreads;
+    counts[j] = 0;
+    retained[j] = 0.0;
+    if (r >= p.rows) continue;
+    int pos;
+    counts[j] = count_at(j, low, pos);
+    used += counts[j];
+    retained[j] = base[j] + (counts[j] ? m.prefix[(int64_t)r * p.width + counts[j] - 1] : 0.0);
+  }
+  long long leftover = free_blocks - block_sum<kBisectThreads>(used, s_red);
+  while (leftover > 0) {
+    double best = INFINITY;
+    int best_row = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      const int r = tid + j * kBisectThreads;
+      if (r >= p.rows || counts[j] >= open[j]) continue;
+      if (retained[j] < best || (retained[j] == best && r < best_row)) {
+        best = retained[j];
+        best_row = r;
+      }
+    }
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      const double ob = __shfl_xor(best, msk, kWave);
+      const int orow = __shfl_xor(best_row, msk, kWave);
+      if (ob < best || (ob == best && orow < best_row)) {
+        best = ob;
+        best_row = orow;
+      }
+    }
+    if (lane == 0) {
+      s_best[wave] = best;
+      s_best_row[wave] = best_row;
+    }
+    __syncthreads();
+    best = s_best[0];
+    best_row = s_best_row[0];
+    for (int w = 1; w < kBisectThreads / kWave; ++w) {
+      if (s_best[w] < best || (s_best[w] == best && s_best_row[w] < best_row)) {
+        best = s_best[w];
+        best_row = s_best_row[w];
+      }
+    }
+    __syncthreads();
+    if (best_row == INT_MAX) break;  // every request keeps all its blocks
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      if (tid + j * kBisectThreads != best_row) continue;
+      const int64_t row0 = (int64_t)best_row * p.width;
+      const RowStat st = p.row_stat[best_row];
+      const double sh = share_of(p, st, best_row, m.vals_out[row0 + counts[j]]);
+      counts[j] += 1;
+      retained[j] = best + sh;  // the level popped plus the kept block's share
+    }
+    --leftover;
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int r = tid + j * kBisectThreads;
+    if (r < p.rows) m.mrow[r].counts = counts[j];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void mm_keep_kernel(const MaxminParams m) {
+  const Params &p = m.p;
+  const int r = blockIdx.x;
+  const State *s = p.state;
+  const RowStat st = p.row_stat[r];
+  const bool all = s->error != 0 || s->mode == kKeepAll || s->mode == kKeepOpen;
+  uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
+  for (int b = threadIdx.x; b < p.width; b += kThreads)
+    krow[b] = (all || b >= st.n || pinned_at(p, r, b, st.n)) ? 1 : 0;
+  if (all) return;
+  __syncthreads();
+  const int counts = s->mode == kSelect ? m.mrow[r].counts : 0;
+  const int64_t row0 = (int64_t)r * p.width;
+  for (int i = threadIdx.x; i < counts; i += kThreads) krow[m.vals_out[row0 + i]] = 1;
+}
+
 }  // namespace alloc
 }  // namespace ekv
 
@@ -397,4 +627,112 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   }
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
+}
+
+namespace {
+
+struct MaxminLayout {
+  size_t state, row_stat, mrow, offsets, keys_in, keys_out, vals_in, vals_out, prefix, temp, temp_bytes, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
+  MaxminLayout l{};
+  const size_t cells = (size_t)rows * (size_t)width;
+  size_t at = 0;
+  l.state = at;
+  at = align256(at + sizeof(alloc::State));
+  l.row_stat = at;
+  at = align256(at + (size_t)rows * sizeof(alloc::RowStat));
+  l.mrow = at;
+  at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
+  l.offsets = at;
+  at = align256(at + (size_t)(rows + 1) * sizeof(int32_t));
+  l.keys_in = at;
+  at = align256(at + cells * 8);
+  l.keys_out = at;
+  at = align256(at + cells * 8);
+  l.vals_in = at;
+  at = align256(at + cells * 4);
+  l.vals_out = at;
+  at = align256(at + cells * 4);
+  l.prefix = at;
+  at = align256(at + cells * 8);
+  l.temp = at;
+  size_t temp = 0;
+  const hipError_t query = rocprim::segmented_radix_sort_pairs_desc((void *)nullptr, temp, (unsigned long long *)nullptr,
+                                           (unsigned long long *)nullptr, (int32_t *)nullptr, (int32_t *)nullptr,
+                                           (unsigned int)cells, (unsigned int)rows, (int32_t *)nullptr,
+                                           (int32_t *)nullptr, 0, 64);
+  l.temp_bytes = query == hipSuccess ? temp : 0;
+  l.total = align256(at + temp) + 256;  // + 256: the base may be realigned
+  return l;
+}
+
+}  // namespace
+
+extern "C" size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width) {
+  if (rows <= 0 || width <= 0) return 256;
+  return maxmin_layout(rows, width).total;
+}
+
+extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *blocks,
+                               const uint8_t *pinned, int64_t pinned_stride, int32_t rows, int32_t width,
+                               int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  if (scores == nullptr || blocks == nullptr || keep == nullptr || workspace == nullptr)
+    return fail(EKV_EINVAL, "ekv_rank_maxmin: null pointer");
+  if (rows < 0 || rows > alloc::kMaxMaxminRows || width < 1 || width > alloc::kMaxWidth)
+    return fail(EKV_EINVAL, "ekv_rank_maxmin: rows %d (max %d), width %d (max %d)", rows, alloc::kMaxMaxminRows,
+                width, alloc::kMaxWidth);
+  if (budget < 0) return fail(EKV_EINVAL, "ekv_rank_maxmin: the budget cannot be negative");
+  if (rows == 0) return EKV_OK;
+  const MaxminLayout l = maxmin_layout(rows, width);
+  if (workspace_bytes < l.total)
+    return fail(EKV_EINVAL, "ekv_rank_maxmin: a workspace of %zu bytes is below the %zu needed", workspace_bytes,
+                l.total);
+  const uintptr_t base = ((uintptr_t)workspace + 255) & ~(uintptr_t)255;
+  alloc::MaxminParams m{};
+  alloc::Params &p = m.p;
+  p.scores = scores;
+  p.scores_stride = scores_stride;
+  p.blocks = blocks;
+  p.weights = nullptr;
+  p.pinned = pinned;
+  p.pinned_stride = pinned_stride;
+  p.rows = rows;
+  p.width = width;
+  p.budget = budget;
+  p.keep = keep;
+  p.keep_stride = keep_stride;
+  p.summary = summary;
+  p.state = (alloc::State *)(base + l.state);
+  p.row_stat = (alloc::RowStat *)(base + l.row_stat);
+  m.mrow = (alloc::MaxminRow *)(base + l.mrow);
+  m.offsets = (int32_t *)(base + l.offsets);
+  m.keys_in = (unsigned long long *)(base + l.keys_in);
+  m.keys_out = (unsigned long long *)(base + l.keys_out);
+  m.vals_in = (int32_t *)(base + l.vals_in);
+  m.vals_out = (int32_t *)(base + l.vals_out);
+  m.prefix = (double *)(base + l.prefix);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
+  hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::mm_keys_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
+  if (rc != EKV_OK) return rc;
+  size_t temp = l.temp_bytes;
+  rc = check_hip(rocprim::segmented_radix_sort_pairs_desc((void *)(base + l.temp), temp, m.keys_in, m.keys_out,
+                                                          m.vals_in, m.vals_out,
+                                                          (unsigned int)((size_t)rows * (size_t)width),
+                                                          (unsigned int)rows, m.offsets, m.offsets + 1, 0, 64, s),
+                 "ekv_rank_maxmin sort");
+  if (rc != EKV_OK) return rc;
+  hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + alloc::kThreads - 1) / alloc::kThreads),
+                     dim3(alloc::kThreads), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_bisect_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
+  return check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
 }

@@ -53,6 +53,8 @@ _SIGNATURES: dict[str, list] = {
     ],
     "ekv_rank_sum_workspace": [_i32],
     "ekv_rank_sum": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p, _sz, _p],
+    "ekv_rank_maxmin_workspace": [_i32, _i32],
+    "ekv_rank_maxmin": [_p, _i64, _p, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p, _sz, _p],
     "ekv_compact_slots": [
         _p, _p, _i32, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _p, _p, _i32, _p,
     ],

@@ -5,7 +5,9 @@ gives every request the same fraction of its unpinned blocks, each ranked by its
 the free budget is split by largest remainder in IEEE double and each request keeps its quota of
 open blocks by (share descending, block index ascending) (``ekv_rank_uniform``).  ``sum`` keeps the
 free budget's unpinned blocks of highest weight * share over all requests, a tie going to the newer
-block, then the earlier request (``ekv_rank_sum``, float64 shares with NumPy's totals).  Pinned
+block, then the earlier request (``ekv_rank_sum``, float64 shares with NumPy's totals).  ``maxmin``
+raises the lowest retained share by the reference's bisection of the level and gives the leftover
+to the lowest request first (``ekv_rank_maxmin``).  Pinned
 blocks (by default the first and the last) always count against the budget, and a budget below
 them is an error.
 
@@ -73,7 +75,7 @@ def allocate(requests: Sequence[Request], budget: int, objective: Objective = "s
     if objective == "sum":
         return _sum_on_device(requests, pinned, budget)
     if objective == "maxmin":
-        raise NotImplementedError(f"the {objective} objective has no device implementation in this build")
+        return _maxmin_on_device(requests, pinned, budget)
     raise ValueError(f"unknown objective {objective!r}")
 
 
@@ -96,6 +98,47 @@ def _sum_on_device(requests: Sequence[Request], pinned: list[np.ndarray], budget
     weights = torch.tensor([float(r.weight) for r in requests], dtype=torch.float64).cuda()
     keep = sum_keep(scores, blocks, weights=weights, pinned=pins, budget=budget)[0].cpu().numpy()
     return [keep[i, : sizes[i]].astype(bool) for i in range(len(requests))]
+
+
+def _maxmin_on_device(requests: Sequence[Request], pinned: list[np.ndarray], budget: int) -> list[np.ndarray]:
+    scores, pins, blocks, sizes = _padded(requests, pinned)
+    keep = maxmin_keep(scores, blocks, pinned=pins, budget=budget)[0].cpu().numpy()
+    return [keep[i, : sizes[i]].astype(bool) for i in range(len(requests))]
+
+
+def maxmin_keep(
+    scores: torch.Tensor,
+    blocks: torch.Tensor,
+    *,
+    budget: int,
+    pinned: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The ``maxmin`` keep mask ``uint8[rows, width]`` on the device (observe/allocation.py:126-166)
+    and the int64 summary (budget, blocks, pinned, status, requests, free); arguments as sum_keep."""
+    if scores.dtype == torch.float32:
+        scores = scores.double()
+    if scores.dtype != torch.float64 or scores.stride(1) != 1:
+        raise ValueError("scores must be float64 (or float32) with contiguous rows")
+    rows, width = int(scores.shape[0]), int(scores.shape[1])
+    if blocks.dtype != torch.int32 or blocks.shape != (rows,):
+        raise ValueError("blocks must be int32 [rows]")
+    if pinned is not None and (pinned.dtype not in (torch.uint8, torch.bool) or pinned.stride(-1) != 1):
+        raise ValueError("pinned must be a uint8 / bool mask with contiguous rows")
+    if budget < 0:
+        raise ValueError("the budget cannot be negative")
+    if out is None:
+        out = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
+    summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
+    need = int(ekv_hip.load().ekv_rank_maxmin_workspace(rows, width))
+    workspace = torch.empty(need, dtype=torch.uint8, device=scores.device)
+    ekv_hip.call(
+        "ekv_rank_maxmin", scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(pinned),
+        pinned.stride(0) if pinned is not None else 0, rows, width, int(budget), out.data_ptr(), out.stride(0),
+        summary.data_ptr(), workspace.data_ptr(), need, ekv_hip.stream_handle(stream),
+    )
+    return out, summary
 
 
 def sum_keep(

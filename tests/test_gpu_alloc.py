@@ -87,3 +87,63 @@ def test_sum_summary_flags_a_budget_below_the_pins():
     assert int(summary[3]) == 1 and int(summary[2]) == 4
     with pytest.raises(ValueError):
         allocation.allocate([allocation.Request(scores=np.ones(5))] * 2, 3, "sum")
+
+
+# ---- maxmin ----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("seed", range(40))
+def test_maxmin_random_requests(seed):
+    rng = np.random.default_rng(seed)
+    scores, pinned = random_requests(rng, int(rng.integers(1, 9)), 40)
+    total = sum(len(s) for s in scores)
+    must = sum(int(p.sum()) for p in pinned)
+    budget = int(rng.integers(must, max(total, must + 1)))
+    reqs = [allocation.Request(scores=s, pinned=p) for s, p in zip(scores, pinned)]
+    assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget))
+
+
+def test_maxmin_identical_requests_and_edges():
+    # identical requests reach the level together: the leftover goes one block each by index
+    rng = np.random.default_rng(4)
+    s = rng.dirichlet(np.full(30, 0.3))
+    scores = [s.copy() for _ in range(12)]
+    pinned = [oa.default_pins(30) for _ in scores]
+    must = sum(int(p.sum()) for p in pinned)
+    for budget in (must, must + 1, must + 7, must + 100, 360 - 1, 360):
+        reqs = [allocation.Request(scores=x) for x in scores]
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), budget
+    with pytest.raises(ValueError):
+        allocation.allocate([allocation.Request(scores=np.ones(5))] * 2, 3, "maxmin")
+
+
+def test_maxmin_float64_scores_zero_rows_and_long_rows():
+    rng = np.random.default_rng(6)
+    scores = [rng.random(n) * (1 + 1e-9 * rng.random(n)) for n in (8191, 8193, 12288, 50)]
+    scores.append(np.zeros(40))  # no evidence: equal shares
+    scores.append(np.array([0.0, -1.0, 2.0, np.float64(1e-300)]))
+    pinned = [oa.default_pins(len(s)) for s in scores]
+    pinned[3] = rng.random(50) < 0.3  # explicit pins
+    total = sum(len(s) for s in scores)
+    for frac in (0.05, 0.3, 0.7, 0.95):
+        budget = max(int(frac * total), sum(int(p.sum()) for p in pinned))
+        reqs = [allocation.Request(scores=s, pinned=p) for s, p in zip(scores, pinned)]
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
+
+
+def test_maxmin_view_build_configuration():
+    c = workloads.config4()
+    shares, blocks = c["shares"], c["blocks"]
+    sizes = blocks.tolist()
+    total = int(blocks.sum())
+    scores = [shares[r, : sizes[r]] for r in range(len(sizes))]
+    pinned = [oa.default_pins(n) for n in sizes]
+    s_dev, b_dev = torch.from_numpy(shares).cuda(), torch.from_numpy(blocks).cuda()
+    for frac in (0.2, 0.5, 0.8):
+        budget = int(np.ceil(frac * total))
+        keep, summary = allocation.maxmin_keep(s_dev, b_dev, budget=budget)
+        got = keep.cpu().numpy()
+        want = oa.allocate_maxmin(scores, pinned, budget)
+        bad = sum(int((got[r, : sizes[r]].astype(bool) != want[r]).sum()) for r in range(len(sizes)))
+        print(f"maxmin at {frac}: budget {budget}, kept {sum(int(w.sum()) for w in want)}, mismatched {bad}",
+              flush=True)
+        assert bad == 0 and int(summary[3]) == 0
