@@ -429,6 +429,16 @@ def main() -> None:
     c4_ms = float(np.median(time_events(view_build_c4, 20, stream)))
     c4_rank_ms = float(np.median(time_events(rank_c4, 20, stream)))
     c4_compact_ms = float(np.median(time_events(compact_c4, 20, stream)))
+    # the other objectives on the same rows: sum (global top-k) and maxmin (water level)
+    from observe.allocation import maxmin_keep, sum_keep
+
+    s4_64 = s4.double()
+    b4 = int(np.ceil(0.5 * int(c4["blocks"].sum())))
+    sum_keep(s4_64, n4, budget=b4)
+    c4_sum_ms = float(np.median(time_events(lambda: sum_keep(s4_64, n4, budget=b4), 10, stream)))
+    maxmin_keep(s4_64, n4, budget=b4)
+    c4_maxmin_ms = float(np.median(time_events(lambda: maxmin_keep(s4_64, n4, budget=b4), 5, stream)))
+    del s4_64
 
     others = other_audit_shapes()
     peak = copy_peak_gbs()
@@ -480,7 +490,9 @@ def main() -> None:
         "view_build_us": {"llama3_step_128_rows": round(view_ms * 1e3, 2),
                           "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2),
                           "config_1024x8192_rank": round(c4_rank_ms * 1e3, 2),
-                          "config_1024x8192_compact": round(c4_compact_ms * 1e3, 2)},
+                          "config_1024x8192_compact": round(c4_compact_ms * 1e3, 2),
+                          "config_1024x8192_sum_objective": round(c4_sum_ms * 1e3, 2),
+                          "config_1024x8192_maxmin_objective": round(c4_maxmin_ms * 1e3, 2)},
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu:

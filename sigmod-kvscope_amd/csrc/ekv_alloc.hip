@@ -31,6 +31,8 @@
 #include <limits.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "ekv_common.hpp"
@@ -194,6 +196,14 @@ __device__ __forceinline__ unsigned long long gain_key(double g) {
   return k < 2ull ? 2ull : k;  // keep 0 and 1 free (only the most negative NaN-free values would map there)
 }
 
+// the float64 value of a key (both zeros decode to +0.0, which every comparison and sum treats
+// as -0.0; key 1, NaN, decodes to NaN)
+__device__ __forceinline__ double key_value(unsigned long long k) {
+  if (k == 1ull) return __builtin_nan("");
+  const unsigned long long bits = (k >> 63) ? (k & ~(1ull << 63)) : ~k;
+  return __builtin_bit_cast(double, bits);
+}
+
 __device__ __forceinline__ double share_of(const Params &p, const RowStat &st, int r, int b) {
   if (!(st.total > 0.0) && st.total == st.total) return 1.0 / (double)max(st.n, 1);  // total <= 0
   return clamp0(p.scores[(int64_t)r * p.scores_stride + b]) / st.total;
@@ -270,7 +280,8 @@ __device__ __forceinline__ unsigned long long tie_key(int r, int b) {
 }
 
 // one radix pass: the digit histogram of the open blocks whose key matches the prefix so far
-// (tie passes: the blocks at the gain threshold, over the tie key)
+// (tie passes: the blocks at the gain threshold, over the tie key).  Workgroup w takes rows
+// w, w + grid, ..., so each workgroup flushes its LDS histogram to the global one once.
 template <bool TIE>
 __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift) {
   __shared__ unsigned int s_hist[256];
@@ -279,17 +290,27 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   s_hist[threadIdx.x] = 0u;
   __syncthreads();
   const unsigned long long prefix = s->prefix, mask = s->mask, threshold = s->threshold;
-  const int r = blockIdx.y;
-  const RowStat st = p.row_stat[r];
-  for (int b = blockIdx.x * kThreads + threadIdx.x; b < st.n; b += gridDim.x * kThreads) {
-    if (pinned_at(p, r, b, st.n)) continue;
-    const unsigned long long k = key_at(p, st, r, b);
-    unsigned long long key = k;
-    if constexpr (TIE) {
-      if (k != threshold) continue;
-      key = tie_key(r, b);
+  for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    const RowStat st = p.row_stat[r];
+    for (int b = threadIdx.x; b < st.n; b += kThreads) {
+      if (pinned_at(p, r, b, st.n)) continue;
+      const unsigned long long k = key_at(p, st, r, b);
+      unsigned long long key = k;
+      if constexpr (TIE) {
+        if (k != threshold) continue;
+        key = tie_key(r, b);
+      }
+      if ((key & mask) != prefix) continue;
+      const unsigned int digit = (unsigned int)(key >> shift) & 255u;
+      // when every counting lane of the wave has one digit (the first passes), one add for all
+      const uint64_t active = __ballot(true);
+      const unsigned int lead = __shfl(digit, __ffsll((long long)active) - 1, kWave);
+      if (__ballot(digit == lead) == active) {
+        if (lane_id() == __ffsll((long long)active) - 1) atomicAdd(&s_hist[lead], (unsigned int)__popcll(active));
+      } else {
+        atomicAdd(&s_hist[digit], 1u);
+      }
     }
-    if ((key & mask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255], 1u);
   }
   __syncthreads();
   const unsigned int c = s_hist[threadIdx.x];
@@ -414,25 +435,38 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
   }
 }
 
-// per request, one thread: the running totals of the open shares in sorted order (np.cumsum)
-__global__ __launch_bounds__(kThreads) void mm_prefix_kernel(const MaxminParams m) {
+// per request, one lane: the running totals of the open shares in sorted order (np.cumsum), the
+// shares decoded from the sorted keys, read as a stream 32 values at a time with the next 32 in
+// flight while the current ones are added
+constexpr int kPrefixBatch = 32;
+
+__global__ __launch_bounds__(kWave) void mm_prefix_kernel(const MaxminParams m) {
   const Params &p = m.p;
-  const int r = blockIdx.x * kThreads + threadIdx.x;
+  const int r = blockIdx.x * kWave + threadIdx.x;
   if (r >= p.rows) return;
-  const RowStat st = p.row_stat[r];
-  const int open = st.open;
+  const int open = p.row_stat[r].open;
   const int64_t row0 = (int64_t)r * p.width;
+  const unsigned long long *keys = m.keys_out + row0;
+  double *out = m.prefix + row0;
+  unsigned long long cur[kPrefixBatch], nxt[kPrefixBatch];
+#pragma unroll
+  for (int k = 0; k < kPrefixBatch; ++k) cur[k] = k < open ? keys[k] : 0ull;
   double acc = 0.0;
-  for (int i0 = 0; i0 < open; i0 += 8) {
-    double v[8];
+  for (int i0 = 0; i0 < open; i0 += kPrefixBatch) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = i0 + k < open ? share_of(p, st, r, m.vals_out[row0 + i0 + k]) : 0.0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (i0 + k >= open) break;
-      acc = (i0 + k == 0) ? v[k] : acc + v[k];
-      m.prefix[row0 + i0 + k] = acc;
+    for (int k = 0; k < kPrefixBatch; ++k) {
+      const int i = i0 + kPrefixBatch + k;
+      nxt[k] = i < open ? keys[i] : 0ull;
     }
+#pragma unroll
+    for (int k = 0; k < kPrefixBatch; ++k) {
+      if (i0 + k >= open) break;
+      const double v = key_value(cur[k]);
+      acc = (i0 + k == 0) ? v : acc + v;
+      out[i0 + k] = acc;
+    }
+#pragma unroll
+    for (int k = 0; k < kPrefixBatch; ++k) cur[k] = nxt[k];
   }
 }
 
@@ -616,7 +650,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(kWave), 0, s, p);
-  const dim3 grid((width + alloc::kThreads - 1) / alloc::kThreads, rows);
+  const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
   for (int pass = 0; pass < 8; ++pass) {  // the gain threshold, 8 bits at a time from the top
     hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, 56 - 8 * pass);
     hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, 56 - 8 * pass, pass == 7);
@@ -730,8 +764,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
                                                           (unsigned int)rows, m.offsets, m.offsets + 1, 0, 64, s),
                  "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
-  hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + alloc::kThreads - 1) / alloc::kThreads),
-                     dim3(alloc::kThreads), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + kWave - 1) / kWave), dim3(kWave), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_bisect_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
   return check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
