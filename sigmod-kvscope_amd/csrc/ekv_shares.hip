@@ -26,6 +26,8 @@
 #include <limits.h>
 #include <math.h>
 
+#include <algorithm>
+
 #include "ekv_common.hpp"
 
 namespace ekv {
@@ -44,6 +46,7 @@ struct Params {
   int32_t layers, cells, cells_pow2, width;
   const int32_t *row_ids, *row_blocks;
   int32_t tile_blocks, aggregate, from_u;
+  int32_t lanes_per_layer;  // the peak pass's lanes per layer (quads path)
   float *shares;
   int64_t shares_stride;
 };
@@ -129,19 +132,26 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   // ---- phase 1: peak and total of every (layer, query row) ------------------------------
   int contrib = 0;
   if constexpr (VEC) {
+    // LPL lanes take one layer (several layers per wave when there are few blocks per lane), each
+    // lane a running (max, sum) per cell of its quads; the lanes of a layer then reduce the max,
+    // rescale their sums once and reduce the sums
     const int QP = cells >> 2, qp_log2 = __builtin_ctz(QP);  // quads per block, dividing 64
-    const int slot = lane & (QP - 1);  // the quad of the block every element of this lane is in
+    const int LPL = p.lanes_per_layer;                       // a power of two, QP <= LPL <= 64
+    const int sub = lane & (LPL - 1);
+    const int slot = sub & (QP - 1);  // the quad of the block every element of this lane is in
+    const int slots = kThreads / LPL;  // layers reduced at once by the workgroup
     const int quads = n * QP;
-    for (int layer = wave; layer < p.layers; layer += kWaves) {
-      const int64_t base = layer * p.layer_stride + row_base;
+    for (int layer = (tid / LPL); layer - (tid / LPL) < p.layers; layer += slots) {
+      const bool live = layer < p.layers;
+      const int64_t base = (live ? layer : 0) * p.layer_stride + row_base;
       const f32x4_t *mq = reinterpret_cast<const f32x4_t *>(p.m + base);
       const f32x4_t *lq = reinterpret_cast<const f32x4_t *>(lplane + base);
       float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int e0 = lane; e0 < quads; e0 += kWave * kBatch) {
+      for (int e0 = sub; live && e0 < quads; e0 += LPL * kBatch) {
         f32x4_t mv[kBatch], lv[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-          const int at = e0 + k * kWave < quads ? e0 + k * kWave : 0;
+          const int at = e0 + k * LPL < quads ? e0 + k * LPL : 0;
           mv[k] = mq[at];
           lv[k] = weight.from_u ? mv[k] : lq[at];
         }
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
           float m[kBatch], w[kBatch];
 #pragma unroll
           for (int k = 0; k < kBatch; ++k) {
-            const int e = e0 + k * kWave;
+            const int e = e0 + k * LPL;
             m[k] = mv[k][j];
             w[k] = e < quads ? weight(mv[k][j], lv[k][j], e >> qp_log2) : 0.0f;
           }
@@ -159,13 +169,14 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        for (int msk = QP; msk < kWave; msk <<= 1) {
-          const float m2 = shfl_xor(mx[j], msk);
-          const float s2 = shfl_xor(sum[j], msk);
-          merge(mx[j], sum[j], m2, s2);
-        }
+        float M = mx[j];
+        for (int msk = QP; msk < LPL; msk <<= 1) M = fmaxf(M, shfl_xor(M, msk));
+        float t = (mx[j] == -INFINITY) ? 0.0f : sum[j] * __expf(mx[j] - M);
+        for (int msk = QP; msk < LPL; msk <<= 1) t += shfl_xor(t, msk);
+        mx[j] = M;
+        sum[j] = t;
       }
-      if (lane < QP) {
+      if (live && sub < QP) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int c = 4 * slot + j;
@@ -334,6 +345,11 @@ int launch(Params p, int nrows, void *stream) {
   const bool aligned = ((uintptr_t)p.m % 16) == 0 && (p.from_u || ((uintptr_t)p.l % 16) == 0) &&
                        p.layer_stride % 4 == 0 && p.row_stride % 4 == 0;
   const bool vec = aligned && p.cells % 4 == 0 && cp == p.cells;  // cells / 4 a power of two
+  // the peak pass: as many lanes per layer as the workgroup has per layer, a power of two from the
+  // quads per block to a wave
+  int lpl = kWave;
+  while (lpl > 1 && lpl * p.layers > kThreads) lpl >>= 1;
+  p.lanes_per_layer = std::max(lpl, std::max(cp / 4, 1));
   if (vec)
     hipLaunchKernelGGL(shares_kernel<true>, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
   else
