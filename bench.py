@@ -282,6 +282,20 @@ def cpu_baseline(step: Step, bound_s: float) -> dict:
     got = step.plane.read_planes()
     live = ~np.isnan(planes[0])
     err = float(np.abs(got[0][live] - planes[0][live]).max())
+    # the rest of the step on the host, as the reference runs it: the planes' read and float64
+    # normalisation, the controller's uniform ranking (budget 0.5, 4 recent blocks pinned) and the
+    # compaction of the block table
+    from oracle import block_view as oracle_view
+    from oracle import controller as oracle_controller
+    from oracle import tile_shares as oracle_shares
+
+    t0 = time.perf_counter()
+    shares = oracle_shares.normalize(oracle_shares.read_rows(got, LAYERS, np.arange(b.rows), 2), b.blocks, 2)
+    t1 = time.perf_counter()
+    keep, _ = oracle_controller.keep_rows(shares.astype(np.float32), b.blocks, np.ones(b.rows), FRACTION, RECENT, 0)
+    t2 = time.perf_counter()
+    oracle_view.compact(b.table, b.lens, keep.astype(bool), b.block_size)
+    t3 = time.perf_counter()
     return {
         "value": round(launches * audit_bytes(b) / busy / 1e9, 3),
         "unit": "GB/s",
@@ -290,6 +304,12 @@ def cpu_baseline(step: Step, bound_s: float) -> dict:
         "sample": f"{launches // LAYERS} passes over the 32 layer launches of the step (all 128 rows, one KV group "
                   f"each) with oracle.audit.tile_lse_torch (gather, matmul, tile max / sum exp), {busy:.1f} s of "
                   f"audit time; tile max agrees with the GPU to {err:.1e}",
+        "step_stages_s": {
+            "audit_32_layers": round(busy / (launches / LAYERS), 4),
+            "normalise_32_layers": round(t1 - t0, 4),
+            "uniform_rank": round(t2 - t1, 4),
+            "compact": round(t3 - t2, 4),
+        },
     }
 
 

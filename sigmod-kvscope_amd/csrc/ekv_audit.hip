@@ -574,13 +574,14 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
     };
 
     // the MFMAs of a chunk: scores of tokens 16 mt + 4 c + i for query row n in sc[4 mt + i]
-    auto mma_chunk = [&](const u32x4 (&L)[2 * NLD], f32x4_t (&acc)[2]) {
+    auto mma_chunk = [&](u32x4 (&L)[2 * NLD], f32x4_t (&acc)[2]) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        // the M-tile through LDS: row n's piece 4 s + c is operand s of this lane
+        // the M-tile through LDS: row n's piece 4 s + c is operand s of this lane, read back into
+        // the registers the M-tile was loaded into
+        u32x4 *D = L + mt * NLD;
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) tr[tr_slot<S>(j * S::kTPI + row_in, piece)] = L[mt * NLD + j];
-        u32x4 D[NLD];
+        for (int j = 0; j < NLD; ++j) tr[tr_slot<S>(j * S::kTPI + row_in, piece)] = D[j];
 #pragma unroll
         for (int s = 0; s < NLD; ++s) D[s] = tr[tr_slot<S>(n, 4 * s + c)];
         acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
