@@ -723,6 +723,7 @@ KernelFn pick_gp(int gp) {
 template <int MODE, int HD>
 KernelFn pick_nl(int nl, int gp) {
   switch (nl) {
+    case 2: return pick_gp<MODE, HD, 2>(gp);
     case 4: return pick_gp<MODE, HD, 4>(gp);
     case 8: return pick_gp<MODE, HD, 8>(gp);
   }
