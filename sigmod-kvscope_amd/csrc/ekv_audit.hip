@@ -5,22 +5,21 @@
 //
 // Design (gfx950, wave64):
 //  * Work list.  The live tiles of the selected rows, times the audited KV heads, form one
-//    flat list; wave w of the grid takes the w-th equal contiguous slice of it (split-K over
-//    the rows' tiles, crossing row boundaries), so every wave does the same amount of work
-//    whatever the length mix.  Every workgroup builds the per-row tile offsets in LDS from
-//    lens/select with a block scan, so the launch needs no host-side knowledge of the lengths,
-//    no scratch memory and no second kernel; it is identical on every step and can be captured
-//    in a graph.  The grid is the number of workgroups the GPU holds at once.
-//  * Loads.  One token's key row of one head is `row_bytes` contiguous bytes; LPT lanes load
-//    it with 16-byte loads, TPI = 64 / LPT tokens per wave instruction.  A chunk is NL such
-//    instructions; chunks are double-buffered so one chunk's loads are in flight while the
-//    previous one is reduced (the prefetch is unconditional inside the loop so that the
-//    compiler's wait counts let it stay in flight).
-//  * Dots.  Each lane multiplies its 16-byte slice with the matching slice of the (padded)
-//    query group kept in registers (v_dot2 for 16-bit / fp8->bf16 keys, FMA for fp32), then a
-//    transpose reduction over the LPT lanes of a token leaves VF complete scores per lane,
-//    head-major, so the per-head max / sum need log2(64/GP) butterfly steps.
-//  * Timer.  With a cycles buffer each unit adds its s_memtime duration to cycles[row] with a
+//    flat list.  Every workgroup builds the per-row tile offsets in LDS from lens/select with a
+//    block scan, so the launch needs no host-side knowledge of the lengths, no scratch memory
+//    and no second kernel; it is identical on every step and can be captured in a graph.
+//  * Three kernels.  16-bit and fp8 keys whose row (one token, one head) is at most 256 bytes
+//    take tile_lse_cu_kernel: one 12-wave workgroup per compute unit, an equal slice of the list
+//    per CU, and the CU's waves share the slice through an LDS counter (a CU serves its loads
+//    about in issue order, so equal per-wave slices leave the last-issued waves finishing last).
+//    512-byte rows (16-bit keys, d = 256) take tile_lse_mfma_kernel, equal per-wave slices.
+//    fp32 keys and blocks under 16 tokens take tile_lse_kernel on the VALU.
+//  * Loads.  A load instruction reads whole key rows (16-byte lanes), the coalesced form that
+//    DRAM serves at the streaming rate whatever the head's offset in the token.
+//  * Dots.  The MFMA kernels compute S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16} after an LDS
+//    pass that turns whole-row loads into token-per-lane operands; the VALU kernel multiplies
+//    each lane's slice with the query slice (v_dot2 / FMA) and reduces over the lanes of a row.
+//  * Timer.  With a cycles buffer each wave adds its s_memtime durations to cycles[row] with a
 //    vector 64-bit atomic (the pass's per-row timer, mlir_pass/lib/eKVTimer.cpp:1348-1387).
 #include <math.h>
 
@@ -33,8 +32,10 @@ namespace audit {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+constexpr int kCuThreads = 768;  // tile_lse_cu_kernel: 12 waves, one workgroup per compute unit
 constexpr int kTileBlocks = 2;  // TILE_BLOCKS, runtime/audit_kernel.py:31
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxRows = 6000;  // LDS holds two ints per row and 16 KB of staged records
 
 enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
@@ -441,19 +442,18 @@ __device__ __forceinline__ void widen_fp8(const u32x4 k, u32x4 &lo, u32x4 &hi) {
   hi = (u32x4){w[4], w[5], w[6], w[7]};
 }
 
-// NT loads the keys with the nontemporal hint (they are read once).
+// The per-wave MFMA kernel, for 512-byte key rows (16-bit keys, d = 256), whose two staged
+// M-tiles per wave would not fit the per-CU kernel's LDS.  NT loads the keys with the
+// nontemporal hint (they are read once).
 //
-// Loads.  A load instruction reads whole key rows (16 lanes x 16 bytes for a 256-byte row, 4
-// rows per instruction), the coalesced form: DRAM serves it at the streaming rate whatever the
-// head's offset in the token, where 64-byte pieces of 16 rows per instruction run up to 35%
-// slower for some heads.  The MFMA wants a token per lane instead, so each 16-row M-tile goes
-// through a per-wave LDS buffer (written in load order, read in operand order, both free of
-// bank conflicts by the slot permutation tr_slot).
+// Loads.  A load instruction reads whole key rows (32 lanes x 16 bytes per 512-byte row, 2 rows
+// per instruction).  The MFMA wants a token per lane instead, so each 16-row M-tile goes through
+// a per-wave LDS buffer (written in load order, read in operand order back into the registers it
+// came from, both free of bank conflicts by the slot permutation tr_slot).
 //
-// Per wave, two chunks are in flight.  A chunk's reduction is split: the MFMAs are the only
-// readers of the load buffer, so the next chunk's loads are issued right after them and the
-// softmax part overlaps with them.  The per-tile records are staged in LDS and written once per
-// window with coalesced stores, so no conditional global store sits between a load and its wait.
+// Per wave, two chunks are in flight: the MFMAs are the only readers of a chunk's registers, so
+// the chunk after next is loaded right after them and the softmax part overlaps with it.  The
+// per-tile records are staged in LDS and written once per window with coalesced stores.
 constexpr int kMaxGroupRows = 16;
 constexpr int kWindowTiles = kWave / kTileBlocks;  // tiles whose block ids one register holds
 constexpr int kStageFloats = kWindowTiles * 2 * kMaxGroupRows;  // per wave: [tile][plane][row]
@@ -477,7 +477,8 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
   // ---- per-row live tiles: one read of select / lens, then a block scan ------------------
   // the audit flag (runtime/audit_kernel.py:64) is read together with the rows' lengths, so
   // that the prologue waits for memory once
-  const bool on = *p.flag != 0u;
+  // (a vector load: a scalar one would be waited for before the lengths are requested)
+  const bool on = *(volatile const uint32_t *)p.flag != 0u;
 #pragma unroll 4
   for (int r = threadIdx.x; r < rows; r += kThreads) {
     const int len = min(max(p.lens[r], 0), p.width * bs);
@@ -511,6 +512,13 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
   u32x4 *tr = s_tr[threadIdx.x / kWave];
   const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
   const int piece = lane % S::kPieces;
+  // the lane's byte offset within an M-tile for load j: row j * TPI + row_in, piece (the host
+  // checks that 16 positions fit in 31 bits)
+  uint32_t voff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * p.k_stride_pos + piece * 16);
+  // scores in log2 units: s2 = log2(e) * scale * q.k, so that exp(s - m) = exp2(s2 - m2)
+  const float scale2 = p.scale * kLog2e;
   const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
   const long long all = (long long)total_tiles * p.groups;
   long long u = all * wave_id / nwaves;
@@ -548,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
         qb[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
       }
     }
-    const int64_t lane_off = (int64_t)row_in * p.k_stride_pos + (int64_t)g * p.k_stride_head + piece * 16;
+    const int64_t head_off = (int64_t)g * p.k_stride_head;
     float *cell_row = p.lse + (int64_t)row * p.row_stride + h * G;
     float m_run = -INFINITY, l_run = 0.0f;
 
@@ -564,10 +572,15 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
         const int b = tile * kTileBlocks + tpos / bs;
         // past the row the tile's first block stands in (in the cache; the scores are masked)
         const int id = __builtin_amdgcn_readlane(ids, (b < nblocks ? b : tile * kTileBlocks) - ids_base);
-        const char *src = p.keys + (int64_t)id * p.k_stride_block + lane_off + (int64_t)(tpos % bs) * p.k_stride_pos;
+        // a wave-uniform base (scalar arithmetic) plus the lane's 32-bit offset
+        const char *src = p.keys + (int64_t)id * p.k_stride_block + head_off + (int64_t)(tpos % bs) * p.k_stride_pos;
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {  // rows j * TPI .. + TPI of the M-tile
-          const u32x4 *at = (const u32x4 *)(src + (int64_t)(j * S::kTPI) * p.k_stride_pos);
+          // (the empty asm keeps the 32-bit offset in the loop, so the load takes the scalar
+          // base directly instead of a 64-bit vector address)
+          uint32_t o = voff[j];
+          asm volatile("" : "+v"(o));
+          const u32x4 *at = (const u32x4 *)(src + o);
           D[mt * NLD + j] = NT ? __builtin_nontemporal_load(at) : *at;
         }
       }
@@ -605,36 +618,41 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
       const int sub = z & (nsub - 1);
       const int tok0 = tile * tile_tokens + sub * CH;
       float sc[8];
+      if (tok0 + CH <= len) {  // the whole chunk is in the row (uniform): no mask
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tok = tok0 + 16 * mt + 4 * c + i;
-          sc[4 * mt + i] = tok < len ? acc[mt][i] * p.scale : -INFINITY;
-        }
+          for (int i = 0; i < 4; ++i) sc[4 * mt + i] = acc[mt][i] * scale2;
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tok = tok0 + 16 * mt + 4 * c + i;
+            sc[4 * mt + i] = tok < len ? acc[mt][i] * scale2 : -INFINITY;
+          }
+      }
       float mx = sc[0];
 #pragma unroll
       for (int k = 1; k < 8; ++k) mx = fmaxf(mx, sc[k]);
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
+      mx = rows_max(mx);
       // exponents are <= 0 (a score minus a max); v_exp_f32 gives 0 for -inf and for underflow
       float sum = 0.0f;
       if (mx != -INFINITY) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) sum += __builtin_amdgcn_exp2f((sc[k] - mx) * kLog2e);
+        for (int k = 0; k < 8; ++k) sum += __builtin_amdgcn_exp2f(sc[k] - mx);
       }
-      sum += shfl_xor(sum, 16);
-      sum += shfl_xor(sum, 32);
+      sum = rows_sum(sum);
       const float M = fmaxf(m_run, mx);
       if (M != -INFINITY) {
-        const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f((m_run - M) * kLog2e);
-        const float bb = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f((mx - M) * kLog2e);
+        const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f(m_run - M);
+        const float bb = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f(mx - M);
         l_run = a + bb;
         m_run = M;
       }
-      if (sub == nsub - 1) {  // the tile is complete: stage its record
+      if (sub == nsub - 1) {  // the tile is complete: stage its record (m back in natural units)
         if (c == 0) {
-          stage[((tile - w0) * 2 + 0) * kMaxGroupRows + n] = m_run;
+          stage[((tile - w0) * 2 + 0) * kMaxGroupRows + n] = m_run * kLn2;
           stage[((tile - w0) * 2 + 1) * kMaxGroupRows + n] = l_run;
         }
         m_run = -INFINITY;
@@ -650,35 +668,30 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
       int z = w0 * nsub;
       u32x4 A[2 * NLD], B[2 * NLD];
       f32x4_t acc[2];
+      // chunk z from registers L; with `next`, L then takes chunk z_next's loads
+      auto step = [&](u32x4 (&L)[2 * NLD], int z_now, bool next, int z_next) {
+        mma_chunk(L, acc);
+        if (next) load_chunk(L, z_next);
+        softmax_chunk(acc, z_now);
+      };
       if (z + 1 == z_end) {
         load_chunk(A, z);
-        mma_chunk(A, acc);
-        softmax_chunk(acc, z);
+        step(A, z, false, 0);
       } else {
         load_chunk(A, z);
         load_chunk(B, z + 1);
         while (z + 3 < z_end) {  // steady state: every load unconditional
-          mma_chunk(A, acc);
-          load_chunk(A, z + 2);
-          softmax_chunk(acc, z);
-          mma_chunk(B, acc);
-          load_chunk(B, z + 3);
-          softmax_chunk(acc, z + 1);
+          step(A, z, true, z + 2);
+          step(B, z + 1, true, z + 3);
           z += 2;
         }
         if (z + 2 < z_end) {
-          mma_chunk(A, acc);
-          load_chunk(A, z + 2);
-          softmax_chunk(acc, z);
-          mma_chunk(B, acc);
-          softmax_chunk(acc, z + 1);
-          mma_chunk(A, acc);
-          softmax_chunk(acc, z + 2);
+          step(A, z, true, z + 2);
+          step(B, z + 1, false, 0);
+          step(A, z + 2, false, 0);
         } else {
-          mma_chunk(A, acc);
-          softmax_chunk(acc, z);
-          mma_chunk(B, acc);
-          softmax_chunk(acc, z + 1);
+          step(A, z, false, 0);
+          step(B, z + 1, false, 0);
         }
       }
       // the window's records into every block of its tiles that the row reaches,
@@ -699,6 +712,305 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
       const uint64_t t_end = __builtin_amdgcn_s_memtime();
       atomicAdd((unsigned long long *)(p.cycles + row), (unsigned long long)(t_end - t_start));
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// The MFMA form with one workgroup per compute unit (key rows of up to 256 bytes).
+//
+// A compute unit serves its waves' loads roughly in the order they were issued, so with equal
+// static slices the waves that issued last receive their data last and finish last: at the
+// Llama-3-8B shape the third workgroup on a CU gets its first chunk ~12 us after the first one
+// and the launch ends on those waves alone.  Here the CU's waves share its slice instead: the
+// slice is cut into rounds of one tile per thread, every thread describes one tile of the round
+// in LDS (row, head, position in the row, the two block ids, the query token), and the waves take
+// tiles from an LDS counter, one tile ahead of the one they load.  A wave that is served early
+// simply takes more tiles, and all waves run out of work together.
+//
+// Per wave one chunk (32 tokens, two M-tiles) is in flight: when it arrives it is written to the
+// wave's LDS buffer (load order in, MFMA operand order out, conflict-free by tr_slot), the next
+// chunk's loads go into the same registers, and the MFMAs and the softmax run from LDS while
+// they are in flight.  Each finished tile's record is stored at once, into both of its blocks.
+// ---------------------------------------------------------------------------------------
+template <int MODE, int HEAD_DIM>
+struct CuShape {
+  using S = MfmaShape<MODE, HEAD_DIM>;
+  static_assert(S::kRowBytes <= 256, "512-byte key rows use tile_lse_mfma_kernel");
+  static constexpr int kThreads = kCuThreads;  // 3 waves per SIMD: the shape's VGPR budget
+  static constexpr int kWaves = kThreads / kWave;
+  static constexpr int kRound = kThreads;  // tiles described per round, one per thread
+  static constexpr int kStash = 2 * 16 * S::kPieces;  // u32x4 per wave: two M-tiles
+  static constexpr size_t kStaticLds =
+      sizeof(u32x4) * kWaves * kStash + sizeof(int4) * kRound + sizeof(int) * (kRound + kWaves + 1);
+};
+
+template <int MODE, int HEAD_DIM>
+__global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p) {
+  using S = MfmaShape<MODE, HEAD_DIM>;
+  using C = CuShape<MODE, HEAD_DIM>;
+  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = S::kChunk;
+  constexpr int NW = C::kWaves, NT = C::kThreads;
+
+  extern __shared__ int s_mem[];       // [rows + 1] tile offsets, [rows] clipped lengths
+  __shared__ int s_scan[NW];
+  __shared__ int s_next;               // the round's next untaken tile
+  __shared__ int4 s_desc[C::kRound];   // (row | head << 16, tile in row, id0, id1)
+  __shared__ int s_qtok[C::kRound];    // the row's query token
+  __shared__ u32x4 s_tr[NW][C::kStash];
+  int *s_off = s_mem;
+  int *s_len = s_mem + p.rows + 1;
+
+  const int rows = p.rows;
+  const int bs = p.block_size;
+  const int tile_tokens = kTileBlocks * bs;
+
+  // ---- per-row live tiles and their scan, as in tile_lse_mfma_kernel ----------------------
+  // (the flag is a vector load issued with the lengths: a scalar one would be waited for first)
+  const bool on = *(volatile const uint32_t *)p.flag != 0u;
+#pragma unroll 4
+  for (int r = threadIdx.x; r < rows; r += NT) {
+    const int len = min(max(p.lens[r], 0), p.width * bs);
+    s_len[r] = len;
+    s_off[r] = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
+  }
+  if (!on) return;  // runtime/audit_kernel.py:64
+  __syncthreads();
+  {
+    const int per = (rows + NT - 1) / NT;
+    const int r0 = threadIdx.x * per;
+    const int r1 = min(r0 + per, rows);
+    int local = 0;
+    for (int r = r0; r < r1; ++r) local += s_off[r];
+    int total = 0;
+    int base = block_exclusive_scan<NT>(local, s_scan, total);
+    for (int r = r0; r < r1; ++r) {
+      const int tiles = s_off[r];
+      s_off[r] = base;
+      base += tiles;
+    }
+    if (threadIdx.x == 0) s_off[rows] = total;
+  }
+  __syncthreads();
+  const int total_tiles = s_off[rows];
+
+  const int lane = lane_id();
+  const int n = lane & 15;  // A: token of the M-tile; B / C: query row
+  const int c = lane >> 4;  // dim piece within a k-step; C: token quad
+  const int nsub = p.nsub;  // chunks per tile
+  const int G = p.group_rows;
+  u32x4 *tr = s_tr[threadIdx.x / kWave];
+  const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
+  const int piece = lane % S::kPieces;
+  uint32_t voff[NLD];  // the lane's byte offset in an M-tile for load j (host-checked to fit)
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * p.k_stride_pos + piece * 16);
+  const float scale2 = p.scale * kLog2e;  // scores in log2 units: exp(s - m) = exp2(s2 - m2)
+
+  // this workgroup's slice of the flat (head, tile) list
+  const long long all = (long long)total_tiles * p.groups;
+  const long long u_first = all * blockIdx.x / gridDim.x;
+  const long long u_last = all * (blockIdx.x + 1) / gridDim.x;
+
+  struct Tile {
+    int row, h, k, id0, id1, qtok;
+  };
+  auto describe = [&](int i) -> Tile {
+    const int4 d = s_desc[i];
+    Tile t;
+    t.row = __builtin_amdgcn_readfirstlane(d.x & 0xffff);
+    t.h = __builtin_amdgcn_readfirstlane(d.x >> 16);
+    t.k = __builtin_amdgcn_readfirstlane(d.y);
+    t.id0 = __builtin_amdgcn_readfirstlane(d.z);
+    t.id1 = __builtin_amdgcn_readfirstlane(d.w);
+    t.qtok = __builtin_amdgcn_readfirstlane(s_qtok[i]);
+    return t;
+  };
+  auto take = [&]() -> int {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+
+  // chunk `sub` of tile T: M-tile mt covers tile positions 32 sub + 16 mt .. + 16, inside one block
+  auto load_chunk = [&](u32x4 (&D)[2 * NLD], const Tile &T, int sub) {
+    const int64_t head_off = (int64_t)(p.group_first + T.h) * p.k_stride_head;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int tpos = sub * CH + 16 * mt;
+      const int id = tpos < bs ? T.id0 : T.id1;  // past the row the tile's first block stands in
+      const char *src = p.keys + (int64_t)id * p.k_stride_block + head_off + (int64_t)(tpos % bs) * p.k_stride_pos;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        uint32_t o = voff[j];
+        asm volatile("" : "+v"(o));  // keeps the scalar-base + 32-bit-offset load form
+        D[mt * NLD + j] = __builtin_nontemporal_load((const u32x4 *)(src + o));
+      }
+    }
+  };
+  // B operand: query row n of the group, the dims k-step s reads (zero past group_rows)
+  auto load_query = [&](u32x4 (&Q)[KS], const Tile &T) {
+    const char *qrow = p.q + (int64_t)T.qtok * p.q_stride_token + (int64_t)((p.group_first + T.h) * G + n) * p.q_stride_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      // 16-bit keys: piece 4s + c (8 dims); fp8 keys: 16-dim piece 4(s/2) + c, half s % 2
+      const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
+      Q[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
+    }
+  };
+  auto stash_chunk = [&](const u32x4 (&L)[2 * NLD]) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) tr[mt * 16 * S::kPieces + tr_slot<S>(j * S::kTPI + row_in, piece)] = L[mt * NLD + j];
+  };
+  auto mma_stashed = [&](const u32x4 (&Q)[KS], f32x4_t (&acc)[2]) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      u32x4 D[NLD];
+#pragma unroll
+      for (int s = 0; s < NLD; ++s) D[s] = tr[mt * 16 * S::kPieces + tr_slot<S>(n, 4 * s + c)];
+      acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (S::kFp8) {
+#pragma unroll
+        for (int s = 0; s < NLD; ++s) {
+          u32x4 lo4, hi4;
+          widen_fp8(D[s], lo4, hi4);
+          acc[mt] = mfma_step<kModeBF16>(lo4, Q[2 * s], acc[mt]);
+          acc[mt] = mfma_step<kModeBF16>(hi4, Q[2 * s + 1], acc[mt]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[s], Q[s], acc[mt]);
+      }
+    }
+  };
+
+  for (long long r0 = u_first; r0 < u_last; r0 += C::kRound) {
+    const int count = (int)min((long long)C::kRound, u_last - r0);
+    // ---- describe the round's tiles, one per thread ------------------------------------
+    if (threadIdx.x < count) {
+      const long long u = r0 + threadIdx.x;
+      const int h = (int)(u / total_tiles);
+      const int t = (int)(u - (long long)h * total_tiles);
+      int lo = 0, hi = rows;  // the row holding tile t: the last row with s_off[row] <= t
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid] <= t) lo = mid; else hi = mid;
+      }
+      const int k = t - s_off[lo];
+      const int nb = (s_len[lo] + bs - 1) / bs;
+      const int32_t *trow = p.table + (int64_t)lo * p.table_stride;
+      const int id0 = trow[kTileBlocks * k];
+      const int id1 = kTileBlocks * k + 1 < nb ? trow[kTileBlocks * k + 1] : id0;
+      s_desc[threadIdx.x] = make_int4(lo | (h << 16), k, id0, id1);
+      s_qtok[threadIdx.x] = p.qrow[lo];
+    }
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+
+    // ---- the waves take the round's tiles -------------------------------------------------
+    int i = take();
+    if (i < count) {
+      Tile T = describe(i);
+      int sub = 0;
+      int ahead = take();  // the tile after T, taken early so its LDS round trip is hidden
+      u32x4 A[2 * NLD], qb[KS], qn[KS];
+      f32x4_t acc[2];
+      load_query(qb, T);
+      load_chunk(A, T, 0);
+      float m_run = -INFINITY, l_run = 0.0f;
+      const bool timed = p.cycles != nullptr;
+      uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
+      uint64_t spent = 0;
+      while (true) {
+        // the chunk after this one: the next part of T, or the first of the tile taken ahead
+        Tile N = T;
+        int nsub_next = sub + 1;
+        bool more = true, new_query = false;
+        if (nsub_next == nsub) {
+          more = ahead < count;
+          if (more) {
+            N = describe(ahead);
+            nsub_next = 0;
+            ahead = take();
+            new_query = N.row != T.row || N.h != T.h;
+          }
+        }
+        stash_chunk(A);  // waits for the chunk
+        if (more) {
+          load_chunk(A, N, nsub_next);
+          if (new_query) load_query(qn, N);
+        }
+        mma_stashed(qb, acc);
+
+        // ---- the chunk's tile max and sum (query row n, tokens 4c + i of each M-tile) ----
+        const int len = s_len[T.row];
+        const int tok0 = T.k * tile_tokens + sub * CH;
+        float sc[8];
+        if (tok0 + CH <= len) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[4 * mt + e] = acc[mt][e] * scale2;
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int tok = tok0 + 16 * mt + 4 * c + e;
+              sc[4 * mt + e] = tok < len ? acc[mt][e] * scale2 : -INFINITY;
+            }
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+        mx = rows_max(mx);
+        // exponents are <= 0 (a score minus a max); v_exp_f32 gives 0 for -inf and for underflow
+        float sum = 0.0f;
+        if (mx != -INFINITY) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
+        }
+        sum = rows_sum(sum);
+        const float M = fmaxf(m_run, mx);
+        if (M != -INFINITY) {
+          const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f(m_run - M);
+          const float b = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f(mx - M);
+          l_run = a + b;
+          m_run = M;
+        }
+        if (sub == nsub - 1) {
+          // the tile's record into each of its blocks the row reaches, runtime/audit_kernel.py:97-109
+          // (lanes of token quads 0 and 1 take blocks 2k and 2k + 1)
+          const int blk = kTileBlocks * T.k + c;
+          if (c < kTileBlocks && n < G && blk < (len + bs - 1) / bs) {
+            float *cell = p.lse + (int64_t)T.row * p.row_stride + T.h * G + (int64_t)blk * p.cells + n;
+            cell[0] = m_run * kLn2;
+            cell[p.plane_stride] = l_run;
+          }
+          m_run = -INFINITY;
+          l_run = 0.0f;
+          if (timed) {
+            // the wave's time since its previous tile goes to this tile's row (first KV head)
+            const uint64_t now = __builtin_amdgcn_s_memtime();
+            if (T.h == 0 && T.row < p.cycles_rows) spent += now - mark;
+            mark = now;
+            if (spent != 0 && (!more || N.row != T.row || N.h != T.h)) {
+              if (lane == 0) atomicAdd((unsigned long long *)(p.cycles + T.row), (unsigned long long)spent);
+              spent = 0;
+            }
+          }
+        }
+        if (!more) break;
+        if (new_query) {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) qb[s] = qn[s];
+        }
+        T = N;
+        sub = nsub_next;
+      }
+    }
+    __syncthreads();  // the next round rewrites the descriptors and the counter
   }
 }
 
@@ -741,12 +1053,17 @@ KernelFn pick_hd(int hd, int nl, int gp) {
 
 constexpr bool kMfmaNontemporal = true;
 
+// key rows of up to 256 bytes: the per-CU kernel; 512-byte rows (16-bit keys, d = 256): the
+// per-wave kernel, whose staging fits 512-byte rows
 template <int MODE>
 KernelFn pick_mfma_hd(int hd) {
+  constexpr bool kFp8 = MODE == kModeFp8Bf16;
   switch (hd) {
-    case 64: return tile_lse_mfma_kernel<MODE, 64, kMfmaNontemporal>;
-    case 128: return tile_lse_mfma_kernel<MODE, 128, kMfmaNontemporal>;
-    case 256: return tile_lse_mfma_kernel<MODE, 256, kMfmaNontemporal>;
+    case 64: return tile_lse_cu_kernel<MODE, 64>;
+    case 128: return tile_lse_cu_kernel<MODE, 128>;
+    case 256:
+      if constexpr (kFp8) return tile_lse_cu_kernel<MODE, 256>;
+      else return tile_lse_mfma_kernel<MODE, 256, kMfmaNontemporal>;
   }
   return nullptr;
 }
@@ -770,8 +1087,9 @@ KernelFn pick(int mode, int hd, int nl, int gp) {
   return nullptr;
 }
 
-// Workgroups of `fn` one compute unit holds at once with `lds` bytes of dynamic LDS (cached).
-int resident_blocks(KernelFn fn, size_t lds) {
+// Workgroups of `fn` one compute unit holds at once with `lds` bytes of dynamic LDS and
+// `threads` threads per workgroup (cached; 0 when one does not fit).
+int resident_blocks(KernelFn fn, size_t lds, int threads) {
   struct Entry {
     KernelFn fn;
     size_t lds;
@@ -784,10 +1102,10 @@ int resident_blocks(KernelFn fn, size_t lds) {
   for (int i = 0; i < used; ++i)
     if (cache[i].fn == fn && cache[i].lds == lds) return cache[i].blocks;
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), kThreads, lds) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(fn), threads, lds) !=
           hipSuccess ||
-      n < 1)
-    n = 2;
+      n < 0)
+    n = 0;
   if (used < 64) cache[used++] = Entry{fn, lds, n};
   return n;
 }
@@ -828,7 +1146,7 @@ extern "C" int ekv_audit_tile_lse(
                 rows, kMaxRows, width, block_size, layer);
   if (group_rows < 1 || group_rows > 16)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d query rows per KV head; at most 16 are recorded", group_rows);
-  if (groups < 1 || group_first < 0 || cells < groups * group_rows)
+  if (groups < 1 || groups > 32767 || group_first < 0 || cells < groups * group_rows)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d groups from %d need %d cells per block, the plane has %d",
                 groups, group_first, groups * group_rows, cells);
   if (((kTileBlocks * block_size) & (kTileBlocks * block_size - 1)) != 0)
@@ -857,9 +1175,11 @@ extern "C" int ekv_audit_tile_lse(
                         tile_tokens % 32 == 0;
   KernelFn fn = nullptr;
   int nsub = 1;
+  int threads = kThreads;  // per workgroup
   if (use_mfma) {
     fn = pick_mfma(mode, head_dim);
     nsub = tile_tokens / 32;
+    if (row_bytes <= 256) threads = kCuThreads;
   } else {
     // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
     // instruction must sit inside one block, and a chunk inside one tile.
@@ -880,6 +1200,10 @@ extern "C" int ekv_audit_tile_lse(
   const uint64_t qaddr = (uint64_t)q | (uint64_t)(q_stride_token * qbytes) | (uint64_t)(q_stride_head * qbytes);
   if ((kaddr & 15) != 0 || (qaddr & 15) != 0)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: key and query rows must be 16-byte aligned");
+  // the MFMA form addresses the 16 positions of an M-tile with 32-bit lane offsets
+  if (use_mfma && (k_stride_pos <= 0 || 16 * k_stride_pos * kbytes + row_bytes > ((int64_t)1 << 31)))
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: key position stride %lld (positive, 16 positions in 2 GiB)",
+                (long long)k_stride_pos);
 
   Params p;
   p.q = (const char *)q;
@@ -919,10 +1243,15 @@ extern "C" int ekv_audit_tile_lse(
   const size_t lds = (size_t)(use_mfma ? 2 * rows + 1 : rows + 1) * sizeof(int);
   const int64_t max_tiles = (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks) * groups;
   const int64_t min_per_wave = p.chunk_tiles;
-  int64_t blocks = (max_tiles + min_per_wave * kWaves - 1) / (min_per_wave * kWaves);
-  const int64_t cap = (int64_t)cu_count() * resident_blocks(fn, lds);
+  const int waves = threads / kWave;
+  int64_t blocks = (max_tiles + min_per_wave * waves - 1) / (min_per_wave * waves);
+  const int resident = resident_blocks(fn, lds, threads);
+  if (resident < 1)
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: a workgroup of %d threads with %zu bytes of row data does "
+                "not fit a compute unit (rows %d)", threads, lds, rows);
+  const int64_t cap = (int64_t)cu_count() * resident;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), lds, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), lds, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_audit_tile_lse launch");
 }

@@ -31,6 +31,49 @@ __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
+// Max / sum over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48), every lane
+// receiving the result, on the VALU with no LDS round trip.  v_permlane16_swap of a register with
+// a copy of itself returns rows (0, 0, 2, 2) and rows (1, 1, 3, 3); v_permlane32_swap returns the
+// low half twice and the high half twice.  Each step combines the two results, so every lane gets
+// the same bits as the xor-16 then xor-32 butterfly.
+//
+// Both the operand copy and the two results pass through empty asm statements.  Without them this
+// compiler folds the exchange: given one value for both operands it takes the results to be equal,
+// and where the two results meet in one expression it reads the first result twice (both seen in
+// the generated code; the parity tests of every kernel that uses these catch either).
+__device__ __forceinline__ void row_swap16(float v, float &a, float &b) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  uint32_t y = x;
+  asm volatile("" : "+v"(y));
+  const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+  uint32_t r0 = r[0], r1 = r[1];
+  asm volatile("" : "+v"(r0), "+v"(r1));
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void row_swap32(float v, float &a, float &b) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  uint32_t y = x;
+  asm volatile("" : "+v"(y));
+  const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+  uint32_t r0 = r[0], r1 = r[1];
+  asm volatile("" : "+v"(r0), "+v"(r1));
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float rows_max(float v) {
+  float a, b;
+  row_swap16(v, a, b);
+  row_swap32(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  float a, b;
+  row_swap16(v, a, b);
+  row_swap32(a + b, a, b);
+  return a + b;
+}
+
 // Sum / max over all 64 lanes; every lane receives the result.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
