@@ -157,6 +157,8 @@ class Step:
         self.plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
         R, W = batch.rows, batch.width
         self.shares = torch.empty(R, W, dtype=torch.float32, device=dev)
+        need = int(self.ekv.load().ekv_tile_shares_workspace(R, W, LAYERS))
+        self.shares_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
         self.keep = torch.empty(R, W, dtype=torch.uint8, device=dev)
         self.summary = torch.zeros(6, dtype=torch.int64, device=dev)
         self.view = torch.zeros(R, W, dtype=torch.int32, device=dev)
@@ -183,8 +185,9 @@ class Step:
         b, p = self.batch, self.plane
         plane_stride, layer_stride, row_stride = p.strides
         self.ekv.call(
-            "ekv_tile_shares", p.lse_address, plane_stride, layer_stride, row_stride, LAYERS, p.cells, b.width,
-            0, self.blocks.data_ptr(), b.rows, 2, self.ekv.AGG_MEAN, self.shares.data_ptr(), b.width, stream,
+            "ekv_tile_shares_ws", p.lse_address, plane_stride, layer_stride, row_stride, LAYERS, p.cells, b.width,
+            0, self.blocks.data_ptr(), b.rows, 2, self.ekv.AGG_MEAN, self.shares.data_ptr(), b.width,
+            self.shares_ws.data_ptr(), self.shares_ws.numel(), stream,
         )
         self.rank_view(stream)
 
@@ -402,8 +405,9 @@ def main() -> None:
     audit_ms = a0.elapsed_time(a1) / (reps * LAYERS)
     # the other stages of the step
     shares_ms = float(np.median(time_events(lambda: step.ekv.call(
-        "ekv_tile_shares", step.plane.lse_address, *step.plane.strides, LAYERS, step.plane.cells, batch.width, 0,
-        step.blocks.data_ptr(), batch.rows, 2, step.ekv.AGG_MEAN, step.shares.data_ptr(), batch.width, handle),
+        "ekv_tile_shares_ws", step.plane.lse_address, *step.plane.strides, LAYERS, step.plane.cells, batch.width, 0,
+        step.blocks.data_ptr(), batch.rows, 2, step.ekv.AGG_MEAN, step.shares.data_ptr(), batch.width,
+        step.shares_ws.data_ptr(), step.shares_ws.numel(), handle),
         20, stream)))
     view_ms = float(np.median(time_events(lambda: step.rank_view(handle), 20, stream)))
 

@@ -108,6 +108,21 @@ int ekv_tile_shares(const float *lse, int64_t lse_plane_stride, int64_t lse_laye
                     void *stream);
 
 /*
+ * ekv_tile_shares with a workspace, the same result (the same rules; float sums in another
+ * fixed order): each row's layers are split over several workgroups, which write per-block
+ * partial sums into the workspace, and a second kernel combines them, so a long row no longer
+ * sets the time on one compute unit.  Replaces the same reference code as ekv_tile_shares.
+ * workspace: ekv_tile_shares_workspace(nrows, width, layers) bytes of device memory the call
+ * may overwrite (no initial contents needed; calls that share one workspace must not overlap).
+ */
+size_t ekv_tile_shares_workspace(int32_t nrows, int32_t width, int32_t layers);
+int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
+                       int64_t lse_row_stride, int32_t layers, int32_t cells, int32_t width,
+                       const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
+                       int32_t tile_blocks, int32_t aggregate, float *shares, int64_t shares_stride,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * The same normalisation from u values already formed, u[layer][row][block][cell]
  * (normalize_tile_lse's own input, observe/tile_shares.py:58-103).
  */

@@ -14,27 +14,33 @@
 // carries weight -- iff m is finite and 0 < l < inf.  With u planes (ekv_normalize_tile_lse),
 // m = u and l = 1.
 //
-// One workgroup of 16 waves per output row.  Phase 1: wave w takes layers w, w + 16, ...; for
-// each it streams the row's [width][cells] records (coalesced; when the cells come in 16-byte
-// quads, as for a group of 4 query rows, a lane loads a block's quad at once; 8 loads of each
-// plane in flight per lane) and keeps a running (max m, sum w exp(m - max)) per cell, which a
-// butterfly over the lanes holding the same cells turns into the record's peak and total, kept
-// in LDS.  Phase 2: the row's blocks x layer groups are spread over all 16 waves; each thread
-// sums (or maxes) its block's shares over its layers and query rows in a fixed order, and the
-// group partials are combined in LDS in a fixed order, so the result is deterministic (no
-// atomics) and the same on every call.
+// A workgroup takes one output row and a range of its layers.  Phase 1: the layers are spread over
+// the waves; for each the row's [width][cells] records are streamed (coalesced; when the cells
+// come in 16-byte quads, as for a group of 4 query rows, a lane loads a block's quad at once; 8
+// loads of each plane in flight per lane) with a running (max m, sum w exp(m - max)) per cell,
+// which a butterfly over the lanes holding the same cells turns into the record's peak and total,
+// kept in LDS.  Phase 2: the row's blocks x layer groups are spread over the workgroup; each
+// thread sums (or maxes) its block's shares over its layers and query rows in a fixed order, and
+// the group partials are combined in LDS in a fixed order.
+//
+// Two forms.  Without a workspace one 1024-thread workgroup takes a whole row, so the longest row
+// sets the time (its records are read twice by one CU).  With a workspace (ekv_tile_shares_ws)
+// the layers are split into K groups, (row, group) workgroups of 256 threads write per-block
+// partial sums (or maxes) and their contributor counts, and a second kernel combines each row's K
+// partials in group order.  Both are deterministic (no atomics) and the same on every call.
 #include <limits.h>
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "ekv_common.hpp"
 
 namespace ekv {
 namespace shares {
 
-constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / kWave;
+constexpr int kThreads = 1024;      // a whole row per workgroup
+constexpr int kSplitThreads = 256;  // a (row, layer group) per workgroup
 constexpr int kBatch = 8;  // quads (or cells) of each plane in flight per lane
 constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
@@ -49,6 +55,9 @@ struct Params {
   int32_t lanes_per_layer;  // the peak pass's lanes per layer (quads path)
   float *shares;
   int64_t shares_stride;
+  int32_t groups;      // layer groups per row (the split form), 1 otherwise
+  float *part;         // split form: [rows][groups][width] partial sums (or maxes)
+  int32_t *part_count; // split form: [rows][groups] contributing (layer, query row) pairs
 };
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -104,14 +113,19 @@ __device__ __forceinline__ void absorb(float &mx, float &sum, const float (&m)[N
 // VEC: the cells of a block come in 16-byte quads (cells a multiple of 4, cells / 4 a power of
 // two, 16-byte aligned planes and strides), so one lane loads a quad with one instruction and
 // quad e of a (layer, row) record is at 4 e.  Otherwise every cell is loaded on its own.
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
+template <bool VEC, int NT, bool SPLIT>
+__global__ __launch_bounds__(NT) void shares_kernel(const Params p) {
+  constexpr int kWaves = NT / kWave;
   extern __shared__ float s_stats[];  // [layers][cells_pow2] peak, then [layers][cells_pow2] 1/total
-  __shared__ float s_part[kThreads];  // per (layer group, block) partial shares
+  __shared__ float s_part[NT];        // per (layer group, block) partial shares
   __shared__ float s_red[kWaves];
   __shared__ int s_contrib;
 
-  const int out_row = blockIdx.x;
+  const int out_row = SPLIT ? blockIdx.x / p.groups : blockIdx.x;
+  const int group = SPLIT ? blockIdx.x - out_row * p.groups : 0;
+  // this workgroup's layers [l_first, l_first + nl); stats are indexed from l_first
+  const int l_first = SPLIT ? group * p.layers / p.groups : 0;
+  const int nl = SPLIT ? (group + 1) * p.layers / p.groups - l_first : p.layers;
   const int src_row = p.row_ids != nullptr ? p.row_ids[out_row] : out_row;
   const int n_row = p.row_blocks != nullptr ? max(p.row_blocks[out_row], 0) : p.width;
   const int n = min(n_row, p.width);  // blocks with records
@@ -119,9 +133,11 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   const int cells = p.cells;
   const RowWeight weight(p, n_row);
   const int64_t row_base = (int64_t)src_row * p.row_stride;
-  const float *lplane = weight.from_u ? p.m : p.l;  // never read through when from_u
+  // the l plane; for u input the m plane again (loaded unconditionally, so that no load waits for
+  // another; the weight ignores it)
+  const float *lplane = weight.from_u ? p.m : p.l;
   float *peak = s_stats;
-  float *inv_total = s_stats + p.layers * CP;
+  float *inv_total = s_stats + nl * CP;
   if (threadIdx.x == 0) s_contrib = 0;
   __syncthreads();
 
@@ -139,11 +155,11 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
     const int LPL = p.lanes_per_layer;                       // a power of two, QP <= LPL <= 64
     const int sub = lane & (LPL - 1);
     const int slot = sub & (QP - 1);  // the quad of the block every element of this lane is in
-    const int slots = kThreads / LPL;  // layers reduced at once by the workgroup
+    const int slots = NT / LPL;  // layers reduced at once by the workgroup
     const int quads = n * QP;
-    for (int layer = (tid / LPL); layer - (tid / LPL) < p.layers; layer += slots) {
-      const bool live = layer < p.layers;
-      const int64_t base = (live ? layer : 0) * p.layer_stride + row_base;
+    for (int layer = (tid / LPL); layer - (tid / LPL) < nl; layer += slots) {
+      const bool live = layer < nl;
+      const int64_t base = (int64_t)(l_first + (live ? layer : 0)) * p.layer_stride + row_base;
       const f32x4_t *mq = reinterpret_cast<const f32x4_t *>(p.m + base);
       const f32x4_t *lq = reinterpret_cast<const f32x4_t *>(lplane + base);
       float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -153,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
         for (int k = 0; k < kBatch; ++k) {
           const int at = e0 + k * LPL < quads ? e0 + k * LPL : 0;
           mv[k] = mq[at];
-          lv[k] = weight.from_u ? mv[k] : lq[at];
+          lv[k] = lq[at];  // the m plane again for u input (its weight ignores it)
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -190,9 +206,9 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   } else {
     const int q = lane & (CP - 1);  // every element a lane visits has this query row (CP divides 64)
     const int span = n * CP;
-    for (int layer = wave; layer < p.layers; layer += kWaves) {
-      const float *mrow = p.m + layer * p.layer_stride + row_base;
-      const float *lrow = lplane + layer * p.layer_stride + row_base;
+    for (int layer = wave; layer < nl; layer += kWaves) {
+      const float *mrow = p.m + (int64_t)(l_first + layer) * p.layer_stride + row_base;
+      const float *lrow = lplane + (int64_t)(l_first + layer) * p.layer_stride + row_base;
       float mx = -INFINITY, sum = 0.0f;
       if (q < cells) {
         for (int e0 = lane; e0 < span; e0 += kWave * kBatch) {
@@ -202,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
             const int e = e0 + k * kWave;
             const int idx = e < span ? (e >> cp_log2) * cells + q : 0;
             m[k] = mrow[idx];
-            w[k] = weight.from_u ? m[k] : lrow[idx];
+            w[k] = lrow[idx];
           }
 #pragma unroll
           for (int k = 0; k < kBatch; ++k) {
@@ -231,14 +247,21 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
   const int contributors = s_contrib;
 
   float *out = p.shares + (int64_t)out_row * p.shares_stride;
-  if (contributors == 0) {  // no evidence about the row, tile_shares.py:103
-    for (int b = tid; b < p.width; b += kThreads) out[b] = NAN;
+  if constexpr (SPLIT) {
+    if (tid == 0) p.part_count[(int64_t)out_row * p.groups + group] = contributors;
+    if (contributors == 0) {  // nothing from these layers: zero partials
+      float *part = p.part + ((int64_t)out_row * p.groups + group) * p.width;
+      for (int b = tid; b < p.width; b += NT) part[b] = 0.0f;
+      return;
+    }
+  } else if (contributors == 0) {  // no evidence about the row, tile_shares.py:103
+    for (int b = tid; b < p.width; b += NT) out[b] = NAN;
     return;
   }
 
   // ---- phase 2: per-block shares, summed (or maxed) over (layer, query row) in a fixed order
   const bool use_max = p.aggregate == EKV_AGG_MAX;
-  // block b's shares over layers [l0, l1)
+  // block b's shares over layers [l0, l1) of this workgroup's range (stats index)
   auto shares_of = [&](int b, int l0, int l1) -> float {
     float acc = 0.0f;
     const int64_t block_base = row_base + (int64_t)b * cells;
@@ -250,9 +273,9 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
           const int rq = r0 + k < r_end ? r0 + k : r0;
-          const int64_t at = (rq >> qp_log2) * p.layer_stride + block_base + 4 * (rq & (QP - 1));
+          const int64_t at = (int64_t)(l_first + (rq >> qp_log2)) * p.layer_stride + block_base + 4 * (rq & (QP - 1));
           mv[k] = *reinterpret_cast<const f32x4_t *>(p.m + at);
-          lv[k] = weight.from_u ? mv[k] : *reinterpret_cast<const f32x4_t *>(lplane + at);
+          lv[k] = *reinterpret_cast<const f32x4_t *>(lplane + at);
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
@@ -276,10 +299,10 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
         for (int k = 0; k < kBatch; ++k) {
           const int rec = r0 + k < r_end ? r0 + k : r0;
           const int layer = rec / cells, c = rec - layer * cells;
-          const int64_t at = layer * p.layer_stride + block_base + c;
+          const int64_t at = (int64_t)(l_first + layer) * p.layer_stride + block_base + c;
           stat[k] = layer * CP + c;
           mv[k] = p.m[at];
-          lv[k] = weight.from_u ? mv[k] : lplane[at];
+          lv[k] = lplane[at];
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
@@ -293,38 +316,249 @@ __global__ __launch_bounds__(kThreads) void shares_kernel(const Params p) {
     return acc;
   };
 
-  // the row's n blocks (rounded up to whole waves) times LG layer groups fill the workgroup
+  // the row's n blocks (rounded up to whole waves) times LG layer groups fill the workgroup;
+  // the split form writes its sums (or maxes) over its layers, the whole-row form the shares
+  float *part = SPLIT ? p.part + ((int64_t)out_row * p.groups + group) * p.width : nullptr;
   const int NC = ((n + kWave - 1) / kWave) * kWave;
-  const int LG = NC >= kThreads ? 1 : min(kThreads / NC, p.layers);
+  const int LG = NC >= NT ? 1 : min(NT / NC, nl);
   float local_total = 0.0f;
   if (LG > 1) {
     const int g = tid / NC, col = tid - g * NC;
     float acc = 0.0f;
-    if (g < LG && col < n) acc = shares_of(col, g * p.layers / LG, (g + 1) * p.layers / LG);
+    if (g < LG && col < n) acc = shares_of(col, g * nl / LG, (g + 1) * nl / LG);
     s_part[tid] = acc;  // = s_part[g * NC + col]
     __syncthreads();
-    for (int b = tid; b < p.width; b += kThreads) {
+    for (int b = tid; b < p.width; b += NT) {
       float v = 0.0f;
       if (b < n) {
         for (int h = 0; h < LG; ++h) v = use_max ? fmaxf(v, s_part[h * NC + b]) : v + s_part[h * NC + b];
       }
       local_total += v;
-      out[b] = use_max ? v : v / (float)contributors;
+      if constexpr (SPLIT) part[b] = v;
+      else out[b] = use_max ? v : v / (float)contributors;
     }
   } else {
-    for (int b = tid; b < p.width; b += kThreads) {
-      const float v = b < n ? shares_of(b, 0, p.layers) : 0.0f;
+    for (int b = tid; b < p.width; b += NT) {
+      const float v = b < n ? shares_of(b, 0, nl) : 0.0f;
       local_total += v;
-      out[b] = use_max ? v : v / (float)contributors;
+      if constexpr (SPLIT) part[b] = v;
+      else out[b] = use_max ? v : v / (float)contributors;
     }
   }
-  if (use_max) {  // renormalise the per-block max, tile_shares.py:97-100
-    const float total = block_sum<kThreads>(local_total, s_red);
-    for (int b = tid; b < p.width; b += kThreads) out[b] = total > 0.0f ? out[b] / total : 0.0f;
+  if (!SPLIT && use_max) {  // renormalise the per-block max, tile_shares.py:97-100
+    const float total = block_sum<NT>(local_total, s_red);
+    for (int b = tid; b < p.width; b += NT) out[b] = total > 0.0f ? out[b] / total : 0.0f;
   }
 }
 
-int launch(Params p, int nrows, void *stream) {
+// Transpose reduction of a[0 .. CUR) over the lanes: each step halves the values a lane carries
+// (the lane with the mask bit keeps the upper half and receives its partner's), so CUR values take
+// CUR - 1 shuffles and then sit one per lane; the remaining masks finish the reduction.
+template <int CUR, int MASK, int N, bool MAX>
+__device__ __forceinline__ void transpose_reduce(float (&a)[N], int lane) {
+  if constexpr (MASK >= 1) {
+    if constexpr (CUR > 1) {
+      constexpr int kHalf = CUR / 2;
+      const bool upper = (lane & MASK) != 0;
+#pragma unroll
+      for (int k = 0; k < kHalf; ++k) {
+        const float send = upper ? a[k] : a[k + kHalf];
+        const float keep = upper ? a[k + kHalf] : a[k];
+        const float got = shfl_xor(send, MASK);
+        a[k] = MAX ? fmaxf(keep, got) : keep + got;
+      }
+      transpose_reduce<kHalf, MASK / 2, N, MAX>(a, lane);
+    } else {
+      const float got = shfl_xor(a[0], MASK);
+      a[0] = MAX ? fmaxf(a[0], got) : a[0] + got;
+      transpose_reduce<1, MASK / 2, N, MAX>(a, lane);
+    }
+  }
+}
+
+// The split form for quads of 4 cells and rows of at most 256 J blocks: one pass over memory.
+// Thread t keeps blocks t + 256 j (j < J) of each of the group's NL layers in registers, the peak
+// and total of each (layer, query row) are workgroup reductions over them (butterflies, then the
+// waves' results in LDS in wave order), and the block's partial is formed from the same registers.
+template <int J, int NL>
+__global__ __launch_bounds__(kSplitThreads) void shares_reg_kernel(const Params p) {
+  constexpr int NT = kSplitThreads, NW = NT / kWave, V = NL * 4;  // V: the group's (layer, cell) pairs
+  static_assert(V <= kWave && (V & (V - 1)) == 0, "a power of two of pairs, at most a wave");
+  __shared__ float s_red[NW][V];
+  const int out_row = blockIdx.x / p.groups;
+  const int group = blockIdx.x - out_row * p.groups;
+  const int l_first = group * p.layers / p.groups;
+  const int nl = (group + 1) * p.layers / p.groups - l_first;  // <= NL
+  const int src_row = p.row_ids != nullptr ? p.row_ids[out_row] : out_row;
+  const int n_row = p.row_blocks != nullptr ? max(p.row_blocks[out_row], 0) : p.width;
+  const int n = min(n_row, p.width);
+  const RowWeight weight(p, n_row);
+  const int64_t row_base = (int64_t)src_row * p.row_stride;
+  const float *lplane = weight.from_u ? p.m : p.l;
+  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
+
+  // the thread's records: m and the weight w (0: the record carries none).  Every load is issued
+  // before any is used, so all are in flight at once; an absent record (past the row or the
+  // group) reads the row's first record, which costs no memory traffic, and is masked afterwards.
+  f32x4_t mv[J][NL], wv[J][NL];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int li = 0; li < NL; ++li) {
+      const int b = t + NT * j;
+      const bool live = b < n && li < nl;
+      const int64_t at = live ? (int64_t)(l_first + li) * p.layer_stride + row_base + 4 * (int64_t)b
+                              : (int64_t)l_first * p.layer_stride + row_base;
+      mv[j][li] = *reinterpret_cast<const f32x4_t *>(p.m + at);
+      wv[j][li] = *reinterpret_cast<const f32x4_t *>(lplane + at);
+    }
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int li = 0; li < NL; ++li) {
+      const bool live = t + NT * j < n && li < nl;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        wv[j][li][c] = live ? weight(mv[j][li][c], wv[j][li][c], t + NT * j) : 0.0f;
+        mv[j][li][c] = live ? mv[j][li][c] : -INFINITY;
+      }
+    }
+
+  // a workgroup-wide max or sum of v[0 .. V); every thread gets the results: a transpose
+  // reduction in each wave (value lane / (64 / V) ends in that lane), then the waves' results
+  // meet in LDS in wave order
+  auto reduce = [&](float (&v)[V], auto max_tag) {
+    constexpr bool is_max = decltype(max_tag)::value;
+    transpose_reduce<V, kWave / 2, V, is_max>(v, lane);
+    constexpr int kLanesPerValue = kWave / V;
+    if ((lane & (kLanesPerValue - 1)) == 0) s_red[wave][lane / kLanesPerValue] = v[0];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      float r = s_red[0][k];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) r = is_max ? fmaxf(r, s_red[w][k]) : r + s_red[w][k];
+      v[k] = r;
+    }
+    __syncthreads();
+  };
+
+  // ---- phase 1: peak M and total T of each (layer, query row) ----------------------------
+  float peak[V], total[V];
+#pragma unroll
+  for (int li = 0; li < NL; ++li)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < J; ++j) mx = wv[j][li][c] > 0.0f ? fmaxf(mx, mv[j][li][c]) : mx;
+      peak[li * 4 + c] = mx;
+    }
+  reduce(peak, std::true_type{});
+#pragma unroll
+  for (int li = 0; li < NL; ++li)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        sum += wv[j][li][c] > 0.0f ? wv[j][li][c] * __expf(mv[j][li][c] - peak[li * 4 + c]) : 0.0f;
+      total[li * 4 + c] = sum;
+    }
+  reduce(total, std::false_type{});
+  int contributors = 0;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    contributors += peak[k] != -INFINITY ? 1 : 0;
+    total[k] = 1.0f / total[k];  // now 1 / T (used only where T > 0)
+  }
+
+  // ---- phase 2: the block's partial over the group's pairs --------------------------------
+  const bool use_max = p.aggregate == EKV_AGG_MAX;
+  float *part = p.part + ((int64_t)out_row * p.groups + group) * p.width;
+  if (t == 0) p.part_count[(int64_t)out_row * p.groups + group] = contributors;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int b = t + NT * j;
+    if (b >= p.width) continue;
+    float acc = 0.0f;
+#pragma unroll
+    for (int li = 0; li < NL; ++li)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float w = wv[j][li][c];  // > 0 only where phase 1 found a peak
+        const float share = w > 0.0f ? w * __expf(mv[j][li][c] - peak[li * 4 + c]) * total[li * 4 + c] : 0.0f;
+        acc = use_max ? fmaxf(acc, share) : acc + share;
+      }
+    part[b] = acc;
+  }
+}
+
+// The split form's second kernel: one workgroup per row combines the row's K partials in group
+// order, then applies the whole-row rules (NaN without evidence, the mean over contributing
+// pairs, or the max renormalised over the row).
+__global__ __launch_bounds__(kSplitThreads) void combine_kernel(const Params p) {
+  constexpr int NT = kSplitThreads;
+  __shared__ float s_red[NT / kWave];
+  const int row = blockIdx.x;
+  const int K = p.groups;
+  const float *part = p.part + (int64_t)row * K * p.width;
+  float *out = p.shares + (int64_t)row * p.shares_stride;
+  int contributors = 0;
+  for (int g0 = 0; g0 < K; g0 += kBatch) {  // kBatch counts in flight
+    int c[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) c[k] = g0 + k < K ? p.part_count[(int64_t)row * K + g0 + k] : 0;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) contributors += c[k];
+  }
+  if (contributors == 0) {  // no evidence about the row, tile_shares.py:103
+    for (int b = threadIdx.x; b < p.width; b += NT) out[b] = NAN;
+    return;
+  }
+  const bool use_max = p.aggregate == EKV_AGG_MAX;
+  float local_total = 0.0f;
+  for (int b = threadIdx.x; b < p.width; b += NT) {
+    float v = 0.0f;
+    for (int g0 = 0; g0 < K; g0 += kBatch) {  // kBatch partials in flight, added in group order
+      float x[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) x[k] = g0 + k < K ? part[(int64_t)(g0 + k) * p.width + b] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) v = use_max ? fmaxf(v, x[k]) : v + x[k];
+    }
+    local_total += v;
+    out[b] = use_max ? v : v / (float)contributors;
+  }
+  if (use_max) {  // renormalise the per-block max, tile_shares.py:97-100
+    const float total = block_sum<NT>(local_total, s_red);
+    for (int b = threadIdx.x; b < p.width; b += NT) out[b] = total > 0.0f ? out[b] / total : 0.0f;
+  }
+}
+
+// The split form's groups per row: enough (row, group) workgroups to cover the GPU about twice,
+// at most one per layer.
+#ifndef EKV_SHARES_WAVES_PER_CU
+#define EKV_SHARES_WAVES_PER_CU 2
+#endif
+int split_groups(int nrows, int layers) {
+  if (nrows < 1) return 1;
+  const int want = (EKV_SHARES_WAVES_PER_CU * cu_count() + nrows - 1) / nrows;
+  return std::max(1, std::min(want, layers));
+}
+
+// (sized for one group per layer, the most either split form takes)
+size_t split_workspace(int nrows, int width, int layers) {
+  const size_t parts = (size_t)nrows * layers * width * sizeof(float);
+  return ((parts + 255) / 256) * 256 + (size_t)nrows * layers * sizeof(int32_t);
+}
+
+// the register form's layers per group for J blocks per thread (at most 12 quads of each plane)
+constexpr int reg_layers(int J) { return J == 1 ? 8 : (J == 4 ? 2 : 4); }
+
+// workspace null: one workgroup per row; otherwise the split form (workspace_bytes at least
+// split_workspace(nrows, width, layers))
+int launch(Params p, int nrows, void *workspace, size_t workspace_bytes, void *stream) {
   if (p.cells < 1 || p.cells > kMaxCells)
     return fail(EKV_EUNSUPPORTED, "tile shares: %d cells per block (at most %d)", p.cells, kMaxCells);
   if (p.layers < 1 || p.width < 1 || p.tile_blocks < 1 || nrows < 0)
@@ -340,21 +574,60 @@ int launch(Params p, int nrows, void *stream) {
   if ((int64_t)p.layers * cp > kMaxStats)
     return fail(EKV_EUNSUPPORTED, "tile shares: %d layers x %d cells exceed the %d statistics kept per row",
                 p.layers, cp, kMaxStats);
+  if (workspace != nullptr && workspace_bytes < split_workspace(nrows, p.width, p.layers))
+    return fail(EKV_EINVAL, "tile shares: workspace of %zu bytes, %zu needed", workspace_bytes,
+                split_workspace(nrows, p.width, p.layers));
   if (nrows == 0) return EKV_OK;
-  const size_t lds = (size_t)2 * p.layers * cp * sizeof(float);
+  const bool split = workspace != nullptr;
+  const int NT = split ? kSplitThreads : kThreads;
+  p.groups = split ? split_groups(nrows, p.layers) : 1;
+  const int group_layers = (p.layers + p.groups - 1) / p.groups;  // the largest group
+  if (split) {
+    const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
+    p.part = (float *)workspace;
+    p.part_count = (int32_t *)((char *)workspace + ((parts + 255) / 256) * 256);
+  }
+  const size_t lds = (size_t)2 * group_layers * cp * sizeof(float);
   const bool aligned = ((uintptr_t)p.m % 16) == 0 && (p.from_u || ((uintptr_t)p.l % 16) == 0) &&
                        p.layer_stride % 4 == 0 && p.row_stride % 4 == 0;
   const bool vec = aligned && p.cells % 4 == 0 && cp == p.cells;  // cells / 4 a power of two
   // the peak pass: as many lanes per layer as the workgroup has per layer, a power of two from the
   // quads per block to a wave
   int lpl = kWave;
-  while (lpl > 1 && lpl * p.layers > kThreads) lpl >>= 1;
+  while (lpl > 1 && lpl * group_layers > NT) lpl >>= 1;
   p.lanes_per_layer = std::max(lpl, std::max(cp / 4, 1));
-  if (vec)
-    hipLaunchKernelGGL(shares_kernel<true>, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL(shares_kernel<false>, dim3(nrows), dim3(kThreads), lds, (hipStream_t)stream, p);
-  return check_hip(hipGetLastError(), "tile shares launch");
+  hipStream_t s = (hipStream_t)stream;
+  if (split && vec && p.cells == 4 && p.width <= 4 * kSplitThreads) {
+    // the register form: one pass, J blocks per thread, reg_layers(J) layers per group
+    const int J = (p.width + kSplitThreads - 1) / kSplitThreads;
+    const int NLg = reg_layers(J);
+    p.groups = (p.layers + NLg - 1) / NLg;
+    const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
+    p.part_count = (int32_t *)((char *)workspace + ((parts + 255) / 256) * 256);
+    const unsigned grid = (unsigned)nrows * (unsigned)p.groups;
+    switch (J) {
+      case 1: hipLaunchKernelGGL((shares_reg_kernel<1, reg_layers(1)>), dim3(grid), dim3(kSplitThreads), 0, s, p); break;
+      case 2: hipLaunchKernelGGL((shares_reg_kernel<2, reg_layers(2)>), dim3(grid), dim3(kSplitThreads), 0, s, p); break;
+      case 3: hipLaunchKernelGGL((shares_reg_kernel<3, reg_layers(3)>), dim3(grid), dim3(kSplitThreads), 0, s, p); break;
+      default: hipLaunchKernelGGL((shares_reg_kernel<4, reg_layers(4)>), dim3(grid), dim3(kSplitThreads), 0, s, p); break;
+    }
+    const int rc = check_hip(hipGetLastError(), "tile shares launch");
+    if (rc != EKV_OK) return rc;
+    hipLaunchKernelGGL(combine_kernel, dim3(nrows), dim3(kSplitThreads), 0, s, p);
+    return check_hip(hipGetLastError(), "tile shares combine launch");
+  }
+  if (!split) {
+    if (vec) hipLaunchKernelGGL((shares_kernel<true, kThreads, false>), dim3(nrows), dim3(NT), lds, s, p);
+    else hipLaunchKernelGGL((shares_kernel<false, kThreads, false>), dim3(nrows), dim3(NT), lds, s, p);
+    return check_hip(hipGetLastError(), "tile shares launch");
+  }
+  const unsigned grid = (unsigned)nrows * (unsigned)p.groups;
+  if (vec) hipLaunchKernelGGL((shares_kernel<true, kSplitThreads, true>), dim3(grid), dim3(NT), lds, s, p);
+  else hipLaunchKernelGGL((shares_kernel<false, kSplitThreads, true>), dim3(grid), dim3(NT), lds, s, p);
+  const int rc = check_hip(hipGetLastError(), "tile shares launch");
+  if (rc != EKV_OK) return rc;
+  hipLaunchKernelGGL(combine_kernel, dim3(nrows), dim3(kSplitThreads), 0, s, p);
+  return check_hip(hipGetLastError(), "tile shares combine launch");
 }
 
 }  // namespace shares
@@ -383,7 +656,37 @@ extern "C" int ekv_tile_shares(const float *lse, int64_t lse_plane_stride, int64
   p.from_u = 0;
   p.shares = shares;
   p.shares_stride = shares_stride;
-  return shares::launch(p, nrows, stream);
+  return shares::launch(p, nrows, nullptr, 0, stream);
+}
+
+extern "C" size_t ekv_tile_shares_workspace(int32_t nrows, int32_t width, int32_t layers) {
+  if (nrows < 0 || width < 1 || layers < 1) return 0;
+  return shares::split_workspace(nrows, width, layers);
+}
+
+extern "C" int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
+                                  int64_t lse_row_stride, int32_t layers, int32_t cells, int32_t width,
+                                  const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
+                                  int32_t tile_blocks, int32_t aggregate, float *shares, int64_t shares_stride,
+                                  void *workspace, size_t workspace_bytes, void *stream) {
+  if (lse == nullptr || shares == nullptr || workspace == nullptr)
+    return fail(EKV_EINVAL, "ekv_tile_shares_ws: null pointer");
+  shares::Params p{};
+  p.m = lse;
+  p.l = lse + lse_plane_stride;
+  p.layer_stride = lse_layer_stride;
+  p.row_stride = lse_row_stride;
+  p.layers = layers;
+  p.cells = cells;
+  p.width = width;
+  p.row_ids = row_ids;
+  p.row_blocks = row_blocks;
+  p.tile_blocks = tile_blocks;
+  p.aggregate = aggregate;
+  p.from_u = 0;
+  p.shares = shares;
+  p.shares_stride = shares_stride;
+  return shares::launch(p, nrows, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row_stride,
@@ -406,5 +709,5 @@ extern "C" int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, in
   p.from_u = 1;
   p.shares = shares;
   p.shares_stride = shares_stride;
-  return shares::launch(p, nrows, stream);
+  return shares::launch(p, nrows, nullptr, 0, stream);
 }

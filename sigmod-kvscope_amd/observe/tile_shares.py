@@ -168,11 +168,14 @@ def tile_shares(
     aggregate: Aggregate = "mean",
     out: torch.Tensor | None = None,
     stream=None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Shares ``float32[len(row_ids), width]`` of the chosen rows straight from the device planes at
     ``base`` (read_tile_rows + normalize_tile_lse fused on the GPU; nothing is copied to the host).
 
-    ``row_ids`` / ``row_blocks`` are int32 device tensors (None: every row / full width)."""
+    ``row_ids`` / ``row_blocks`` are int32 device tensors (None: every row / full width).  The rows'
+    layers are split over several workgroups through a device workspace (``workspace``, a uint8
+    device tensor of at least ``shares_workspace_bytes`` bytes, or one allocated here)."""
     code = _aggregate_code(aggregate)
     n = rows if row_ids is None else int(row_ids.shape[0])
     if out is None:
@@ -183,13 +186,23 @@ def tile_shares(
         if t is not None and (t.dtype != torch.int32 or not t.is_cuda or t.stride(0) != 1):
             raise ValueError("row_ids and row_blocks must be contiguous int32 device tensors")
     layer_stride = rows * width * group_rows
+    need = shares_workspace_bytes(n, width, layers)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=out.device)
+    if workspace.dtype != torch.uint8 or not workspace.is_cuda or workspace.numel() < need:
+        raise ValueError(f"workspace must be a uint8 device tensor of at least {need} bytes")
     ekv_hip.call(
-        "ekv_tile_shares",
+        "ekv_tile_shares_ws",
         int(base), table_layers * layer_stride, layer_stride, width * group_rows, layers, group_rows, width,
         ekv_hip.ptr(row_ids), ekv_hip.ptr(row_blocks), n, int(tile_blocks), code, out.data_ptr(), out.stride(0),
-        ekv_hip.stream_handle(stream),
+        workspace.data_ptr(), workspace.numel(), ekv_hip.stream_handle(stream),
     )
     return out
+
+
+def shares_workspace_bytes(rows: int, width: int, layers: int) -> int:
+    """Device bytes ``tile_shares`` needs as its workspace for ``rows`` output rows."""
+    return int(ekv_hip.load().ekv_tile_shares_workspace(int(rows), int(width), int(layers)))
 
 
 class DeviceTileShareSource:

@@ -121,3 +121,55 @@ def test_device_share_source_reads_only_live_rows(tmp_path, monkeypatch):
     assert np.isnan(got[1]).all()
     want = ots.normalize(ots.read_rows(planes, 2, np.array([0, 2, 3]), 2), row_blocks[[0, 2, 3]], 2)
     assert_close(got[[0, 2, 3]], want, what="device share source")
+
+
+@pytest.mark.parametrize("aggregate", ["mean", "max"])
+@pytest.mark.parametrize("layers,cells,width", [(1, 4, 300), (5, 4, 300), (32, 4, 300), (32, 4, 200), (9, 4, 700),
+                                                (3, 4, 1000), (7, 5, 300), (4, 4, 1100)])
+def test_split_form_matches_the_whole_row_form_and_the_oracle(layers, cells, width, aggregate):
+    # ekv_tile_shares_ws spreads a row's layers over several workgroups and combines their partial
+    # sums (in registers for quads of 4 cells up to 1024 blocks, re-reading the records otherwise);
+    # it must give the whole-row kernel's shares (up to float summation order) and the oracle's
+    import ekv_hip
+
+    rng = np.random.default_rng(40 + layers * 3 + cells + width)
+    table_layers, rows, tile = layers + 1, 11, 2
+    m = rng.normal(0, 3, (table_layers, rows, width, cells)).astype(np.float32)
+    l = rng.uniform(0.5, 30, (table_layers, rows, width, cells)).astype(np.float32)
+    l[rng.random(l.shape) < 0.02] = 0.0
+    m[rng.random(m.shape) < 0.03] = -np.inf
+    m[:, 4] = np.nan  # a row without evidence
+    m[: layers // 2 + 1, 6] = np.nan  # a row with evidence in the later layers only
+    planes = np.stack([m, l])
+    dev = planes_on_device(planes)
+    row_ids = np.array([0, 1, 2, 4, 5, 6, 8, 10])
+    row_blocks = np.array([width, width - 1, 1, 17, width + 3, width // 2, 0, 2])  # tails, past the width, empty
+    ids = torch.from_numpy(row_ids.astype(np.int32)).cuda()
+    blocks = torch.from_numpy(row_blocks.astype(np.int32)).cuda()
+    split = tile_shares.tile_shares(dev.data_ptr(), table_layers, layers, rows, width, cells, ids, blocks, tile,
+                                    aggregate)
+    whole = torch.empty_like(split)
+    layer_stride = rows * width * cells
+    ekv_hip.call("ekv_tile_shares", dev.data_ptr(), table_layers * layer_stride, layer_stride, width * cells, layers,
+                 cells, width, ids.data_ptr(), blocks.data_ptr(), len(row_ids), tile,
+                 ekv_hip.AGG_MAX if aggregate == "max" else ekv_hip.AGG_MEAN, whole.data_ptr(), width,
+                 ekv_hip.stream_handle())
+    torch.cuda.synchronize()
+    got_split = split.cpu().numpy().astype(np.float64)
+    got_whole = whole.cpu().numpy().astype(np.float64)
+    want = ots.normalize(ots.read_rows(planes, layers, row_ids, tile), row_blocks, tile, aggregate)
+    what = f"{layers} layers, {cells} cells, {aggregate}"
+    assert_close(got_split, want, what="split " + what)
+    assert_close(got_whole, want, what="whole row " + what)
+    assert_close(got_split, got_whole, 1e-6, what="split vs whole row " + what)
+
+
+def test_split_form_rejects_a_short_workspace():
+    rng = np.random.default_rng(5)
+    planes = np.stack([rng.normal(0, 2, (2, 4, 64, 4)), rng.uniform(1, 5, (2, 4, 64, 4))]).astype(np.float32)
+    dev = planes_on_device(planes)
+    need = tile_shares.shares_workspace_bytes(4, 64, 2)
+    assert need > 0
+    short = torch.empty(need - 1, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        tile_shares.tile_shares(dev.data_ptr(), 2, 2, 4, 64, 4, None, None, 2, workspace=short)
