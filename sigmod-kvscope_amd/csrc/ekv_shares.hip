@@ -538,12 +538,9 @@ __global__ __launch_bounds__(kSplitThreads) void combine_kernel(const Params p) 
 
 // The split form's groups per row: enough (row, group) workgroups to cover the GPU about twice,
 // at most one per layer.
-#ifndef EKV_SHARES_WAVES_PER_CU
-#define EKV_SHARES_WAVES_PER_CU 2
-#endif
 int split_groups(int nrows, int layers) {
   if (nrows < 1) return 1;
-  const int want = (EKV_SHARES_WAVES_PER_CU * cu_count() + nrows - 1) / nrows;
+  const int want = (2 * cu_count() + nrows - 1) / nrows;
   return std::max(1, std::min(want, layers));
 }
 
