@@ -36,7 +36,7 @@ constexpr int kCuThreads = 768;  // tile_lse_cu_kernel: 12 waves, one workgroup 
 constexpr int kTileBlocks = 2;  // TILE_BLOCKS, runtime/audit_kernel.py:31
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxRows = 6000;  // LDS holds two ints per row and 16 KB of staged records
+constexpr int kMaxRows = 6000;  // LDS holds two ints per row beside the kernels' staging buffers
 
 enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
 
