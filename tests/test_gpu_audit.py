@@ -96,6 +96,26 @@ def test_chunking_does_not_change_a_bit():
         assert np.array_equal(r, results[0], equal_nan=True)
 
 
+def test_workgroup_slices_of_several_rounds():
+    # a large minimum of tiles per wave gives few workgroups, each taking several rounds of 768
+    # described tiles, the rounds crossing rows and KV heads; every record is the default launch's
+    batch = workloads.config2_batch()
+    pool = workloads.device_pool(batch, torch.bfloat16, seed=batch.seed + 3)
+    q = torch.from_numpy(workloads.queries(batch, 1)[0]).to(torch.bfloat16).cuda()
+    table = torch.from_numpy(batch.table).cuda()
+    lens = torch.from_numpy(batch.lens).cuda()
+    scale = batch.head_dim ** -0.5
+    results = []
+    for chunk in (0, 300):
+        plane = RecordingPlane(1, batch.rows, batch.width, batch.group_rows, batch.block_size, kv_heads=batch.kv_heads)
+        flag(plane)
+        results.append(record(plane, 0, table, lens, q, pool[:, 0], scale, chunk_tiles=chunk))
+    assert not np.isnan(results[0][0]).all()
+    assert np.array_equal(results[1], results[0], equal_nan=True)
+    del pool
+    torch.cuda.empty_cache()
+
+
 def test_llama3_8b_decode_shape_one_layer():
     batch = workloads.config2_batch()
     pool = workloads.device_pool(batch, torch.bfloat16, seed=batch.seed)
