@@ -130,6 +130,22 @@ def test_maxmin_float64_scores_zero_rows_and_long_rows():
         assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
 
 
+def test_maxmin_ties_in_rows_sorted_in_lds():
+    # rows of up to 8192 blocks are sorted in LDS (a bitonic sort by share desc, block asc): rows full
+    # of exactly equal shares must keep the stable order the reference's argsort gives
+    rng = np.random.default_rng(9)
+    scores = [np.round(rng.random(n) * 8) / 8 for n in (8192, 4097, 1000, 64)]  # 9 distinct values
+    scores.append(np.full(300, 0.25))
+    scores.append(np.zeros(40))
+    pinned = [oa.default_pins(len(s)) for s in scores]
+    pinned[2] = rng.random(1000) < 0.2
+    total = sum(len(s) for s in scores)
+    for frac in (0.1, 0.4, 0.6, 0.9):
+        budget = max(int(frac * total), sum(int(p.sum()) for p in pinned))
+        reqs = [allocation.Request(scores=s, pinned=p) for s, p in zip(scores, pinned)]
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
+
+
 def test_maxmin_view_build_configuration():
     c = workloads.config4()
     shares, blocks = c["shares"], c["blocks"]
