@@ -806,7 +806,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * p.k_stride_pos + piece * 16);
   const float scale2 = p.scale * kLog2e;  // scores in log2 units: exp(s - m) = exp2(s2 - m2)
 
-  // this workgroup's slice of the flat (head, tile) list
+  // this workgroup's slice of the flat (tile, head) list
   const long long all = (long long)total_tiles * p.groups;
   const long long u_first = all * blockIdx.x / gridDim.x;
   const long long u_last = all * (blockIdx.x + 1) / gridDim.x;
@@ -890,8 +890,10 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
     // ---- describe the round's tiles, one per thread ------------------------------------
     if (threadIdx.x < count) {
       const long long u = r0 + threadIdx.x;
-      const int h = (int)(u / total_tiles);
-      const int t = (int)(u - (long long)h * total_tiles);
+      // tile-major: the audited KV heads of a tile are adjacent, so the waves of a CU read the
+      // heads of the same token rows at about the same time (nearly whole rows for DRAM)
+      const int t = (int)(u / p.groups);
+      const int h = (int)(u - (long long)t * p.groups);
       int lo = 0, hi = rows;  // the row holding tile t: the last row with s_off[row] <= t
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
