@@ -8,15 +8,14 @@
 //    flat list.  Every workgroup builds the per-row tile offsets in LDS from lens/select with a
 //    block scan, so the launch needs no host-side knowledge of the lengths, no scratch memory
 //    and no second kernel; it is identical on every step and can be captured in a graph.
-//  * Three kernels.  16-bit and fp8 keys whose row (one token, one head) is at most 256 bytes
-//    take tile_lse_cu_kernel: one 12-wave workgroup per compute unit, an equal slice of the list
+//  * Two kernels.  16-bit and fp8 keys (d = 64, 128, 256) in blocks of at least 16 tokens take
+//    tile_lse_cu_kernel: one 12-wave workgroup per compute unit, an equal slice of the list
 //    per CU, and the CU's waves share the slice through an LDS counter (a CU serves its loads
 //    about in issue order, so equal per-wave slices leave the last-issued waves finishing last).
-//    512-byte rows (16-bit keys, d = 256) take tile_lse_mfma_kernel, equal per-wave slices.
 //    fp32 keys and blocks under 16 tokens take tile_lse_kernel on the VALU.
 //  * Loads.  A load instruction reads whole key rows (16-byte lanes), the coalesced form that
 //    DRAM serves at the streaming rate whatever the head's offset in the token.
-//  * Dots.  The MFMA kernels compute S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16} after an LDS
+//  * Dots.  The MFMA kernel computes S^T = K Q^T on v_mfma_f32_16x16x32_{bf16,f16} after an LDS
 //    pass that turns whole-row loads into token-per-lane operands; the VALU kernel multiplies
 //    each lane's slice with the query slice (v_dot2 / FMA) and reduces over the lanes of a row.
 //  * Timer.  With a cycles buffer each wave adds its s_memtime durations to cycles[row] with a
@@ -389,10 +388,10 @@ __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
 // v_mfma_f32_16x16x32_{bf16,f16}.  A = keys (M = 16 tokens of one block, K = 32 dims),
 // B = the query group (N = 16 query rows, zero past group_rows), C = scores.  Lane l holds
 // A[token l % 16][dims of piece l / 16] and B[dims of piece l / 16][query row l % 16]; the 16-byte
-// dim pieces are permuted identically in A and B (piece 4s + l / 16 feeds k-step s), so each wave
-// load reads 64 contiguous bytes of each of 16 tokens.  C gives lane l the scores of tokens
-// 4 (l / 16) + i of query row l % 16, so a query row's max / sum over a 32-token chunk is a local
-// reduction of 8 values and two butterfly steps.
+// dim pieces are permuted identically in A and B (piece 4s + l / 16 feeds k-step s), and the
+// keys reach that token-per-lane layout through LDS from whole-row loads.  C gives lane l the
+// scores of tokens 4 (l / 16) + i of query row l % 16, so a query row's max / sum over a chunk
+// is a local reduction of 4 values per M-tile and two swaps across the wave's 16-lane rows.
 // ---------------------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -404,7 +403,6 @@ struct MfmaShape {
   static constexpr int kKBytes = kFp8 ? 1 : 2;
   static constexpr int kSteps = HEAD_DIM / 32;                   // k-steps of 32 dims
   static constexpr int kLoads = kFp8 ? kSteps / 2 : kSteps;      // 16-byte key loads per M-tile
-  static constexpr int kChunk = 32;                              // tokens per chunk: two M-tiles
   static constexpr int kRowBytes = HEAD_DIM * kKBytes;           // one token's key row of one head
   static constexpr int kPieces = kRowBytes / 16;                 // 16-byte pieces of a row
   static constexpr int kTPI = kWave / kPieces;                   // whole rows per load instruction
@@ -442,281 +440,8 @@ __device__ __forceinline__ void widen_fp8(const u32x4 k, u32x4 &lo, u32x4 &hi) {
   hi = (u32x4){w[4], w[5], w[6], w[7]};
 }
 
-// The per-wave MFMA kernel, for 512-byte key rows (16-bit keys, d = 256), whose two staged
-// M-tiles per wave would not fit the per-CU kernel's LDS.  NT loads the keys with the
-// nontemporal hint (they are read once).
-//
-// Loads.  A load instruction reads whole key rows (32 lanes x 16 bytes per 512-byte row, 2 rows
-// per instruction).  The MFMA wants a token per lane instead, so each 16-row M-tile goes through
-// a per-wave LDS buffer (written in load order, read in operand order back into the registers it
-// came from, both free of bank conflicts by the slot permutation tr_slot).
-//
-// Per wave, two chunks are in flight: the MFMAs are the only readers of a chunk's registers, so
-// the chunk after next is loaded right after them and the softmax part overlaps with it.  The
-// per-tile records are staged in LDS and written once per window with coalesced stores.
-constexpr int kMaxGroupRows = 16;
-constexpr int kWindowTiles = kWave / kTileBlocks;  // tiles whose block ids one register holds
-constexpr int kStageFloats = kWindowTiles * 2 * kMaxGroupRows;  // per wave: [tile][plane][row]
-
-template <int MODE, int HEAD_DIM, bool NT>
-__global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p) {
-  using S = MfmaShape<MODE, HEAD_DIM>;
-  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = S::kChunk;
-
-  extern __shared__ int s_mem[];  // [rows + 1] tile offsets, [rows] clipped lengths
-  __shared__ int s_scan[kWaves];
-  __shared__ float s_stage[kWaves][kStageFloats];
-  __shared__ u32x4 s_tr[kWaves][16 * S::kPieces];  // one M-tile of key rows per wave
-  int *s_off = s_mem;
-  int *s_len = s_mem + p.rows + 1;
-
-  const int rows = p.rows;
-  const int bs = p.block_size;
-  const int tile_tokens = kTileBlocks * bs;
-
-  // ---- per-row live tiles: one read of select / lens, then a block scan ------------------
-  // the audit flag (runtime/audit_kernel.py:64) is read together with the rows' lengths, so
-  // that the prologue waits for memory once
-  // (a vector load: a scalar one would be waited for before the lengths are requested)
-  const bool on = *(volatile const uint32_t *)p.flag != 0u;
-#pragma unroll 4
-  for (int r = threadIdx.x; r < rows; r += kThreads) {
-    const int len = min(max(p.lens[r], 0), p.width * bs);
-    s_len[r] = len;
-    s_off[r] = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
-  }
-  if (!on) return;
-  __syncthreads();
-  const int per = (rows + kThreads - 1) / kThreads;
-  const int r0 = threadIdx.x * per;
-  const int r1 = min(r0 + per, rows);
-  int local = 0;
-  for (int r = r0; r < r1; ++r) local += s_off[r];
-  int total_tiles = 0;
-  int base = block_exclusive_scan<kThreads>(local, s_scan, total_tiles);
-  for (int r = r0; r < r1; ++r) {
-    const int tiles = s_off[r];
-    s_off[r] = base;
-    base += tiles;
-  }
-  if (threadIdx.x == 0) s_off[rows] = total_tiles;
-  __syncthreads();
-
-  const int lane = lane_id();
-  const int n = lane & 15;   // A: token of the M-tile; B / C: query row
-  const int c = lane >> 4;   // dim piece within a k-step; C: token quad
-  const int nwaves = gridDim.x * kWaves;
-  const int nsub = p.nsub;   // chunks per tile
-  const int G = p.group_rows;
-  float *stage = s_stage[threadIdx.x / kWave];
-  u32x4 *tr = s_tr[threadIdx.x / kWave];
-  const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
-  const int piece = lane % S::kPieces;
-  // the lane's byte offset within an M-tile for load j: row j * TPI + row_in, piece (the host
-  // checks that 16 positions fit in 31 bits)
-  uint32_t voff[NLD];
-#pragma unroll
-  for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * p.k_stride_pos + piece * 16);
-  // scores in log2 units: s2 = log2(e) * scale * q.k, so that exp(s - m) = exp2(s2 - m2)
-  const float scale2 = p.scale * kLog2e;
-  const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
-  const long long all = (long long)total_tiles * p.groups;
-  long long u = all * wave_id / nwaves;
-  const long long u_end = all * (wave_id + 1) / nwaves;
-
-  while (u < u_end) {
-    const int h = (int)(u / total_tiles);
-    const int t = (int)(u - (long long)h * total_tiles);
-    int lo = 0, hi = rows;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_off[mid] <= t) lo = mid; else hi = mid;
-    }
-    const int row = lo;
-    const long long seg_end = min(u_end, (long long)(h + 1) * total_tiles);
-    const int t_stop = (int)min((long long)s_off[row + 1], seg_end - (long long)h * total_tiles);
-    const int tile_begin = t - s_off[row];
-    const int tile_end = t_stop - s_off[row];
-    u += t_stop - t;
-    const uint64_t t_start = __builtin_amdgcn_s_memtime();
-
-    const int len = s_len[row];
-    const int nblocks = (len + bs - 1) / bs;
-    const int g = p.group_first + h;  // KV head
-    const int32_t *trow = p.table + (int64_t)row * p.table_stride;
-
-    // B operand: query row n of the group, the dims k-step s reads (zero past group_rows)
-    u32x4 qb[KS];
-    {
-      const char *qrow = p.q + (int64_t)p.qrow[row] * p.q_stride_token + (int64_t)(g * G + n) * p.q_stride_head;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        // 16-bit keys: piece 4s + c (8 dims); fp8 keys: 16-dim piece 4(s/2) + c, half s % 2
-        const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
-        qb[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
-      }
-    }
-    const int64_t head_off = (int64_t)g * p.k_stride_head;
-    float *cell_row = p.lse + (int64_t)row * p.row_stride + h * G;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    int ids = 0, ids_base = 0, w0 = 0;
-    // chunk z: tokens 32 (z % nsub) .. + 32 of tile z / nsub, two M-tiles of 16 tokens; an M-tile lies in
-    // one block (16 divides the block size), whose id comes from the window register
-    auto load_chunk = [&](u32x4 (&D)[2 * NLD], int z) {
-      const int tile = z >> p.nsub_log2;
-      const int off = (z & (nsub - 1)) * CH;  // token offset in the tile
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int tpos = off + 16 * mt;
-        const int b = tile * kTileBlocks + tpos / bs;
-        // past the row the tile's first block stands in (in the cache; the scores are masked)
-        const int id = __builtin_amdgcn_readlane(ids, (b < nblocks ? b : tile * kTileBlocks) - ids_base);
-        // a wave-uniform base (scalar arithmetic) plus the lane's 32-bit offset
-        const char *src = p.keys + (int64_t)id * p.k_stride_block + head_off + (int64_t)(tpos % bs) * p.k_stride_pos;
-#pragma unroll
-        for (int j = 0; j < NLD; ++j) {  // rows j * TPI .. + TPI of the M-tile
-          // (the empty asm keeps the 32-bit offset in the loop, so the load takes the scalar
-          // base directly instead of a 64-bit vector address)
-          uint32_t o = voff[j];
-          asm volatile("" : "+v"(o));
-          const u32x4 *at = (const u32x4 *)(src + o);
-          D[mt * NLD + j] = NT ? __builtin_nontemporal_load(at) : *at;
-        }
-      }
-    };
-
-    // the MFMAs of a chunk: scores of tokens 16 mt + 4 c + i for query row n in sc[4 mt + i]
-    auto mma_chunk = [&](u32x4 (&L)[2 * NLD], f32x4_t (&acc)[2]) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        // the M-tile through LDS: row n's piece 4 s + c is operand s of this lane, read back into
-        // the registers the M-tile was loaded into
-        u32x4 *D = L + mt * NLD;
-#pragma unroll
-        for (int j = 0; j < NLD; ++j) tr[tr_slot<S>(j * S::kTPI + row_in, piece)] = D[j];
-#pragma unroll
-        for (int s = 0; s < NLD; ++s) D[s] = tr[tr_slot<S>(n, 4 * s + c)];
-        acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (S::kFp8) {
-#pragma unroll
-          for (int s = 0; s < NLD; ++s) {
-            u32x4 lo4, hi4;
-            widen_fp8(D[s], lo4, hi4);
-            acc[mt] = mfma_step<kModeBF16>(lo4, qb[2 * s], acc[mt]);
-            acc[mt] = mfma_step<kModeBF16>(hi4, qb[2 * s + 1], acc[mt]);
-          }
-        } else {
-#pragma unroll
-          for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[s], qb[s], acc[mt]);
-        }
-      }
-    };
-
-    auto softmax_chunk = [&](const f32x4_t (&acc)[2], int z) {
-      const int tile = z >> p.nsub_log2;
-      const int sub = z & (nsub - 1);
-      const int tok0 = tile * tile_tokens + sub * CH;
-      float sc[8];
-      if (tok0 + CH <= len) {  // the whole chunk is in the row (uniform): no mask
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sc[4 * mt + i] = acc[mt][i] * scale2;
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int tok = tok0 + 16 * mt + 4 * c + i;
-            sc[4 * mt + i] = tok < len ? acc[mt][i] * scale2 : -INFINITY;
-          }
-      }
-      float mx = sc[0];
-#pragma unroll
-      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, sc[k]);
-      mx = rows_max(mx);
-      // exponents are <= 0 (a score minus a max); v_exp_f32 gives 0 for -inf and for underflow
-      float sum = 0.0f;
-      if (mx != -INFINITY) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) sum += __builtin_amdgcn_exp2f(sc[k] - mx);
-      }
-      sum = rows_sum(sum);
-      const float M = fmaxf(m_run, mx);
-      if (M != -INFINITY) {
-        const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f(m_run - M);
-        const float bb = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f(mx - M);
-        l_run = a + bb;
-        m_run = M;
-      }
-      if (sub == nsub - 1) {  // the tile is complete: stage its record (m back in natural units)
-        if (c == 0) {
-          stage[((tile - w0) * 2 + 0) * kMaxGroupRows + n] = m_run * kLn2;
-          stage[((tile - w0) * 2 + 1) * kMaxGroupRows + n] = l_run;
-        }
-        m_run = -INFINITY;
-        l_run = 0.0f;
-      }
-    };
-
-    for (w0 = tile_begin; w0 < tile_end; w0 += kWindowTiles) {
-      const int w1 = min(w0 + kWindowTiles, tile_end);
-      ids_base = w0 * kTileBlocks;
-      ids = ids_base + lane < nblocks ? trow[ids_base + lane] : 0;
-      const int z_end = w1 * nsub;
-      int z = w0 * nsub;
-      u32x4 A[2 * NLD], B[2 * NLD];
-      f32x4_t acc[2];
-      // chunk z from registers L; with `next`, L then takes chunk z_next's loads
-      auto step = [&](u32x4 (&L)[2 * NLD], int z_now, bool next, int z_next) {
-        mma_chunk(L, acc);
-        if (next) load_chunk(L, z_next);
-        softmax_chunk(acc, z_now);
-      };
-      if (z + 1 == z_end) {
-        load_chunk(A, z);
-        step(A, z, false, 0);
-      } else {
-        load_chunk(A, z);
-        load_chunk(B, z + 1);
-        while (z + 3 < z_end) {  // steady state: every load unconditional
-          step(A, z, true, z + 2);
-          step(B, z + 1, true, z + 3);
-          z += 2;
-        }
-        if (z + 2 < z_end) {
-          step(A, z, true, z + 2);
-          step(B, z + 1, false, 0);
-          step(A, z + 2, false, 0);
-        } else {
-          step(A, z, false, 0);
-          step(B, z + 1, false, 0);
-        }
-      }
-      // the window's records into every block of its tiles that the row reaches,
-      // runtime/audit_kernel.py:97-109 (a wave reads only what it staged itself)
-      __builtin_amdgcn_wave_barrier();
-      const int b0 = w0 * kTileBlocks;
-      const int nb = min(w1 * kTileBlocks, nblocks) - b0;
-      for (int e = lane; e < nb * G; e += kWave) {
-        const int b = e / G, q = e - b * G;
-        float *cell = cell_row + (int64_t)(b0 + b) * p.cells + q;
-        cell[0] = stage[((b >> 1) * 2 + 0) * kMaxGroupRows + q];
-        cell[p.plane_stride] = stage[((b >> 1) * 2 + 1) * kMaxGroupRows + q];
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
-
-    if (p.cycles != nullptr && h == 0 && row < p.cycles_rows && lane == 0) {
-      const uint64_t t_end = __builtin_amdgcn_s_memtime();
-      atomicAdd((unsigned long long *)(p.cycles + row), (unsigned long long)(t_end - t_start));
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------------------
-// The MFMA form with one workgroup per compute unit (key rows of up to 256 bytes).
+// The MFMA kernel: one workgroup per compute unit.
 //
 // A compute unit serves its waves' loads roughly in the order they were issued, so with equal
 // static slices the waves that issued last receive their data last and finish last: at the
@@ -727,19 +452,23 @@ __global__ __launch_bounds__(kThreads) void tile_lse_mfma_kernel(const Params p)
 // tiles from an LDS counter, one tile ahead of the one they load.  A wave that is served early
 // simply takes more tiles, and all waves run out of work together.
 //
-// Per wave one chunk (32 tokens, two M-tiles) is in flight: when it arrives it is written to the
-// wave's LDS buffer (load order in, MFMA operand order out, conflict-free by tr_slot), the next
-// chunk's loads go into the same registers, and the MFMAs and the softmax run from LDS while
-// they are in flight.  Each finished tile's record is stored at once, into both of its blocks.
+// Per wave one chunk (8 KB of keys: two 16-token M-tiles of rows up to 256 bytes, one M-tile of
+// 512-byte rows) is in flight: when it arrives it is written to the wave's LDS buffer (load order
+// in, MFMA operand order out, conflict-free by tr_slot), the next chunk's loads go into the same
+// registers, and the MFMAs and the softmax run from LDS while they are in flight.  Each finished
+// tile's record is stored at once, into both of its blocks.
 // ---------------------------------------------------------------------------------------
 template <int MODE, int HEAD_DIM>
 struct CuShape {
   using S = MfmaShape<MODE, HEAD_DIM>;
-  static_assert(S::kRowBytes <= 256, "512-byte key rows use tile_lse_mfma_kernel");
+  static_assert(S::kRowBytes <= 512, "key rows of up to 512 bytes");
   static constexpr int kThreads = kCuThreads;  // 3 waves per SIMD: the shape's VGPR budget
   static constexpr int kWaves = kThreads / kWave;
   static constexpr int kRound = kThreads;  // tiles described per round, one per thread
-  static constexpr int kStash = 2 * 16 * S::kPieces;  // u32x4 per wave: two M-tiles
+  // M-tiles of 16 tokens per chunk: 8 KB of keys in flight per wave (one M-tile of 512-byte rows)
+  static constexpr int kMT = S::kRowBytes > 256 ? 1 : 2;
+  static constexpr int kChunk = 16 * kMT;  // tokens per chunk
+  static constexpr int kStash = kMT * 16 * S::kPieces;  // u32x4 per wave: the chunk's M-tiles
   static constexpr size_t kStaticLds =
       sizeof(u32x4) * kWaves * kStash + sizeof(int4) * kRound + sizeof(int) * (kRound + kWaves + 1);
 };
@@ -748,7 +477,7 @@ template <int MODE, int HEAD_DIM>
 __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p) {
   using S = MfmaShape<MODE, HEAD_DIM>;
   using C = CuShape<MODE, HEAD_DIM>;
-  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = S::kChunk;
+  constexpr int KS = S::kSteps, NLD = S::kLoads, MT = C::kMT, CH = C::kChunk;
   constexpr int NW = C::kWaves, NT = C::kThreads;
 
   extern __shared__ int s_mem[];       // [rows + 1] tile offsets, [rows] clipped lengths
@@ -764,7 +493,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   const int bs = p.block_size;
   const int tile_tokens = kTileBlocks * bs;
 
-  // ---- per-row live tiles and their scan, as in tile_lse_mfma_kernel ----------------------
+  // ---- per-row live tiles (runtime/audit_kernel.py:65-69) and their exclusive scan ---------
   // (the flag is a vector load issued with the lengths: a scalar one would be waited for first)
   const bool on = *(volatile const uint32_t *)p.flag != 0u;
 #pragma unroll 4
@@ -831,11 +560,11 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
     return __builtin_amdgcn_readfirstlane(v);
   };
 
-  // chunk `sub` of tile T: M-tile mt covers tile positions 32 sub + 16 mt .. + 16, inside one block
-  auto load_chunk = [&](u32x4 (&D)[2 * NLD], const Tile &T, int sub) {
+  // chunk `sub` of tile T: M-tile mt covers tile positions CH sub + 16 mt .. + 16, inside one block
+  auto load_chunk = [&](u32x4 (&D)[MT * NLD], const Tile &T, int sub) {
     const int64_t head_off = (int64_t)(p.group_first + T.h) * p.k_stride_head;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       const int tpos = sub * CH + 16 * mt;
       const int id = tpos < bs ? T.id0 : T.id1;  // past the row the tile's first block stands in
       const char *src = p.keys + (int64_t)id * p.k_stride_block + head_off + (int64_t)(tpos % bs) * p.k_stride_pos;
@@ -857,15 +586,15 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
       Q[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
     }
   };
-  auto stash_chunk = [&](const u32x4 (&L)[2 * NLD]) {
+  auto stash_chunk = [&](const u32x4 (&L)[MT * NLD]) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int j = 0; j < NLD; ++j) tr[mt * 16 * S::kPieces + tr_slot<S>(j * S::kTPI + row_in, piece)] = L[mt * NLD + j];
   };
-  auto mma_stashed = [&](const u32x4 (&Q)[KS], f32x4_t (&acc)[2]) {
+  auto mma_stashed = [&](const u32x4 (&Q)[KS], f32x4_t (&acc)[MT]) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       u32x4 D[NLD];
 #pragma unroll
       for (int s = 0; s < NLD; ++s) D[s] = tr[mt * 16 * S::kPieces + tr_slot<S>(n, 4 * s + c)];
@@ -916,8 +645,8 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
       Tile T = describe(i);
       int sub = 0;
       int ahead = take();  // the tile after T, taken early so its LDS round trip is hidden
-      u32x4 A[2 * NLD], qb[KS], qn[KS];
-      f32x4_t acc[2];
+      u32x4 A[MT * NLD], qb[KS], qn[KS];
+      f32x4_t acc[MT];
       load_query(qb, T);
       load_chunk(A, T, 0);
       float m_run = -INFINITY, l_run = 0.0f;
@@ -948,15 +677,15 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
         // ---- the chunk's tile max and sum (query row n, tokens 4c + i of each M-tile) ----
         const int len = s_len[T.row];
         const int tok0 = T.k * tile_tokens + sub * CH;
-        float sc[8];
+        float sc[4 * MT];
         if (tok0 + CH <= len) {
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) sc[4 * mt + e] = acc[mt][e] * scale2;
         } else {
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int tok = tok0 + 16 * mt + 4 * c + e;
@@ -965,13 +694,13 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
         }
         float mx = sc[0];
 #pragma unroll
-        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+        for (int e = 1; e < 4 * MT; ++e) mx = fmaxf(mx, sc[e]);
         mx = rows_max(mx);
         // exponents are <= 0 (a score minus a max); v_exp_f32 gives 0 for -inf and for underflow
         float sum = 0.0f;
         if (mx != -INFINITY) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
+          for (int e = 0; e < 4 * MT; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
         }
         sum = rows_sum(sum);
         const float M = fmaxf(m_run, mx);
@@ -1053,19 +782,12 @@ KernelFn pick_hd(int hd, int nl, int gp) {
   return nullptr;
 }
 
-constexpr bool kMfmaNontemporal = true;
-
-// key rows of up to 256 bytes: the per-CU kernel; 512-byte rows (16-bit keys, d = 256): the
-// per-wave kernel, whose staging fits 512-byte rows
 template <int MODE>
 KernelFn pick_mfma_hd(int hd) {
-  constexpr bool kFp8 = MODE == kModeFp8Bf16;
   switch (hd) {
     case 64: return tile_lse_cu_kernel<MODE, 64>;
     case 128: return tile_lse_cu_kernel<MODE, 128>;
-    case 256:
-      if constexpr (kFp8) return tile_lse_cu_kernel<MODE, 256>;
-      else return tile_lse_mfma_kernel<MODE, 256, kMfmaNontemporal>;
+    case 256: return tile_lse_cu_kernel<MODE, 256>;
   }
   return nullptr;
 }
@@ -1180,8 +902,8 @@ extern "C" int ekv_audit_tile_lse(
   int threads = kThreads;  // per workgroup
   if (use_mfma) {
     fn = pick_mfma(mode, head_dim);
-    nsub = tile_tokens / 32;
-    if (row_bytes <= 256) threads = kCuThreads;
+    nsub = tile_tokens / (row_bytes > 256 ? 16 : 32);  // chunks of 8 KB of keys
+    threads = kCuThreads;
   } else {
     // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
     // instruction must sit inside one block, and a chunk inside one tile.
