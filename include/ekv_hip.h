@@ -145,6 +145,8 @@ int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row
  *    max(floor, ceil(fraction * total)) in IEEE double, total = sum of blocks[r].
  *  - free blocks are split by largest remainder in IEEE double, then each row keeps its quota
  *    of open blocks by (share desc, block index asc).  Shares are max(score, 0) as float32.
+ * scores[r, b], pinned[r, b] and released[r, b] are read for every b < width (rows of `width`
+ * readable entries; the values past blocks[r] are ignored).
  * keep[r, b] (uint8, row stride keep_stride) is written for every r < rows, b < width: 1 for
  * rows that do not take part and for b >= blocks[r], else pinned | chosen, 0 for released.
  * summary (optional int64[6]): budget, total, floor (pinned blocks), status, requests, free.

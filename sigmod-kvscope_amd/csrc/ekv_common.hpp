@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/ekv_hip.h"
 
 namespace ekv {
@@ -85,25 +87,62 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
   return v;
 }
-__device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+// Integer sums and scans over a wave on DPP lane moves (no LDS round trip; a __shfl is a
+// ds_bpermute, whose latency a chain of six pays six times).  Every lane of the wave must be
+// active.  GFX9 DPP controls: quad_perm [1,0,3,2] and [2,3,0,1] (xor 1, xor 2 in each quad),
+// row_shr:n = 0x110 + n, row_ror:n = 0x120 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ int dpp_move(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, BOUND_ZERO);
+}
+// each lane receives the sum of its 16-lane row
+__device__ __forceinline__ int row_sum_int(int v) {
+  v += dpp_move<0xB1>(v);
+  v += dpp_move<0x4E>(v);
+  v += dpp_move<0x124>(v);
+  v += dpp_move<0x128>(v);
   return v;
+}
+__device__ __forceinline__ long long row_sum_i64(long long v) {
+  auto step = [](long long x, long long y) { return x + y; };
+  auto move = [](long long x, auto ctrl) {
+    const int lo = dpp_move<decltype(ctrl)::value>((int)(uint32_t)x);
+    const int hi = dpp_move<decltype(ctrl)::value>((int)(uint32_t)((uint64_t)x >> 32));
+    return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+  };
+  v = step(v, move(v, std::integral_constant<int, 0xB1>()));
+  v = step(v, move(v, std::integral_constant<int, 0x4E>()));
+  v = step(v, move(v, std::integral_constant<int, 0x124>()));
+  v = step(v, move(v, std::integral_constant<int, 0x128>()));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+  v = row_sum_int(v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
 }
 __device__ __forceinline__ long long wave_sum_i64(long long v) {
+  v = row_sum_i64(v);
+  long long s = 0;
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-  return v;
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), 16 * r);
+    s += (long long)(((uint64_t)hi << 32) | lo);
+  }
+  return s;
 }
 
-// Inclusive scan of `v` across the 64 lanes of a wave.
+// Inclusive scan of `v` across the 64 lanes of a wave: shifts within each 16-lane row, then the
+// rows' totals carried forward (lane 15 into row 1 and row 3, then lane 31 into rows 2 and 3).
+// Every lane of the wave must be active.
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    int up = __shfl_up(v, d, kWave);
-    if (lane >= d) v += up;
-  }
+  v += dpp_move<0x111, 0xf, true>(v);
+  v += dpp_move<0x112, 0xf, true>(v);
+  v += dpp_move<0x114, 0xf, true>(v);
+  v += dpp_move<0x118, 0xf, true>(v);
+  v += dpp_move<0x142, 0xa>(v);
+  v += dpp_move<0x143, 0xc>(v);
   return v;
 }
 
@@ -133,8 +172,14 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int *scratch, int &to
 template <int NT, typename T>
 __device__ __forceinline__ T block_sum(T v, T *scratch) {
   constexpr int kWaves = NT / kWave;
+  if constexpr (std::is_same<T, int>::value) {
+    v = wave_sum_int(v);
+  } else if constexpr (std::is_same<T, long long>::value) {
+    v = wave_sum_i64(v);
+  } else {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  }
   if (lane_id() == 0) scratch[threadIdx.x / kWave] = v;
   __syncthreads();
   T s = 0;

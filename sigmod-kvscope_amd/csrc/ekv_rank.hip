@@ -146,6 +146,24 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   const int lane = lane_id();
   const int wave = tid / kWave;
 
+  // ---- the row's blocks: scores and masks into registers (block tid + kThreads i) -----------
+  // The loads are issued first and bounded by the width only, so that they overlap the row
+  // counts' loads and reductions below instead of waiting for them.
+  const RowInfo me = row_info(p, row);
+  const float *srow = p.scores + (int64_t)row * p.scores_stride;
+  float sv[kPer];
+  uint32_t gone_bits = 0, pin_mask_bits = 0;  // released / explicitly pinned, from the masks
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = tid + i * kThreads;
+    const bool in = b < p.width;
+    sv[i] = in ? srow[b] : 0.0f;
+    if (p.released != nullptr)
+      gone_bits |= (in && p.released[(int64_t)row * p.released_stride + b] != 0) ? (1u << i) : 0u;
+    if (p.pinned != nullptr)
+      pin_mask_bits |= (in && p.pinned[(int64_t)row * p.pinned_stride + b] != 0) ? (1u << i) : 0u;
+  }
+
   // ---- totals over every row: controller.py:435-437, allocation.py:57-67 -----------------
   // the open blocks of the first kRowRegs * kThreads rows stay in registers for the quota pass
   long long open_reg[kRowRegs];
@@ -195,24 +213,21 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     p.summary[5] = free_blocks;
   }
 
-  const RowInfo me = row_info(p, row);
   uint8_t *keep_row = p.keep + (int64_t)row * p.keep_stride;
   if (!me.part || error) {  // rows without evidence read in full, controller.py:401
     for (int b = tid; b < p.width; b += kThreads) keep_row[b] = 1;
     return;
   }
 
-  // ---- the row's blocks: scores and masks into registers (block tid + kThreads i) -----------
-  const float *srow = p.scores + (int64_t)row * p.scores_stride;
-  float sv[kPer];
+  // the row's existing and pinned blocks (is_pinned / exists over the loaded masks)
   uint32_t exist_bits = 0, pin_bits = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int b = tid + i * kThreads;
     const bool in = b < me.n;
-    sv[i] = in ? srow[b] : 0.0f;
-    exist_bits |= (in && exists(p, row, b)) ? (1u << i) : 0u;
-    pin_bits |= (in && is_pinned(p, me, row, b)) ? (1u << i) : 0u;
+    const bool pinned = p.pinned != nullptr ? ((pin_mask_bits >> i) & 1u) != 0 : (b == 0 || b >= me.pin_at);
+    exist_bits |= (in && !((gone_bits >> i) & 1u)) ? (1u << i) : 0u;
+    pin_bits |= (in && pinned) ? (1u << i) : 0u;
   }
 
   // ---- this row's quota: largest remainder in IEEE double, allocation.py:79-86 ---------------

@@ -231,6 +231,11 @@ def uniform_keep(
     for name, t in (("measured", measured), ("pinned", pinned), ("released", released)):
         if t is not None and (t.dtype not in (torch.uint8, torch.bool) or t.stride(-1) != 1):
             raise ValueError(f"{name} must be a uint8 / bool mask with contiguous rows")
+    if measured is not None and measured.shape != (rows,):
+        raise ValueError("measured must be [rows]")
+    for name, t in (("pinned", pinned), ("released", released)):
+        if t is not None and t.shape != (rows, width):
+            raise ValueError(f"{name} must be [rows, width] like scores")
     if pin_from is not None and (pin_from.dtype != torch.int32 or pin_from.shape != (rows,)):
         raise ValueError("pin_from must be int32 [rows]")
     if out is None:
