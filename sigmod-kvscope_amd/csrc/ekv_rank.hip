@@ -34,6 +34,7 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxPer = 24;                  // blocks per thread, block tid + kThreads i
 constexpr int kMaxWidth = kThreads * kMaxPer;  // 12288: a row lives in registers
+static_assert(kMaxWidth < 65536, "a row's block counts fit 16-bit fields");
 constexpr int kRowRegs = 4;                  // rows per thread whose open count stays in registers
 constexpr uint32_t kClosed = 0xFFFFFFFFu;  // key of a block that is not open
 
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   __shared__ int s_hist[2][256];
   __shared__ int s_count[kPer * kWaves];  // equal keys per (load, wave), then their exclusive scan
   __shared__ int s_scan[kWaves];
-  __shared__ int s_digit, s_krem;
+  __shared__ int s_digit, s_krem, s_whole;
 
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -235,16 +236,17 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
   const long long my_floor = (long long)my_exact;
   const double my_frac = my_exact - (double)my_floor;
-  // [0] floors, [1] rows ahead in the leftover order, [2..4] has NaN / +inf / positive score,
-  // then [0] (in the second reduction) open blocks
-  long long q5[5] = {0, 0, 0, 0, 0};
+  // [0] floors, [1] rows ahead in the leftover order, [2] four counts of the row's blocks in
+  // 16-bit fields (a row has at most kMaxWidth < 2^16 blocks): existing blocks with a NaN score,
+  // with a +inf score, with a positive score, and open blocks
+  long long q3[3] = {0, 0, 0};
   if (!keep_all) {
     auto visit = [&](int r, long long open) {
       const double exact = open_total > 0 ? (double)(free_blocks * open) / (double)open_total : 0.0;
       const long long fl = (long long)exact;
       const double frac = exact - (double)fl;
-      q5[0] += fl;
-      q5[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
+      q3[0] += fl;
+      q3[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
     };
 #pragma unroll
     for (int i = 0; i < kRowRegs; ++i)
@@ -257,25 +259,28 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   // key mode of the row's shares: allocation.py:46-52 over the existing blocks
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    if (!((exist_bits >> i) & 1u)) continue;
-    const float s = sv[i];
-    q5[2] |= __builtin_isnan(s) ? 1 : 0;
-    q5[3] |= (__builtin_isinf(s) && s > 0.0f) ? 1 : 0;
-    q5[4] |= s > 0.0f ? 1 : 0;
+    if ((exist_bits >> i) & 1u) {
+      const float s = sv[i];
+      q3[2] += __builtin_isnan(s) ? 1ll : 0ll;
+      q3[2] += (__builtin_isinf(s) && s > 0.0f) ? 1ll << 16 : 0ll;
+      q3[2] += s > 0.0f ? 1ll << 32 : 0ll;
+    }
+    q3[2] += (((exist_bits & ~pin_bits) >> i) & 1u) ? 1ll << 48 : 0ll;
   }
-  block_sums(q5, s_red);
+  block_sums(q3, s_red);
   long long quota;
   if (keep_all) {
     quota = my_open;
   } else {
-    const long long leftover = free_blocks - q5[0];
-    quota = my_floor + (q5[1] < leftover ? 1 : 0);
+    const long long leftover = free_blocks - q3[0];
+    quota = my_floor + (q3[1] < leftover ? 1 : 0);
   }
-  const int mode = q5[2] ? 0 : (q5[3] ? 2 : (q5[4] ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
+  const long long has_nan = q3[2] & 0xffff, has_inf = (q3[2] >> 16) & 0xffff, has_pos = (q3[2] >> 32) & 0xffff;
+  const long long open_count = (q3[2] >> 48) & 0xffff;
+  const int mode = has_nan ? 0 : (has_inf ? 2 : (has_pos ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
 
   // ---- keys of the open blocks (order-preserving, larger first), kClosed elsewhere ----------
   uint32_t key[kPer];
-  long long open_count[1] = {0};
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     key[i] = kClosed;
@@ -284,20 +289,21 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
       if (mode == 1) key[i] = s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
       else if (mode == 2) key[i] = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
       else key[i] = 0u;
-      open_count[0] += 1;
     }
   }
-  block_sums(open_count, s_red);
 
   // keep: blocks past the row's end 1, released 0, pinned 1, open blocks decided here
   uint32_t open_keep = 0;
-  if (quota >= open_count[0]) {
+  if (quota >= open_count) {
     open_keep = ~0u;
   } else if (quota > 0) {
     // radix select of the quota-th largest key, 8 bits at a time from the top; the histogram is
-    // double-buffered so that clearing the next one needs no extra barrier
+    // double-buffered so that clearing the next one needs no extra barrier.  The select stops
+    // early once the quota ends exactly at the end of a digit's bucket: every key with that
+    // prefix is kept and no tie needs ranking.
     uint32_t prefix = 0, mask = 0;
     int k_rem = (int)quota;
+    bool whole = false;
     if (tid < 256) s_hist[0][tid] = 0;
     __syncthreads();
 #pragma unroll
@@ -325,6 +331,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
             if (acc < k_rem && acc + c[j] >= k_rem) {
               s_digit = 255 - 4 * lane - j;
               s_krem = k_rem - acc;
+              s_whole = acc + c[j] == k_rem ? 1 : 0;
             }
             acc += c[j];
           }
@@ -334,27 +341,36 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
       prefix |= (uint32_t)s_digit << shift;
       mask |= 255u << shift;
       k_rem = s_krem;
+      whole = __builtin_amdgcn_readfirstlane(s_whole) != 0;
+      if (whole) break;
     }
-    // keep every key above the threshold and the first k_rem equal keys by block index
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    int eq_rank[kPer];
+    if (whole) {
+      // the quota is every key whose top bits are at least the prefix
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const uint64_t eq = __ballot(key[i] == prefix);
-      eq_rank[i] = __popcll(eq & below);
-      if (lane == 0) s_count[i * kWaves + wave] = __popcll(eq);
-    }
-    __syncthreads();
-    const int v = tid < kPer * kWaves ? s_count[tid] : 0;
-    int eq_total;
-    const int excl = block_exclusive_scan<kThreads>(v, s_scan, eq_total);
-    if (tid < kPer * kWaves) s_count[tid] = excl;
-    __syncthreads();
+      for (int i = 0; i < kPer; ++i)
+        open_keep |= (key[i] != kClosed && (key[i] & mask) >= prefix) ? (1u << i) : 0u;
+    } else {
+      // keep every key above the threshold and the first k_rem equal keys by block index
+      const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      int eq_rank[kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const bool kept = key[i] != kClosed &&
-                        (key[i] > prefix || (key[i] == prefix && s_count[i * kWaves + wave] + eq_rank[i] < k_rem));
-      open_keep |= kept ? (1u << i) : 0u;
+      for (int i = 0; i < kPer; ++i) {
+        const uint64_t eq = __ballot(key[i] == prefix);
+        eq_rank[i] = __popcll(eq & below);
+        if (lane == 0) s_count[i * kWaves + wave] = __popcll(eq);
+      }
+      __syncthreads();
+      const int v = tid < kPer * kWaves ? s_count[tid] : 0;
+      int eq_total;
+      const int excl = block_exclusive_scan<kThreads>(v, s_scan, eq_total);
+      if (tid < kPer * kWaves) s_count[tid] = excl;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const bool kept = key[i] != kClosed &&
+                          (key[i] > prefix || (key[i] == prefix && s_count[i * kWaves + wave] + eq_rank[i] < k_rem));
+        open_keep |= kept ? (1u << i) : 0u;
+      }
     }
   }
 #pragma unroll
