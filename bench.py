@@ -163,7 +163,7 @@ class Step:
         self.summary = torch.zeros(6, dtype=torch.int64, device=dev)
         self.view = torch.zeros(R, W, dtype=torch.int32, device=dev)
         self.view_lens = torch.zeros(R, dtype=torch.int32, device=dev)
-        self.counts = torch.zeros(5, dtype=torch.int64, device=dev)
+        self.counts = torch.zeros(R, 5, dtype=torch.int64, device=dev)  # per-row view counters
         self.scale = batch.head_dim ** -0.5
 
     def audit(self, layer: int, stream: int) -> None:

@@ -220,9 +220,11 @@ int ekv_compact_view(const int32_t *table, int64_t table_stride, const int32_t *
  * counters (runtime/block_view.py:272-295 and :297-329).
  * keep = committed | !live | audited[r] | !decoding[r], then & !released  (committed NULL:
  * all ones; audited / decoding / released NULL: none / all decoding / none).
- * counts (optional int64[5], accumulated): read, full, audit, untrimmed, expired blocks of
- * decode rows, as DecodeView._count.  view_table and view_lens may be NULL (counts only, as
- * DecodeView.skip needs).
+ * counts (optional int64[rows][5], row-major, accumulated): row r adds its read, full, audit,
+ * untrimmed and expired blocks (decode rows only) to counts[5r .. 5r+4]; DecodeView._count's
+ * five totals are the column sums.  Each row's workgroup owns its slot, so the counters need no
+ * atomics; calls that share a counts buffer must be ordered (one stream).  view_table and
+ * view_lens may be NULL (counts only, as DecodeView.skip needs).
  */
 int ekv_build_view(const int32_t *table, int64_t table_stride, const int32_t *seq_lens,
                    const uint8_t *committed, int64_t committed_stride, const uint8_t *released,

@@ -75,18 +75,40 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const Params p) {
     for (int w = 0; w < kPlanWaves; ++w) kept += s_wave[w];
     __syncthreads();
   }
-  if (tid == 0) {
-    const int new_length = blocks > 0 ? (kept - 1) * bt + length - (blocks - 1) * bt : 0;
-    p.lens[row] = new_length;
-    if (p.counts != nullptr && real) {
-      const long long read = kept, full = blocks;
-      if (read) atomicAdd((unsigned long long *)&p.counts[0], (unsigned long long)read);
-      if (full) atomicAdd((unsigned long long *)&p.counts[1], (unsigned long long)full);
-      if (audited && read) atomicAdd((unsigned long long *)&p.counts[2], (unsigned long long)read);
-      if (new_length == length && !audited && p.active != 0 && read)
-        atomicAdd((unsigned long long *)&p.counts[3], (unsigned long long)read);
-      if (p.active == 0 && read) atomicAdd((unsigned long long *)&p.counts[4], (unsigned long long)read);
-    }
+  if (tid == 0) p.lens[row] = blocks > 0 ? (kept - 1) * bt + length - (blocks - 1) * bt : 0;
+}
+
+// The counters, runtime/sglang_compact.py:62-73, by one workgroup from every row's old and new
+// offsets: a row of `blocks` blocks whose length went from `length` to `new_length` kept
+// blocks + (new_length - length) / block_tokens of them.  One uncontended add per counter (the
+// rows' workgroups of plan_kernel would otherwise contend on the same five addresses).
+__device__ __forceinline__ void add_counts(const Params &p, const int *s_new, const int *s_old) {
+  __shared__ long long s_red[5][kGatherThreads / kWave];
+  const int bt = p.block_tokens;
+  long long v[5] = {0, 0, 0, 0, 0};  // read, full, audit, untrimmed, expired
+  for (int r = threadIdx.x; r < p.n_real && r < p.n_rows; r += kGatherThreads) {
+    const int length = s_old[r + 1] - s_old[r];
+    const int new_length = s_new[r + 1] - s_new[r];
+    const int blocks = length > 0 ? (length + bt - 1) / bt : 0;
+    const long long kept = blocks > 0 ? blocks + (new_length - length) / bt : 0;
+    const bool audited = p.audit != nullptr && p.audit[r] != 0;
+    v[0] += kept;
+    v[1] += blocks;
+    v[2] += audited ? kept : 0;
+    v[3] += (new_length == length && !audited && p.active != 0) ? kept : 0;
+    v[4] += p.active == 0 ? kept : 0;
+  }
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    v[k] = wave_sum_i64(v[k]);
+    if (lane_id() == 0) s_red[k][wave] = v[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < 5) {
+    long long t = 0;
+    for (int w = 0; w < kGatherThreads / kWave; ++w) t += s_red[threadIdx.x][w];
+    if (t != 0) atomicAdd((unsigned long long *)&p.counts[threadIdx.x], (unsigned long long)t);
   }
 }
 
@@ -120,8 +142,10 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const Params p) 
   offsets_in_lds(p, s_new, s_old, s_scan);
   const int rows = p.n_rows;
   const int total = s_new[rows];
-  if (blockIdx.x == 0)
+  if (blockIdx.x == 0) {
     for (int r = threadIdx.x; r <= rows; r += kGatherThreads) p.new_indptr[r] = s_new[r];
+    if (p.counts != nullptr) add_counts(p, s_new, s_old);
+  }
   const int bt = p.block_tokens;
   const int sb = p.slot_bytes;
 #pragma unroll

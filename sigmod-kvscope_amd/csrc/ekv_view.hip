@@ -33,19 +33,26 @@ struct Params {
   int32_t *view_table;
   int64_t view_stride;
   int32_t *view_lens;
-  long long *counts;
+  long long *counts;  // [rows][5] per-row counters, accumulated
 };
 
 // the row's blocks and whether it reads them all
 struct RowPlan {
-  int L;          // tokens
-  long long n64;  // blocks, ceil(L / bs) (0 for L <= 0), block_view.py:49
-  int n;          // the same, clipped: only b < W and b == n - 1 < W matter
-  bool whole;     // every block of the row is read
+  int L;            // tokens
+  long long n64;    // blocks, ceil(L / bs) (0 for L <= 0), block_view.py:49
+  int n;            // the same, clipped: only b < W and b == n - 1 < W matter
+  bool whole;       // every block of the row is read
+  long long c[5];   // thread 0: the row's counters before this call
 };
 
 __device__ __forceinline__ RowPlan row_plan(const Params &p, int row) {
   RowPlan r;
+  // the row's own counter slot: one workgroup per row adds to it, so no atomics are needed, and
+  // its load goes out with the row's other loads
+  if (threadIdx.x == 0 && p.counts != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) r.c[k] = p.counts[5LL * row + k];
+  }
   r.L = p.seq_lens[row];
   r.n64 = r.L > 0 ? ((long long)r.L + p.block_size - 1) / p.block_size : 0;
   r.n = r.n64 > p.width + 1LL ? p.width + 1 : (int)r.n64;
@@ -63,12 +70,12 @@ __device__ __forceinline__ void count_whole_row(const Params &p, const RowPlan &
   if (threadIdx.x != 0 || p.counts == nullptr) return;
   const bool decoding = p.decoding == nullptr || p.decoding[row] != 0;
   const long long read = decoding ? r.n64 : 0;
-  if (read) {
-    atomicAdd((unsigned long long *)&p.counts[0], (unsigned long long)read);
-    atomicAdd((unsigned long long *)&p.counts[1], (unsigned long long)read);
-    if (p.live) atomicAdd((unsigned long long *)&p.counts[3], (unsigned long long)read);
-    else atomicAdd((unsigned long long *)&p.counts[4], (unsigned long long)read);
-  }
+  long long *c = p.counts + 5LL * row;
+  c[0] = r.c[0] + read;
+  c[1] = r.c[1] + read;
+  c[2] = r.c[2];
+  c[3] = r.c[3] + (p.live ? read : 0);
+  c[4] = r.c[4] + (p.live ? 0 : read);
 }
 
 // keep' of block b from its keep and released bytes, block_view.py:51 and :280-281
@@ -93,11 +100,12 @@ __device__ __forceinline__ void finish_row(const Params &p, const RowPlan &r, in
     const bool whole_read = view_len == r.L;
     const long long rd = decoding ? read : 0, f = decoding ? full : 0;
     const long long untrimmed = (whole_read && !in_audit && p.live) ? rd : 0;
-    if (rd) atomicAdd((unsigned long long *)&p.counts[0], (unsigned long long)rd);
-    if (f) atomicAdd((unsigned long long *)&p.counts[1], (unsigned long long)f);
-    if (in_audit && rd) atomicAdd((unsigned long long *)&p.counts[2], (unsigned long long)rd);
-    if (untrimmed) atomicAdd((unsigned long long *)&p.counts[3], (unsigned long long)untrimmed);
-    if (!p.live && rd) atomicAdd((unsigned long long *)&p.counts[4], (unsigned long long)rd);
+    long long *c = p.counts + 5LL * row;
+    c[0] = r.c[0] + rd;
+    c[1] = r.c[1] + f;
+    c[2] = r.c[2] + (in_audit ? rd : 0);
+    c[3] = r.c[3] + untrimmed;
+    c[4] = r.c[4] + (p.live ? 0 : rd);
   }
 }
 

@@ -200,7 +200,8 @@ class DecodeView:
             self._device = device
             self._table = torch.zeros(self.rows, self.width, dtype=torch.int32, device=device)
             self._lens = torch.zeros(self.rows, dtype=torch.int32, device=device)
-            self._counts = torch.zeros(len(self.COUNTERS), dtype=torch.int64, device=device)
+            # per-row counters (ekv_build_view adds each row's to its own slot); totals are column sums
+            self._counts = torch.zeros(self.rows, len(self.COUNTERS), dtype=torch.int64, device=device)
             self._audited_dev = torch.zeros(self.rows, dtype=torch.uint8, device=device)
             self._decoding_dev = torch.ones(self.rows, dtype=torch.uint8, device=device)
 
@@ -278,13 +279,13 @@ class DecodeView:
         """The blocks read and the blocks full reads would have read, over every decode step."""
         if self._counts is None:
             return 0, 0
-        values = self._counts.tolist()
+        values = self._counts.sum(dim=0).tolist()
         return int(values[0]), int(values[1])
 
     def read_breakdown(self) -> dict[str, int]:
         if self._counts is None:
             return dict.fromkeys(self.COUNTERS, 0)
-        return dict(zip(self.COUNTERS, (int(x) for x in self._counts.tolist())))
+        return dict(zip(self.COUNTERS, (int(x) for x in self._counts.sum(dim=0).tolist())))
 
     def skip(self, seq_lens: torch.Tensor, query_lens: torch.Tensor) -> None:
         """A shared-prefix batch reads the engine's table and records nothing; its decode rows count as
@@ -296,6 +297,8 @@ class DecodeView:
         num_reqs = len(query_lens)
         if num_reqs == 0:
             return
+        if num_reqs > self.rows:
+            raise ValueError(f"batch of {num_reqs} rows exceeds the view's {self.rows} rows")
         self._ensure_device(seq_lens.device)
         assert self._counts is not None and self._decoding_dev is not None
         decode = np.asarray(query_lens.numpy() == 1)
