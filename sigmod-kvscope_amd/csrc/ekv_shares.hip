@@ -455,14 +455,19 @@ __global__ __launch_bounds__(kSplitThreads) void shares_reg_kernel(const Params 
       peak[li * 4 + c] = mx;
     }
   reduce(peak, std::true_type{});
+  // each record's term w exp(m - M) replaces its weight (m is not needed again), which keeps the
+  // kernel within the registers of four workgroups per compute unit
 #pragma unroll
   for (int li = 0; li < NL; ++li)
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float sum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < J; ++j)
-        sum += wv[j][li][c] > 0.0f ? wv[j][li][c] * __expf(mv[j][li][c] - peak[li * 4 + c]) : 0.0f;
+      for (int j = 0; j < J; ++j) {
+        const float term = wv[j][li][c] > 0.0f ? wv[j][li][c] * __expf(mv[j][li][c] - peak[li * 4 + c]) : 0.0f;
+        wv[j][li][c] = term;
+        sum += term;
+      }
       total[li * 4 + c] = sum;
     }
   reduce(total, std::false_type{});
@@ -486,8 +491,8 @@ __global__ __launch_bounds__(kSplitThreads) void shares_reg_kernel(const Params 
     for (int li = 0; li < NL; ++li)
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const float w = wv[j][li][c];  // > 0 only where phase 1 found a peak
-        const float share = w > 0.0f ? w * __expf(mv[j][li][c] - peak[li * 4 + c]) * total[li * 4 + c] : 0.0f;
+        const float term = wv[j][li][c];  // > 0 only where phase 1 found a peak
+        const float share = term > 0.0f ? term * total[li * 4 + c] : 0.0f;
         acc = use_max ? fmaxf(acc, share) : acc + share;
       }
     part[b] = acc;
