@@ -496,15 +496,28 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   // ---- per-row live tiles (runtime/audit_kernel.py:65-69) and their exclusive scan ---------
   // (the flag is a vector load issued with the lengths: a scalar one would be waited for first)
   const bool on = *(volatile const uint32_t *)p.flag != 0u;
+  if (rows <= NT) {
+    // a row per thread: its tile count stays in a register through the scan
+    int tiles = 0;
+    if (threadIdx.x < rows) {
+      const int len = min(max(p.lens[threadIdx.x], 0), p.width * bs);
+      s_len[threadIdx.x] = len;
+      tiles = p.select[threadIdx.x] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
+    }
+    if (!on) return;  // runtime/audit_kernel.py:64
+    int total = 0;
+    const int base = block_exclusive_scan<NT>(tiles, s_scan, total);
+    if (threadIdx.x < rows) s_off[threadIdx.x] = base;
+    if (threadIdx.x == 0) s_off[rows] = total;
+  } else {
 #pragma unroll 4
-  for (int r = threadIdx.x; r < rows; r += NT) {
-    const int len = min(max(p.lens[r], 0), p.width * bs);
-    s_len[r] = len;
-    s_off[r] = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
-  }
-  if (!on) return;  // runtime/audit_kernel.py:64
-  __syncthreads();
-  {
+    for (int r = threadIdx.x; r < rows; r += NT) {
+      const int len = min(max(p.lens[r], 0), p.width * bs);
+      s_len[r] = len;
+      s_off[r] = p.select[r] != 0 ? (len + tile_tokens - 1) / tile_tokens : 0;  // :65-69
+    }
+    if (!on) return;  // runtime/audit_kernel.py:64
+    __syncthreads();
     const int per = (rows + NT - 1) / NT;
     const int r0 = threadIdx.x * per;
     const int r1 = min(r0 + per, rows);
