@@ -204,10 +204,40 @@ __device__ __forceinline__ double key_value(unsigned long long k) {
   return __builtin_bit_cast(double, bits);
 }
 
-__device__ __forceinline__ double share_of(const Params &p, const RowStat &st, int r, int b) {
+__device__ __forceinline__ double share_value(const RowStat &st, double score) {
   if (!(st.total > 0.0) && st.total == st.total) return 1.0 / (double)max(st.n, 1);  // total <= 0
-  return clamp0(p.scores[(int64_t)r * p.scores_stride + b]) / st.total;
+  return clamp0(score) / st.total;
 }
+__device__ __forceinline__ double share_of(const Params &p, const RowStat &st, int r, int b) {
+  return share_value(st, p.scores[(int64_t)r * p.scores_stride + b]);
+}
+
+// A row's blocks b0 + kThreads u (u < U) for one thread: the scores and pinned flags loaded
+// together before any is used (one memory latency per U blocks, not per block).
+template <int U>
+struct BlockRun {
+  double score[U];
+  uint32_t pinned = 0, inside = 0;
+  __device__ __forceinline__ void load(const Params &p, int r, int b0, int n) {
+    const double *srow = p.scores + (int64_t)r * p.scores_stride;
+    const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
+    uint8_t pin[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = b0 + u * kThreads;
+      score[u] = b < n ? srow[b] : 0.0;
+      pin[u] = (prow != nullptr && b < n) ? prow[b] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int b = b0 + u * kThreads;
+      inside |= b < n ? (1u << u) : 0u;
+      const bool pn = prow != nullptr ? pin[u] != 0 : (b == 0 || b == n - 1);
+      pinned |= (b < n && pn) ? (1u << u) : 0u;
+    }
+  }
+};
+constexpr int kRun = 8;  // blocks per thread per step of the per-row loops
 
 __device__ __forceinline__ double weight_of(const Params &p, int r) { return p.weights != nullptr ? p.weights[r] : 1.0; }
 
@@ -236,18 +266,39 @@ __global__ __launch_bounds__(kWave) void prepare_kernel(const Params p) {
     st.open = n - pinned;
     st.pad = 0;
     p.row_stat[r] = st;
-    atomicAdd((unsigned long long *)&p.state->must, (unsigned long long)pinned);
-    atomicAdd((unsigned long long *)&p.state->sizes, (unsigned long long)n);
-    atomicAdd((unsigned long long *)&p.state->open_total, (unsigned long long)(n - pinned));
-    atomicAdd((unsigned long long *)&p.state->requests, 1ull);
   }
 }
 
-// the budget's mode (allocation.py:57-76) and the select's start
-__global__ void decide_kernel(const Params p) {
+// the requests' pinned, existing and open blocks, summed over the rows' statistics by one
+// workgroup, then the budget's mode (allocation.py:57-76) and the select's start
+__global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
+  __shared__ long long s_red[3][kThreads / kWave];
+  long long v[3] = {0, 0, 0};  // must, sizes, open_total
+  for (int r = threadIdx.x; r < p.rows; r += kThreads) {
+    const RowStat st = p.row_stat[r];
+    v[0] += st.pinned;
+    v[1] += st.n;
+    v[2] += st.open;
+  }
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    v[k] = wave_sum_i64(v[k]);
+    if (lane_id() == 0) s_red[k][wave] = v[k];
+  }
+  __syncthreads();
   if (threadIdx.x != 0) return;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    v[k] = 0;
+    for (int w = 0; w < kThreads / kWave; ++w) v[k] += s_red[k][w];
+  }
   State *s = p.state;
-  const long long must = s->must, sizes = s->sizes, budget = p.budget;
+  s->must = v[0];
+  s->sizes = v[1];
+  s->open_total = v[2];
+  s->requests = p.rows;
+  const long long must = v[0], sizes = v[1], budget = p.budget;
   s->budget = budget;
   s->error = (must > budget && budget < sizes) ? 1 : 0;
   const long long free_blocks = budget - must;
@@ -255,7 +306,7 @@ __global__ void decide_kernel(const Params p) {
   int mode;
   if (budget >= sizes) mode = kKeepAll;
   else if (free_blocks <= 0) mode = kPinnedOnly;
-  else if (free_blocks >= s->open_total) mode = kKeepOpen;
+  else if (free_blocks >= v[2]) mode = kKeepOpen;
   else mode = kSelect;
   s->mode = mode;
   s->k_rem = free_blocks;
@@ -266,7 +317,7 @@ __global__ void decide_kernel(const Params p) {
     p.summary[1] = sizes;
     p.summary[2] = must;
     p.summary[3] = s->error;
-    p.summary[4] = s->requests;
+    p.summary[4] = p.rows;
     p.summary[5] = free_blocks;
   }
 }
@@ -292,23 +343,40 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   const unsigned long long prefix = s->prefix, mask = s->mask, threshold = s->threshold;
   for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
     const RowStat st = p.row_stat[r];
-    for (int b = threadIdx.x; b < st.n; b += kThreads) {
-      if (pinned_at(p, r, b, st.n)) continue;
-      const unsigned long long k = key_at(p, st, r, b);
-      unsigned long long key = k;
-      if constexpr (TIE) {
-        if (k != threshold) continue;
-        key = tie_key(r, b);
-      }
-      if ((key & mask) != prefix) continue;
-      const unsigned int digit = (unsigned int)(key >> shift) & 255u;
-      // when every counting lane of the wave has one digit (the first passes), one add for all
-      const uint64_t active = __ballot(true);
-      const unsigned int lead = __shfl(digit, __ffsll((long long)active) - 1, kWave);
-      if (__ballot(digit == lead) == active) {
-        if (lane_id() == __ffsll((long long)active) - 1) atomicAdd(&s_hist[lead], (unsigned int)__popcll(active));
-      } else {
-        atomicAdd(&s_hist[digit], 1u);
+    const double weight = weight_of(p, r);
+    for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < st.n; b0 += kThreads * kRun) {
+      BlockRun<kRun> run;
+      run.load(p, r, b0, st.n);
+#pragma unroll
+      for (int u = 0; u < kRun; ++u) {
+        const int b = b0 + u * kThreads;
+        bool counted = false;
+        unsigned int digit = 0u;
+        if (((run.inside & ~run.pinned) >> u) & 1u) {
+          const unsigned long long k = gain_key(weight * share_value(st, run.score[u]));
+          unsigned long long key = k;
+          bool take = true;
+          if constexpr (TIE) {
+            take = k == threshold;
+            key = tie_key(r, b);
+          }
+          if (take && (key & mask) == prefix) {
+            counted = true;
+            digit = (unsigned int)(key >> shift) & 255u;
+          }
+        }
+        // when every counting lane of the wave has one digit (the first passes), one add for all
+        const uint64_t active = __ballot(counted);
+        if (active == 0) continue;
+        const unsigned int lead = (unsigned int)__builtin_amdgcn_readlane((int)digit, __ffsll((long long)active) - 1);
+        const bool same = __ballot(counted && digit == lead) == active;
+        if (counted) {
+          if (same) {
+            if (lane_id() == __ffsll((long long)active) - 1) atomicAdd(&s_hist[lead], (unsigned int)__popcll(active));
+          } else {
+            atomicAdd(&s_hist[digit], 1u);
+          }
+        }
       }
     }
   }
@@ -363,17 +431,25 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
   const int mode = s->mode;
   const bool error = s->error != 0;
   const unsigned long long threshold = s->threshold, tie = s->prefix;
+  const double weight = weight_of(p, r);
   uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
-  for (int b = threadIdx.x; b < p.width; b += kThreads) {
-    uint8_t k;
-    if (error || b >= st.n || mode == kKeepAll || pinned_at(p, r, b, st.n)) k = 1;
-    else if (mode == kKeepOpen) k = 1;
-    else if (mode == kPinnedOnly) k = 0;
-    else {
-      const unsigned long long key = key_at(p, st, r, b);
-      k = (key > threshold || (key == threshold && tie_key(r, b) >= tie)) ? 1 : 0;
+  for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < p.width; b0 += kThreads * kRun) {
+    BlockRun<kRun> run;
+    run.load(p, r, b0, st.n);
+#pragma unroll
+    for (int u = 0; u < kRun; ++u) {
+      const int b = b0 + u * kThreads;
+      if (b >= p.width) continue;
+      uint8_t k;
+      if (error || b >= st.n || mode == kKeepAll || ((run.pinned >> u) & 1u)) k = 1;
+      else if (mode == kKeepOpen) k = 1;
+      else if (mode == kPinnedOnly) k = 0;
+      else {
+        const unsigned long long key = gain_key(weight * share_value(st, run.score[u]));
+        k = (key > threshold || (key == threshold && tie_key(r, b) >= tie)) ? 1 : 0;
+      }
+      krow[b] = k;
     }
-    krow[b] = k;
   }
 }
 
@@ -649,7 +725,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
-  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
   for (int pass = 0; pass < 8; ++pass) {  // the gain threshold, 8 bits at a time from the top
     hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, 56 - 8 * pass);
@@ -753,7 +829,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
-  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::mm_keys_kernel, dim3(rows), dim3(kWave), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
