@@ -88,8 +88,43 @@ __device__ __forceinline__ double clamp0(double s) { return (s >= 0.0 || s != s)
 
 // ---- NumPy's sum of n values get(i), by one wave; every lane returns it -----------------------
 // The reduction hands its inner loop at most kChunk values at a time and adds each run's pairwise
-// sum to the result in turn, starting from the identity 0.0.
+// sum to the result in turn, starting from the identity 0.0.  A run's recursion splits a piece of
+// more than 128 values at n2 = len / 2 rounded down to a multiple of 8; the left part is at most
+// len / 2 and the right one at most len / 2 + 8, so a run of at most 8192 values reaches pieces of
+// at most 128 within kPairDepth = 7 levels.  The recursion is unrolled at compile time (no stack
+// arrays, whose dynamic indexing made one lane's walk of the tree take tens of microseconds).
 constexpr int kChunk = 8192;
+constexpr int kPairDepth = 7;
+
+template <int D>
+__device__ __forceinline__ void plan_leaves(int s, int len, int &leaves, int *s_start, int *s_len) {
+  if constexpr (D > 0) {
+    if (len > 128) {
+      int n2 = len / 2;
+      n2 -= n2 % 8;
+      plan_leaves<D - 1>(s, n2, leaves, s_start, s_len);
+      plan_leaves<D - 1>(s + n2, len - n2, leaves, s_start, s_len);
+      return;
+    }
+  }
+  s_start[leaves] = s;
+  s_len[leaves] = len;
+  ++leaves;
+}
+
+template <int D>
+__device__ __forceinline__ double combine_leaves(int len, int &next, const double *s_leaf) {
+  if constexpr (D > 0) {
+    if (len > 128) {
+      int n2 = len / 2;
+      n2 -= n2 % 8;
+      const double left = combine_leaves<D - 1>(n2, next, s_leaf);
+      const double right = combine_leaves<D - 1>(len - n2, next, s_leaf);
+      return left + right;
+    }
+  }
+  return s_leaf[next++];
+}
 
 template <class Get>
 __device__ double numpy_sum(Get get, int n, int *s_start, int *s_len, double *s_leaf) {
@@ -97,27 +132,8 @@ __device__ double numpy_sum(Get get, int n, int *s_start, int *s_len, double *s_
   __shared__ int s_nleaves;
   if (lane == 0) {  // the leaves of every run, left to right: pieces of at most 128 values
     int leaves = 0;
-    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk) {
-      int stack_s[16], stack_n[16], sp = 0;
-      stack_s[0] = c0;
-      stack_n[0] = n > 0 ? min(n - c0, kChunk) : 0;
-      while (sp >= 0) {
-        const int s = stack_s[sp], len = stack_n[sp];
-        --sp;
-        if (len <= 128) {
-          s_start[leaves] = s;
-          s_len[leaves] = len;
-          ++leaves;
-        } else {
-          int n2 = len / 2;
-          n2 -= n2 % 8;
-          stack_s[++sp] = s + n2;  // right half second
-          stack_n[sp] = len - n2;
-          stack_s[++sp] = s;
-          stack_n[sp] = n2;
-        }
-      }
-    }
+    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk)
+      plan_leaves<kPairDepth>(c0, n > 0 ? min(n - c0, kChunk) : 0, leaves, s_start, s_len);
     s_nleaves = leaves;
   }
   __builtin_amdgcn_wave_barrier();
@@ -148,40 +164,8 @@ __device__ double numpy_sum(Get get, int n, int *s_start, int *s_len, double *s_
   double total = 0.0;
   if (lane == 0) {  // every run combined in its recursion's order, the runs added in turn
     int next = 0;
-    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk) {
-      int st_len[16], st_stage[16];
-      double st_left[16];
-      int sp = 0;
-      double ret = 0.0;
-      st_len[0] = n > 0 ? min(n - c0, kChunk) : 0;
-      st_stage[0] = 0;
-      while (sp >= 0) {
-        const int len = st_len[sp];
-        if (len <= 128) {
-          ret = s_leaf[next++];
-          --sp;
-          continue;
-        }
-        int n2 = len / 2;
-        n2 -= n2 % 8;
-        if (st_stage[sp] == 0) {
-          st_stage[sp] = 1;
-          ++sp;
-          st_len[sp] = n2;
-          st_stage[sp] = 0;
-        } else if (st_stage[sp] == 1) {
-          st_left[sp] = ret;
-          st_stage[sp] = 2;
-          ++sp;
-          st_len[sp] = len - n2;
-          st_stage[sp] = 0;
-        } else {
-          ret = st_left[sp] + ret;
-          --sp;
-        }
-      }
-      total += ret;
-    }
+    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk)
+      total += combine_leaves<kPairDepth>(n > 0 ? min(n - c0, kChunk) : 0, next, s_leaf);
   }
   return __shfl(total, 0, kWave);
 }
