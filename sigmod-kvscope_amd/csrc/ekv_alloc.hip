@@ -452,6 +452,7 @@ struct MaxminParams {
   MaxminRow *mrow;
   unsigned long long *keys_in, *keys_out;
   int32_t *vals_in, *vals_out;
+  int32_t *ends;  // end of request r's sort segment: its blocks, row0 .. row0 + n
   double *prefix;
   int32_t *offsets;
 };
@@ -478,11 +479,27 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const double base = numpy_sum([&](int k) { return share_of(p, st, r, s_pin[k]); }, npin, s_start, s_len, s_leaf);
   const int64_t row0 = (int64_t)r * p.width;
-  for (int b = lane; b < p.width; b += kWave) {
-    unsigned long long key = 0ull;
-    if (b < st.n && !pinned_at(p, r, b, st.n)) key = gain_key(share_of(p, st, r, b));
-    m.keys_in[row0 + b] = key;
-    m.vals_in[row0 + b] = b;
+  // the sort segment is the request's blocks (pinned ones keyed 0 sort after its open ones); the
+  // rest of the row is neither sorted nor read
+  const double *srow = p.scores + (int64_t)r * p.scores_stride;
+  const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
+  for (int b0 = lane; b0 - lane < st.n; b0 += kWave * kRun) {  // kRun blocks' loads at once
+    double score[kRun];
+    uint8_t pin[kRun];
+#pragma unroll
+    for (int u = 0; u < kRun; ++u) {
+      const int b = b0 + u * kWave;
+      score[u] = b < st.n ? srow[b] : 0.0;
+      pin[u] = (prow != nullptr && b < st.n) ? prow[b] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kRun; ++u) {
+      const int b = b0 + u * kWave;
+      if (b >= st.n) continue;
+      const bool pinned = prow != nullptr ? pin[u] != 0 : (b == 0 || b == st.n - 1);
+      m.keys_in[row0 + b] = pinned ? 0ull : gain_key(share_value(st, score[u]));
+      m.vals_in[row0 + b] = b;
+    }
   }
   if (lane == 0) {
     MaxminRow mr;
@@ -491,7 +508,7 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
     mr.counts = 0;
     m.mrow[r] = mr;
     m.offsets[r] = (int32_t)row0;
-    if (r == p.rows - 1) m.offsets[p.rows] = (int32_t)(row0 + p.width);
+    m.ends[r] = (int32_t)(row0 + st.n);
   }
 }
 
@@ -726,7 +743,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, offsets, keys_in, keys_out, vals_in, vals_out, prefix, temp, temp_bytes, total;
+  size_t state, row_stat, mrow, offsets, ends, keys_in, keys_out, vals_in, vals_out, prefix, temp, temp_bytes, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -742,7 +759,9 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   l.mrow = at;
   at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
   l.offsets = at;
-  at = align256(at + (size_t)(rows + 1) * sizeof(int32_t));
+  at = align256(at + (size_t)rows * sizeof(int32_t));
+  l.ends = at;
+  at = align256(at + (size_t)rows * sizeof(int32_t));
   l.keys_in = at;
   at = align256(at + cells * 8);
   l.keys_out = at;
@@ -805,6 +824,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   p.row_stat = (alloc::RowStat *)(base + l.row_stat);
   m.mrow = (alloc::MaxminRow *)(base + l.mrow);
   m.offsets = (int32_t *)(base + l.offsets);
+  m.ends = (int32_t *)(base + l.ends);
   m.keys_in = (unsigned long long *)(base + l.keys_in);
   m.keys_out = (unsigned long long *)(base + l.keys_out);
   m.vals_in = (int32_t *)(base + l.vals_in);
@@ -821,7 +841,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   rc = check_hip(rocprim::segmented_radix_sort_pairs_desc((void *)(base + l.temp), temp, m.keys_in, m.keys_out,
                                                           m.vals_in, m.vals_out,
                                                           (unsigned int)((size_t)rows * (size_t)width),
-                                                          (unsigned int)rows, m.offsets, m.offsets + 1, 0, 64, s),
+                                                          (unsigned int)rows, m.offsets, m.ends, 0, 64, s),
                  "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + kWave - 1) / kWave), dim3(kWave), 0, s, m);
