@@ -452,32 +452,33 @@ __device__ __forceinline__ void widen_fp8(const u32x4 k, u32x4 &lo, u32x4 &hi) {
 // tiles from an LDS counter, one tile ahead of the one they load.  A wave that is served early
 // simply takes more tiles, and all waves run out of work together.
 //
-// Per wave one chunk (8 KB of keys: two 16-token M-tiles of rows up to 256 bytes, one M-tile of
-// 512-byte rows) is in flight: when it arrives it is written to the wave's LDS buffer (load order
-// in, MFMA operand order out, conflict-free by tr_slot), the next chunk's loads go into the same
-// registers, and the MFMAs and the softmax run from LDS while they are in flight.  Each finished
-// tile's record is stored at once, into both of its blocks.
+// Per wave one chunk of MT 16-token M-tiles is in flight (8 KB of keys: one M-tile of 512-byte
+// rows, two of 256-byte rows, four of rows up to 128 bytes when a tile holds 64 tokens): when it
+// arrives it is written to the wave's LDS buffer (load order in, MFMA operand order out,
+// conflict-free by tr_slot), the next chunk's loads go into the same registers, and the MFMAs and
+// the softmax run from LDS while they are in flight.  Each finished tile's record is stored at
+// once, into both of its blocks.
 // ---------------------------------------------------------------------------------------
-template <int MODE, int HEAD_DIM>
+template <int MODE, int HEAD_DIM, int MT>
 struct CuShape {
   using S = MfmaShape<MODE, HEAD_DIM>;
   static_assert(S::kRowBytes <= 512, "key rows of up to 512 bytes");
+  static_assert(MT >= 1 && MT * 16 * S::kRowBytes <= 8192, "at most 8 KB of keys per chunk");
   static constexpr int kThreads = kCuThreads;  // 3 waves per SIMD: the shape's VGPR budget
   static constexpr int kWaves = kThreads / kWave;
   static constexpr int kRound = kThreads;  // tiles described per round, one per thread
-  // M-tiles of 16 tokens per chunk: 8 KB of keys in flight per wave (one M-tile of 512-byte rows)
-  static constexpr int kMT = S::kRowBytes > 256 ? 1 : 2;
+  static constexpr int kMT = MT;           // M-tiles of 16 tokens per chunk
   static constexpr int kChunk = 16 * kMT;  // tokens per chunk
   static constexpr int kStash = kMT * 16 * S::kPieces;  // u32x4 per wave: the chunk's M-tiles
   static constexpr size_t kStaticLds =
       sizeof(u32x4) * kWaves * kStash + sizeof(int4) * kRound + sizeof(int) * (kRound + kWaves + 1);
 };
 
-template <int MODE, int HEAD_DIM>
+template <int MODE, int HEAD_DIM, int MT>
 __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p) {
   using S = MfmaShape<MODE, HEAD_DIM>;
-  using C = CuShape<MODE, HEAD_DIM>;
-  constexpr int KS = S::kSteps, NLD = S::kLoads, MT = C::kMT, CH = C::kChunk;
+  using C = CuShape<MODE, HEAD_DIM, MT>;
+  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
   constexpr int NW = C::kWaves, NT = C::kThreads;
 
   extern __shared__ int s_mem[];       // [rows + 1] tile offsets, [rows] clipped lengths
@@ -795,21 +796,33 @@ KernelFn pick_hd(int hd, int nl, int gp) {
   return nullptr;
 }
 
+// M-tiles per chunk: 8 KB of keys, within one tile (`wide`: a tile holds at least 64 tokens)
+constexpr int chunk_mtiles(int row_bytes, bool wide) { return row_bytes > 256 ? 1 : (row_bytes > 128 || !wide ? 2 : 4); }
+
+template <int MODE, int HD>
+KernelFn pick_mfma_mt(bool wide) {
+  constexpr int kRowBytes = MfmaShape<MODE, HD>::kRowBytes;
+  if constexpr (kRowBytes <= 128) {
+    if (wide) return tile_lse_cu_kernel<MODE, HD, chunk_mtiles(kRowBytes, true)>;
+  }
+  return tile_lse_cu_kernel<MODE, HD, chunk_mtiles(kRowBytes, false)>;
+}
+
 template <int MODE>
-KernelFn pick_mfma_hd(int hd) {
+KernelFn pick_mfma_hd(int hd, bool wide) {
   switch (hd) {
-    case 64: return tile_lse_cu_kernel<MODE, 64>;
-    case 128: return tile_lse_cu_kernel<MODE, 128>;
-    case 256: return tile_lse_cu_kernel<MODE, 256>;
+    case 64: return pick_mfma_mt<MODE, 64>(wide);
+    case 128: return pick_mfma_mt<MODE, 128>(wide);
+    case 256: return pick_mfma_mt<MODE, 256>(wide);
   }
   return nullptr;
 }
 
-KernelFn pick_mfma(int mode, int hd) {
+KernelFn pick_mfma(int mode, int hd, bool wide) {
   switch (mode) {
-    case kModeF16: return pick_mfma_hd<kModeF16>(hd);
-    case kModeBF16: return pick_mfma_hd<kModeBF16>(hd);
-    case kModeFp8Bf16: return pick_mfma_hd<kModeFp8Bf16>(hd);
+    case kModeF16: return pick_mfma_hd<kModeF16>(hd, wide);
+    case kModeBF16: return pick_mfma_hd<kModeBF16>(hd, wide);
+    case kModeFp8Bf16: return pick_mfma_hd<kModeFp8Bf16>(hd, wide);
   }
   return nullptr;
 }
@@ -914,8 +927,9 @@ extern "C" int ekv_audit_tile_lse(
   int nsub = 1;
   int threads = kThreads;  // per workgroup
   if (use_mfma) {
-    fn = pick_mfma(mode, head_dim);
-    nsub = tile_tokens / (row_bytes > 256 ? 16 : 32);  // chunks of 8 KB of keys
+    const bool wide = tile_tokens % 64 == 0;
+    fn = pick_mfma(mode, head_dim, wide);
+    nsub = tile_tokens / (16 * chunk_mtiles(row_bytes, wide));  // chunks of up to 8 KB of keys
     threads = kCuThreads;
   } else {
     // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
