@@ -36,6 +36,7 @@ constexpr int kTileBlocks = 2;  // TILE_BLOCKS, runtime/audit_kernel.py:31
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxRows = 6000;  // LDS holds two ints per row beside the kernels' staging buffers
+constexpr int kCycleSlots = 64;  // per-row cycle accumulators of a round in tile_lse_cu_kernel
 
 enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
 
@@ -470,8 +471,8 @@ struct CuShape {
   static constexpr int kMT = MT;           // M-tiles of 16 tokens per chunk
   static constexpr int kChunk = 16 * kMT;  // tokens per chunk
   static constexpr int kStash = kMT * 16 * S::kPieces;  // u32x4 per wave: the chunk's M-tiles
-  static constexpr size_t kStaticLds =
-      sizeof(u32x4) * kWaves * kStash + sizeof(int4) * kRound + sizeof(int) * (kRound + kWaves + 1);
+  static constexpr size_t kStaticLds = sizeof(u32x4) * kWaves * kStash + sizeof(int4) * kRound +
+                                       sizeof(int) * (kRound + kWaves + 1) + sizeof(unsigned long long) * kCycleSlots;
 };
 
 template <int MODE, int HEAD_DIM, int MT>
@@ -487,6 +488,9 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   __shared__ int4 s_desc[C::kRound];   // (row | head << 16, tile in row, id0, id1)
   __shared__ int s_qtok[C::kRound];    // the row's query token
   __shared__ u32x4 s_tr[NW][C::kStash];
+  // timer: the round's cycles per row, rows row0 .. row0 + kCycleSlots - 1 of the round (its rows
+  // are contiguous from its first tile's), flushed once per round instead of once per wave
+  __shared__ unsigned long long s_cycles[kCycleSlots];
   int *s_off = s_mem;
   int *s_len = s_mem + p.rows + 1;
 
@@ -533,6 +537,8 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
     }
     if (threadIdx.x == 0) s_off[rows] = total;
   }
+  if (p.cycles != nullptr)
+    for (int k = threadIdx.x; k < kCycleSlots; k += NT) s_cycles[k] = 0ull;
   __syncthreads();
   const int total_tiles = s_off[rows];
 
@@ -652,6 +658,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
     }
     if (threadIdx.x == 0) s_next = 0;
     __syncthreads();
+    const int round_row0 = __builtin_amdgcn_readfirstlane(s_desc[0].x & 0xffff);  // the round's first row
 
     // ---- the waves take the round's tiles -------------------------------------------------
     int i = take();
@@ -666,7 +673,6 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
       float m_run = -INFINITY, l_run = 0.0f;
       const bool timed = p.cycles != nullptr;
       uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
-      uint64_t spent = 0;
       while (true) {
         // the chunk after this one: the next part of T, or the first of the tile taken ahead
         Tile N = T;
@@ -735,15 +741,17 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
           }
           m_run = -INFINITY;
           l_run = 0.0f;
-          if (timed) {
-            // the wave's time since its previous tile goes to this tile's row (first KV head)
+          if (timed && (!more || N.row != T.row || N.h != T.h)) {
+            // the wave's time since its previous tile goes to this tile's row (first KV head).  Over
+            // a run of tiles of one row and head those intervals telescope, so the clock is read
+            // once, where the run ends (a clock read waits for the wave's LDS traffic).
             const uint64_t now = __builtin_amdgcn_s_memtime();
-            if (T.h == 0 && T.row < p.cycles_rows) spent += now - mark;
-            mark = now;
-            if (spent != 0 && (!more || N.row != T.row || N.h != T.h)) {
-              if (lane == 0) atomicAdd((unsigned long long *)(p.cycles + T.row), (unsigned long long)spent);
-              spent = 0;
+            if (T.h == 0 && T.row < p.cycles_rows && lane == 0) {
+              const int slot = T.row - round_row0;
+              if (slot < kCycleSlots) atomicAdd(&s_cycles[slot], (unsigned long long)(now - mark));
+              else atomicAdd((unsigned long long *)(p.cycles + T.row), (unsigned long long)(now - mark));
             }
+            mark = now;
           }
         }
         if (!more) break;
@@ -756,6 +764,14 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
       }
     }
     __syncthreads();  // the next round rewrites the descriptors and the counter
+    if (p.cycles != nullptr && threadIdx.x < kCycleSlots) {
+      // the round's rows: one add each (cleared before the next round's barrier)
+      const unsigned long long c = s_cycles[threadIdx.x];
+      if (c != 0ull) {
+        atomicAdd((unsigned long long *)(p.cycles + round_row0 + threadIdx.x), c);
+        s_cycles[threadIdx.x] = 0ull;
+      }
+    }
   }
 }
 
