@@ -71,3 +71,27 @@ def test_descriptor_paths(tmp_path, monkeypatch):
     with open(path, "w") as f:
         f.write('{"a": 1}\n\n{"b": 2}\n')
     assert read_json_lines(path) == [{"a": 1}, {"b": 2}]
+
+
+def test_skip_rejects_a_batch_wider_than_the_view():
+    # the per-row read counters have one slot per view row: a larger batch is refused before any
+    # device work (DecodeView.skip, runtime/block_view.py:352-361)
+    import torch
+
+    view = DecodeView(rows=2, width=4, block_size=16)
+    with pytest.raises(ValueError):
+        view.skip(torch.tensor([16, 32, 48], dtype=torch.int32), torch.ones(3, dtype=torch.int32))
+
+
+def test_uniform_keep_rejects_masks_of_another_shape():
+    # the ranking reads scores and masks for every b < width, so masks must be [rows, width]
+    import torch
+
+    scores = torch.zeros(2, 8, dtype=torch.float32)
+    blocks = torch.tensor([4, 8], dtype=torch.int32)
+    with pytest.raises(ValueError):
+        allocation.uniform_keep(scores, blocks, pinned=torch.zeros(2, 4, dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        allocation.uniform_keep(scores, blocks, released=torch.zeros(3, 8, dtype=torch.uint8))
+    with pytest.raises(ValueError):
+        allocation.uniform_keep(scores, blocks, measured=torch.zeros(3, dtype=torch.uint8))
