@@ -296,6 +296,37 @@ def test_records_give_the_true_share(kind):
         assert tv < 1e-3 and kept > 1.0 - 1e-9
 
 
+def test_timer_over_rounds_of_many_short_rows():
+    # One workgroup's rounds each span more rows than the kernel's 64 per-round cycle slots (the rows
+    # past them add to the accumulator directly), with two KV heads audited (only the first head's
+    # tiles are timed): every selected row's cycles grow at every launch, the others stay zero.
+    rows, bs, hkv, hq, d = 400, 16, 2, 8, 64
+    rng = np.random.default_rng(17)
+    lens = rng.integers(1, 65, size=rows).astype(np.int32)  # one or two tiles of 32 tokens
+    n = (lens + bs - 1) // bs
+    width = int(n.max())
+    table = np.zeros((rows, width), dtype=np.int32)
+    cursor = 1
+    for r in range(rows):
+        table[r, : n[r]] = np.arange(cursor, cursor + n[r])
+        cursor += int(n[r])
+    pool = torch.randn(cursor, 2, bs, hkv, d, device="cuda").to(torch.bfloat16)
+    q = torch.randn(rows, hq, d, device="cuda").to(torch.bfloat16)
+    plane = RecordingPlane(1, rows, width, hq // hkv, bs, kv_heads=hkv, timer=True)
+    flag(plane)
+    select = np.ones(rows, bool)
+    select[::7] = False
+    table_t, lens_t = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
+    prev = plane.read_cycles()
+    for _ in range(3):
+        got = record(plane, 0, table_t, lens_t, q, pool[:, 0], d**-0.5, select=select, chunk_tiles=1000)
+        cur = plane.read_cycles()
+        assert (cur[select] > prev[select]).all(), "a selected row's cycles did not grow"
+        assert (cur[~select] == 0).all(), "an unselected row was timed"
+        prev = cur
+    assert not np.isnan(got[0][0][select]).all()
+
+
 def test_timer_accumulates_per_row_cycles():
     # rows with planted work (lengths 512 * (r + 1)); the accumulator only grows, unselected rows stay 0,
     # and the per-launch cycles of a row follow its work (tests/_row_cycles_check.py:61-69, 120-163).
