@@ -481,6 +481,8 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   using C = CuShape<MODE, HEAD_DIM, MT>;
   constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
   constexpr int NW = C::kWaves, NT = C::kThreads;
+  static_assert(C::kStaticLds + sizeof(int) * (2 * kMaxRows + 1) <= 160 * 1024,
+                "the staging buffers and the largest row count's offsets fit a compute unit's LDS");
 
   extern __shared__ int s_mem[];       // [rows + 1] tile offsets, [rows] clipped lengths
   __shared__ int s_scan[NW];
