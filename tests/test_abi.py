@@ -41,3 +41,44 @@ def test_argument_errors_map_to_value_error():
     except ValueError as err:
         raised = str(err)
     assert raised and "null" in raised
+
+
+COMPUTE = ("ekv_audit_tile_lse", "ekv_tile_shares", "ekv_tile_shares_ws", "ekv_normalize_tile_lse",
+           "ekv_rank_uniform", "ekv_rank_uniform_ws", "ekv_rank_sum", "ekv_rank_maxmin", "ekv_compact_view",
+           "ekv_build_view", "ekv_compact_slots")
+
+
+def test_every_entry_point_rejects_null_pointers_on_the_host():
+    # null pointers with zero sizes: each entry point's argument checks refuse them (ValueError)
+    # before any device call, which is why this runs without a GPU
+    import pytest
+
+    lib = ekv_hip.load()
+    for name in COMPUTE:
+        args = [0] * len(getattr(lib, name).argtypes)
+        with pytest.raises(ValueError):
+            ekv_hip.call(name, *args)
+
+
+def test_shape_limits_are_refused_on_the_host():
+    import pytest
+
+    P = 256  # a placeholder device address: the checks below refuse the call before using it
+    # ranking: a row wider than the register-resident maximum
+    with pytest.raises(ValueError, match="width"):
+        ekv_hip.call("ekv_rank_uniform", P, 20000, P, 0, 0, 0, 0, 0, 0, 0, 4, 20000, 0.5, -1, P, 20000, 0, 0)
+    # ranking: explicit masks without a workspace
+    with pytest.raises(ValueError, match="workspace"):
+        ekv_hip.call("ekv_rank_uniform", P, 8, P, 0, P, 8, 0, 0, 0, 0, 4, 8, 0.5, -1, P, 8, 0, 0)
+    # audit: more query rows per KV head than a record holds
+    audit = [P, ekv_hip.BF16, 4096, 128, P, ekv_hip.BF16, 65536, 1024, 128, 1.0, P, 8, P, P, P, P,
+             P, 1 << 20, 1 << 16, 64, 17, 0, 0, 0.1, 0, 0, 1, 17, 4, 8, 16, 2, 128, 0, 0]
+    with pytest.raises(ValueError, match="query rows"):
+        ekv_hip.call("ekv_audit_tile_lse", *audit)
+    # audit: tiles of another number of blocks than the records hold
+    audit[20], audit[27], audit[31] = 4, 4, 3
+    with pytest.raises(ValueError, match="tiles"):
+        ekv_hip.call("ekv_audit_tile_lse", *audit)
+    # SGLang lists: slots of 3 bytes
+    with pytest.raises(ValueError, match="slots"):
+        ekv_hip.call("ekv_compact_slots", P, P, 3, P, 8, 0, 1, 1, 1, 8, 16, 16, P, P, P, 8, P, 0, 0, 0)
