@@ -19,8 +19,8 @@
 //
 // maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
 // the lowest request first (observe/allocation.py:126-166).  Per request: the pinned shares' NumPy
-// sum (base), its open blocks in stable descending share order (a segmented radix sort over the
-// same order-preserving keys) and their running float64 totals, added in that order as
+// sum (base), its open blocks in stable descending share order (a block radix sort in LDS over the
+// same order-preserving keys, one workgroup per request) and their running float64 totals, added in that order as
 // np.cumsum does.  The 60-step bisection of the level runs in one workgroup: a request's count at
 // a level is min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the
 // shifted-by-2r comparison NumPy's single search makes, and every request keeps the bracket of
@@ -33,7 +33,7 @@
 
 #include <algorithm>
 
-#include <rocprim/device/device_segmented_radix_sort.hpp>
+#include <rocprim/block/block_radix_sort.hpp>
 
 #include "ekv_common.hpp"
 
@@ -450,11 +450,9 @@ struct MaxminRow {
 struct MaxminParams {
   Params p;
   MaxminRow *mrow;
-  unsigned long long *keys_in, *keys_out;
-  int32_t *vals_in, *vals_out;
-  int32_t *ends;  // end of request r's sort segment: its blocks, row0 .. row0 + n
+  unsigned long long *keys_in, *keys_out;  // the requests' sort keys, in block order and sorted
+  int32_t *vals_out;                       // the sorted keys' block indices
   double *prefix;
-  int32_t *offsets;
 };
 
 // per request, one wave: the base, the sort keys of the open blocks (0 elsewhere), the offsets
@@ -479,8 +477,8 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const double base = numpy_sum([&](int k) { return share_of(p, st, r, s_pin[k]); }, npin, s_start, s_len, s_leaf);
   const int64_t row0 = (int64_t)r * p.width;
-  // the sort segment is the request's blocks (pinned ones keyed 0 sort after its open ones); the
-  // rest of the row is neither sorted nor read
+  // the request's blocks in block order (pinned ones keyed 0 sort after its open ones); the rest of
+  // the row is neither sorted nor read
   const double *srow = p.scores + (int64_t)r * p.scores_stride;
   const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
   for (int b0 = lane; b0 - lane < st.n; b0 += kWave * kRun) {  // kRun blocks' loads at once
@@ -498,7 +496,6 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
       if (b >= st.n) continue;
       const bool pinned = prow != nullptr ? pin[u] != 0 : (b == 0 || b == st.n - 1);
       m.keys_in[row0 + b] = pinned ? 0ull : gain_key(share_value(st, score[u]));
-      m.vals_in[row0 + b] = b;
     }
   }
   if (lane == 0) {
@@ -507,8 +504,37 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
     mr.open = st.open;
     mr.counts = 0;
     m.mrow[r] = mr;
-    m.offsets[r] = (int32_t)row0;
-    m.ends[r] = (int32_t)(row0 + st.n);
+  }
+}
+
+// per request, one workgroup: its n keys in stable descending order (equal keys, such as the pinned
+// blocks' 0, keep block order), with the block index of each, by a block radix sort in LDS; the
+// positions past n are padding keys 0, which sort after every block of the request
+constexpr int kSortThreads = 1024;
+
+template <int ITEMS>
+__global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParams m) {
+  using Sort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
+  __shared__ typename Sort::storage_type storage;
+  const int r = blockIdx.x;
+  const int n = m.p.row_stat[r].n;
+  const int64_t row0 = (int64_t)r * m.p.width;
+  unsigned long long keys[ITEMS];
+  int vals[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int pos = threadIdx.x * ITEMS + i;
+    keys[i] = pos < n ? m.keys_in[row0 + pos] : 0ull;
+    vals[i] = pos;
+  }
+  Sort().sort_desc(keys, vals, storage);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int pos = threadIdx.x * ITEMS + i;
+    if (pos < n) {
+      m.keys_out[row0 + pos] = keys[i];
+      m.vals_out[row0 + pos] = vals[i];
+    }
   }
 }
 
@@ -743,7 +769,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, offsets, ends, keys_in, keys_out, vals_in, vals_out, prefix, temp, temp_bytes, total;
+  size_t state, row_stat, mrow, keys_in, keys_out, vals_out, prefix, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -758,28 +784,15 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)rows * sizeof(alloc::RowStat));
   l.mrow = at;
   at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
-  l.offsets = at;
-  at = align256(at + (size_t)rows * sizeof(int32_t));
-  l.ends = at;
-  at = align256(at + (size_t)rows * sizeof(int32_t));
   l.keys_in = at;
   at = align256(at + cells * 8);
   l.keys_out = at;
   at = align256(at + cells * 8);
-  l.vals_in = at;
-  at = align256(at + cells * 4);
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
   at = align256(at + cells * 8);
-  l.temp = at;
-  size_t temp = 0;
-  const hipError_t query = rocprim::segmented_radix_sort_pairs_desc((void *)nullptr, temp, (unsigned long long *)nullptr,
-                                           (unsigned long long *)nullptr, (int32_t *)nullptr, (int32_t *)nullptr,
-                                           (unsigned int)cells, (unsigned int)rows, (int32_t *)nullptr,
-                                           (int32_t *)nullptr, 0, 64);
-  l.temp_bytes = query == hipSuccess ? temp : 0;
-  l.total = align256(at + temp) + 256;  // + 256: the base may be realigned
+  l.total = at + 256;  // + 256: the base may be realigned
   return l;
 }
 
@@ -823,11 +836,8 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   p.state = (alloc::State *)(base + l.state);
   p.row_stat = (alloc::RowStat *)(base + l.row_stat);
   m.mrow = (alloc::MaxminRow *)(base + l.mrow);
-  m.offsets = (int32_t *)(base + l.offsets);
-  m.ends = (int32_t *)(base + l.ends);
   m.keys_in = (unsigned long long *)(base + l.keys_in);
   m.keys_out = (unsigned long long *)(base + l.keys_out);
-  m.vals_in = (int32_t *)(base + l.vals_in);
   m.vals_out = (int32_t *)(base + l.vals_out);
   m.prefix = (double *)(base + l.prefix);
   hipStream_t s = (hipStream_t)stream;
@@ -837,12 +847,13 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   hipLaunchKernelGGL(alloc::mm_keys_kernel, dim3(rows), dim3(kWave), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
-  size_t temp = l.temp_bytes;
-  rc = check_hip(rocprim::segmented_radix_sort_pairs_desc((void *)(base + l.temp), temp, m.keys_in, m.keys_out,
-                                                          m.vals_in, m.vals_out,
-                                                          (unsigned int)((size_t)rows * (size_t)width),
-                                                          (unsigned int)rows, m.offsets, m.ends, 0, 64, s),
-                 "ekv_rank_maxmin sort");
+  if (width <= 4 * alloc::kSortThreads)
+    hipLaunchKernelGGL(alloc::mm_sort_kernel<4>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
+  else if (width <= 8 * alloc::kSortThreads)
+    hipLaunchKernelGGL(alloc::mm_sort_kernel<8>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
+  else
+    hipLaunchKernelGGL(alloc::mm_sort_kernel<12>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
+  rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + kWave - 1) / kWave), dim3(kWave), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_bisect_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
