@@ -20,8 +20,8 @@
 // maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
 // the lowest request first (observe/allocation.py:126-166).  Per request: the pinned shares' NumPy
 // sum (base), its open blocks in stable descending share order (a block radix sort in LDS over the
-// same order-preserving keys, one workgroup per request) and their running float64 totals, added in that order as
-// np.cumsum does.  The 60-step bisection of the level runs in one workgroup: a request's count at
+// same order-preserving keys, one workgroup per request), and their running float64 totals, added
+// in that order as np.cumsum does by one lane per request.  The 60-step bisection of the level runs in one workgroup: a request's count at
 // a level is min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the
 // shifted-by-2r comparison NumPy's single search makes, and every request keeps the bracket of
 // positions its count can still take, so later steps search a few entries.  The leftover goes one
@@ -450,13 +450,12 @@ struct MaxminRow {
 struct MaxminParams {
   Params p;
   MaxminRow *mrow;
-  unsigned long long *keys_in, *keys_out;  // the requests' sort keys, in block order and sorted
-  int32_t *vals_out;                       // the sorted keys' block indices
-  double *prefix;
+  int32_t *vals_out;  // per request, its blocks' indices in sorted order
+  double *prefix;     // per request, the running totals of its open shares in that order
 };
 
-// per request, one wave: the base, the sort keys of the open blocks (0 elsewhere), the offsets
-__global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
+// per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts
+__global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
   __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
   __shared__ double s_leaf[kMaxLeaves];
   __shared__ unsigned short s_pin[kMaxWidth];  // the pinned blocks, in order
@@ -476,28 +475,6 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   const double base = numpy_sum([&](int k) { return share_of(p, st, r, s_pin[k]); }, npin, s_start, s_len, s_leaf);
-  const int64_t row0 = (int64_t)r * p.width;
-  // the request's blocks in block order (pinned ones keyed 0 sort after its open ones); the rest of
-  // the row is neither sorted nor read
-  const double *srow = p.scores + (int64_t)r * p.scores_stride;
-  const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
-  for (int b0 = lane; b0 - lane < st.n; b0 += kWave * kRun) {  // kRun blocks' loads at once
-    double score[kRun];
-    uint8_t pin[kRun];
-#pragma unroll
-    for (int u = 0; u < kRun; ++u) {
-      const int b = b0 + u * kWave;
-      score[u] = b < st.n ? srow[b] : 0.0;
-      pin[u] = (prow != nullptr && b < st.n) ? prow[b] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < kRun; ++u) {
-      const int b = b0 + u * kWave;
-      if (b >= st.n) continue;
-      const bool pinned = prow != nullptr ? pin[u] != 0 : (b == 0 || b == st.n - 1);
-      m.keys_in[row0 + b] = pinned ? 0ull : gain_key(share_value(st, score[u]));
-    }
-  }
   if (lane == 0) {
     MaxminRow mr;
     mr.base = base;
@@ -507,69 +484,109 @@ __global__ __launch_bounds__(kWave) void mm_keys_kernel(const MaxminParams m) {
   }
 }
 
-// per request, one workgroup: its n keys in stable descending order (equal keys, such as the pinned
-// blocks' 0, keep block order), with the block index of each, by a block radix sort in LDS; the
-// positions past n are padding keys 0, which sort after every block of the request
+// per request, one workgroup:
+// 1. the sort keys of its n blocks, the pinned ones keyed 0;
+// 2. a block radix sort of them in LDS, stable and descending, so equal keys (such as the pinned
+//    blocks' 0) keep block order and the padding keys 0 past n sort after every block;
+// 3. the sorted block indices, and the open blocks' shares in sorted order (for the totals).
 constexpr int kSortThreads = 1024;
 
 template <int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParams m) {
   using Sort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
   __shared__ typename Sort::storage_type storage;
+  const Params &p = m.p;
   const int r = blockIdx.x;
-  const int n = m.p.row_stat[r].n;
-  const int64_t row0 = (int64_t)r * m.p.width;
+  const RowStat st = p.row_stat[r];
+  const int n = st.n, open = st.open;
+  const double *srow = p.scores + (int64_t)r * p.scores_stride;
+  const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
   unsigned long long keys[ITEMS];
   int vals[ITEMS];
+  double score[ITEMS];
+  uint8_t pin[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {  // every load issued before any is used
+    const int pos = threadIdx.x * ITEMS + i;
+    score[i] = pos < n ? srow[pos] : 0.0;
+    pin[i] = (prow != nullptr && pos < n) ? prow[pos] : 0;
+  }
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int pos = threadIdx.x * ITEMS + i;
-    keys[i] = pos < n ? m.keys_in[row0 + pos] : 0ull;
+    const bool pinned = prow != nullptr ? pin[i] != 0 : (pos == 0 || pos == n - 1);
+    keys[i] = (pos < n && !pinned) ? gain_key(share_value(st, score[i])) : 0ull;
     vals[i] = pos;
   }
-  Sort().sort_desc(keys, vals, storage);
+  Sort().sort_desc_to_striped(keys, vals, storage);
+  const int64_t row0 = (int64_t)r * p.width;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int pos = threadIdx.x * ITEMS + i;
-    if (pos < n) {
-      m.keys_out[row0 + pos] = keys[i];
-      m.vals_out[row0 + pos] = vals[i];
-    }
+  for (int i = 0; i < ITEMS; ++i) {  // striped: position i * kSortThreads + thread
+    const int pos = i * kSortThreads + threadIdx.x;
+    if (pos < n) m.vals_out[row0 + pos] = vals[i];
+    if (pos < open) m.prefix[row0 + pos] = key_value(keys[i]);
   }
 }
 
-// per request, one lane: the running totals of the open shares in sorted order (np.cumsum), the
-// shares decoded from the sorted keys, read as a stream 32 values at a time with the next 32 in
-// flight while the current ones are added
-constexpr int kPrefixBatch = 32;
+// per request, one wave: the running totals of its sorted open shares (np.cumsum), in place. One
+// float64 chain per request, added by lane 0: the wave stages the shares through LDS a chunk at a
+// time with coalesced loads, the next chunk's loads in flight while lane 0 adds the current chunk
+// from LDS and stores the totals. One wave per request keeps every request's chain in flight at
+// once (one per SIMD at 1024 requests), where a workgroup that also sorted would run one at a time
+// per CU.
+constexpr int kTotalsChunk = 1024;  // values per chunk: 16 per lane
+constexpr int kChainBatch = 16;     // values lane 0 reads from LDS before adding them
 
-__global__ __launch_bounds__(kWave) void mm_prefix_kernel(const MaxminParams m) {
-  const Params &p = m.p;
-  const int r = blockIdx.x * kWave + threadIdx.x;
-  if (r >= p.rows) return;
-  const int open = p.row_stat[r].open;
-  const int64_t row0 = (int64_t)r * p.width;
-  const unsigned long long *keys = m.keys_out + row0;
-  double *out = m.prefix + row0;
-  unsigned long long cur[kPrefixBatch], nxt[kPrefixBatch];
+__global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) {
+  static_assert(kTotalsChunk % kWave == 0 && kTotalsChunk % kChainBatch == 0, "whole batches per chunk");
+  constexpr int kPer = kTotalsChunk / kWave;
+  __shared__ double s_chunk[kTotalsChunk];
+  const int r = blockIdx.x;
+  const int lane = lane_id();
+  const int open = m.p.row_stat[r].open;
+  double *row = m.prefix + (int64_t)r * m.p.width;
+  double v[kPer];
 #pragma unroll
-  for (int k = 0; k < kPrefixBatch; ++k) cur[k] = k < open ? keys[k] : 0ull;
-  double acc = 0.0;
-  for (int i0 = 0; i0 < open; i0 += kPrefixBatch) {
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kWave + lane;
+    v[j] = i < open ? row[i] : 0.0;
+  }
+  // -0.0 + x is x for every x, so the first total is the first share itself, as in np.cumsum
+  double acc = -0.0;
+  for (int c0 = 0; c0 < open; c0 += kTotalsChunk) {
 #pragma unroll
-    for (int k = 0; k < kPrefixBatch; ++k) {
-      const int i = i0 + kPrefixBatch + k;
-      nxt[k] = i < open ? keys[i] : 0ull;
+    for (int j = 0; j < kPer; ++j) s_chunk[j * kWave + lane] = v[j];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {  // the next chunk
+      const int i = c0 + kTotalsChunk + j * kWave + lane;
+      v[j] = i < open ? row[i] : 0.0;
     }
+    if (lane == 0) {
+      const int len = min(open - c0, kTotalsChunk);
+      double *out = row + c0;
+      for (int i0 = 0; i0 < len; i0 += kChainBatch) {
+        double x[kChainBatch];
 #pragma unroll
-    for (int k = 0; k < kPrefixBatch; ++k) {
-      if (i0 + k >= open) break;
-      const double v = key_value(cur[k]);
-      acc = (i0 + k == 0) ? v : acc + v;
-      out[i0 + k] = acc;
+        for (int k = 0; k < kChainBatch; ++k) x[k] = s_chunk[i0 + k];
+#pragma unroll
+        for (int k = 0; k < kChainBatch; ++k) {
+          acc += x[k];
+          x[k] = acc;
+        }
+        if (i0 + kChainBatch <= len) {
+#pragma unroll
+          for (int k = 0; k < kChainBatch; ++k) out[i0 + k] = x[k];
+        } else {
+#pragma unroll
+          for (int k = 0; k < kChainBatch; ++k)
+            if (i0 + k < len) out[i0 + k] = x[k];
+        }
+      }
     }
-#pragma unroll
-    for (int k = 0; k < kPrefixBatch; ++k) cur[k] = nxt[k];
+    __builtin_amdgcn_wave_barrier();  // lane 0's reads of the chunk are done before it is refilled
   }
 }
 
@@ -769,7 +786,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, keys_in, keys_out, vals_out, prefix, total;
+  size_t state, row_stat, mrow, vals_out, prefix, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -784,10 +801,6 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)rows * sizeof(alloc::RowStat));
   l.mrow = at;
   at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
-  l.keys_in = at;
-  at = align256(at + cells * 8);
-  l.keys_out = at;
-  at = align256(at + cells * 8);
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
@@ -836,15 +849,13 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   p.state = (alloc::State *)(base + l.state);
   p.row_stat = (alloc::RowStat *)(base + l.row_stat);
   m.mrow = (alloc::MaxminRow *)(base + l.mrow);
-  m.keys_in = (unsigned long long *)(base + l.keys_in);
-  m.keys_out = (unsigned long long *)(base + l.keys_out);
   m.vals_out = (int32_t *)(base + l.vals_out);
   m.prefix = (double *)(base + l.prefix);
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
-  hipLaunchKernelGGL(alloc::mm_keys_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_base_kernel, dim3(rows), dim3(kWave), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
   if (width <= 4 * alloc::kSortThreads)
@@ -855,7 +866,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
     hipLaunchKernelGGL(alloc::mm_sort_kernel<12>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
-  hipLaunchKernelGGL(alloc::mm_prefix_kernel, dim3((rows + kWave - 1) / kWave), dim3(kWave), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3(rows), dim3(kWave), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_bisect_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
   return check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
