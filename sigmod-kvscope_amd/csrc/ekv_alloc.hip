@@ -452,6 +452,7 @@ struct MaxminParams {
   MaxminRow *mrow;
   int32_t *vals_out;  // per request, its blocks' indices in sorted order
   double *prefix;     // per request, the running totals of its open shares in that order
+  int32_t *order;     // the requests, longest first: the sorting workgroups' order
 };
 
 // per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts
@@ -489,15 +490,17 @@ __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
 // 2. a block radix sort of them in LDS, stable and descending, so equal keys (such as the pinned
 //    blocks' 0) keep block order and the padding keys 0 past n sort after every block;
 // 3. the sorted block indices, and the open blocks' shares in sorted order (for the totals).
+// The keys per thread (ITEMS) are the fewest that hold the request's n blocks, so a short request
+// sorts only its own length.
 constexpr int kSortThreads = 1024;
 
 template <int ITEMS>
-__global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParams m) {
-  using Sort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
-  __shared__ typename Sort::storage_type storage;
+using RequestSort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
+
+template <int ITEMS>
+__device__ __forceinline__ void sort_request(const MaxminParams &m, const RowStat &st, int r,
+                                             typename RequestSort<ITEMS>::storage_type &storage) {
   const Params &p = m.p;
-  const int r = blockIdx.x;
-  const RowStat st = p.row_stat[r];
   const int n = st.n, open = st.open;
   const double *srow = p.scores + (int64_t)r * p.scores_stride;
   const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
@@ -518,7 +521,7 @@ __global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParam
     keys[i] = (pos < n && !pinned) ? gain_key(share_value(st, score[i])) : 0ull;
     vals[i] = pos;
   }
-  Sort().sort_desc_to_striped(keys, vals, storage);
+  RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage);
   const int64_t row0 = (int64_t)r * p.width;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {  // striped: position i * kSortThreads + thread
@@ -526,6 +529,59 @@ __global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParam
     if (pos < n) m.vals_out[row0 + pos] = vals[i];
     if (pos < open) m.prefix[row0 + pos] = key_value(keys[i]);
   }
+}
+
+// the requests by length, longest first (in classes of 256 blocks; any order within a class, as each
+// sort writes only its own request's outputs), so the longest sorts start first and the short ones
+// fill in behind them rather than leaving a long one to run alone at the end
+constexpr int kOrderStep = 256;
+constexpr int kOrderClasses = kMaxWidth / kOrderStep + 1;
+
+__global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminParams m) {
+  __shared__ int s_count[kOrderClasses], s_next[kOrderClasses];
+  const int tid = threadIdx.x;
+  const int rows = m.p.rows;
+  if (tid < kOrderClasses) s_count[tid] = 0;
+  __syncthreads();
+  for (int r = tid; r < rows; r += kSortThreads) atomicAdd(&s_count[m.p.row_stat[r].n / kOrderStep], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int at = 0;
+    for (int c = kOrderClasses - 1; c >= 0; --c) {
+      s_next[c] = at;
+      at += s_count[c];
+    }
+  }
+  __syncthreads();
+  for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[m.p.row_stat[r].n / kOrderStep], 1)] = r;
+}
+
+template <int MAX_ITEMS>
+__global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParams m) {
+  using Largest = typename RequestSort<MAX_ITEMS>::storage_type;
+  constexpr int kMid = MAX_ITEMS < 8 ? MAX_ITEMS : 8;
+  static_assert(sizeof(typename RequestSort<1>::storage_type) <= sizeof(Largest) &&
+                    sizeof(typename RequestSort<2>::storage_type) <= sizeof(Largest) &&
+                    sizeof(typename RequestSort<4>::storage_type) <= sizeof(Largest) &&
+                    sizeof(typename RequestSort<kMid>::storage_type) <= sizeof(Largest),
+                "the largest sort's storage holds every smaller one");
+  static_assert(alignof(typename RequestSort<1>::storage_type) <= alignof(Largest) &&
+                    alignof(typename RequestSort<kMid>::storage_type) <= alignof(Largest),
+                "and is aligned for it");
+  __shared__ Largest storage;
+  const int r = m.order[blockIdx.x];
+  const RowStat st = m.p.row_stat[r];
+  auto &raw = storage;
+  if (st.n <= kSortThreads)
+    sort_request<1>(m, st, r, reinterpret_cast<typename RequestSort<1>::storage_type &>(raw));
+  else if (st.n <= 2 * kSortThreads)
+    sort_request<2>(m, st, r, reinterpret_cast<typename RequestSort<2>::storage_type &>(raw));
+  else if (MAX_ITEMS == 4 || st.n <= 4 * kSortThreads)
+    sort_request<4>(m, st, r, reinterpret_cast<typename RequestSort<4>::storage_type &>(raw));
+  else if (MAX_ITEMS == 8 || st.n <= 8 * kSortThreads)
+    sort_request<kMid>(m, st, r, reinterpret_cast<typename RequestSort<kMid>::storage_type &>(raw));
+  else
+    sort_request<MAX_ITEMS>(m, st, r, raw);
 }
 
 // per request, one wave: the running totals of its sorted open shares (np.cumsum), in place. One
@@ -786,7 +842,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, vals_out, prefix, total;
+  size_t state, row_stat, mrow, order, vals_out, prefix, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -801,6 +857,8 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)rows * sizeof(alloc::RowStat));
   l.mrow = at;
   at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
+  l.order = at;
+  at = align256(at + (size_t)rows * sizeof(int32_t));
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
@@ -851,11 +909,13 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   m.mrow = (alloc::MaxminRow *)(base + l.mrow);
   m.vals_out = (int32_t *)(base + l.vals_out);
   m.prefix = (double *)(base + l.prefix);
+  m.order = (int32_t *)(base + l.order);
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::mm_base_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_order_kernel, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
   if (width <= 4 * alloc::kSortThreads)

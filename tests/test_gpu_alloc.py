@@ -131,8 +131,9 @@ def test_maxmin_float64_scores_zero_rows_and_long_rows():
 
 
 def test_maxmin_ties_in_rows_sorted_in_lds():
-    # rows of up to 8192 blocks are sorted in LDS (a bitonic sort by share desc, block asc): rows full
-    # of exactly equal shares must keep the stable order the reference's argsort gives
+    # each request's blocks are sorted in LDS (a stable radix sort by share desc, so equal shares keep
+    # block order): rows full of exactly equal shares must keep the stable order the reference's
+    # argsort gives
     rng = np.random.default_rng(9)
     scores = [np.round(rng.random(n) * 8) / 8 for n in (8192, 4097, 1000, 64)]  # 9 distinct values
     scores.append(np.full(300, 0.25))
@@ -163,3 +164,18 @@ def test_maxmin_view_build_configuration():
         print(f"maxmin at {frac}: budget {budget}, kept {sum(int(w.sum()) for w in want)}, mismatched {bad}",
               flush=True)
         assert bad == 0 and int(summary[3]) == 0
+
+
+@pytest.mark.parametrize("rows", [1500, 3000, 6000, 8192])
+def test_maxmin_many_requests(rows):
+    # past 1024 requests each bisection thread carries 2, 4 or 8 of them
+    rng = np.random.default_rng(rows)
+    sizes = rng.integers(1, 30, size=rows)
+    scores = [rng.random(int(n)) for n in sizes]
+    scores[5] = np.zeros(int(sizes[5]))
+    pinned = [oa.default_pins(int(n)) for n in sizes]
+    total, must = int(sizes.sum()), sum(int(p.sum()) for p in pinned)
+    for frac in (0.3, 0.75):
+        budget = max(int(frac * total), must)
+        reqs = [allocation.Request(scores=s, pinned=p) for s, p in zip(scores, pinned)]
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
