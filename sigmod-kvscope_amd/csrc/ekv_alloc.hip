@@ -439,8 +439,7 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
 
 // ---- maxmin --------------------------------------------------------------------------------
 constexpr int kBisectThreads = 1024;
-constexpr int kRowsPerThread = 8;  // rows a bisection thread keeps in registers
-constexpr int kMaxMaxminRows = kBisectThreads * kRowsPerThread;
+constexpr int kMaxMaxminRows = kBisectThreads * 8;  // at most 8 requests per bisection thread
 
 struct MaxminRow {
   double base;  // NumPy's sum of the pinned shares
@@ -453,7 +452,14 @@ struct MaxminParams {
   int32_t *vals_out;  // per request, its blocks' indices in sorted order
   double *prefix;     // per request, the running totals of its open shares in that order
   int32_t *order;     // the requests, longest first: the sorting workgroups' order
+  int32_t *level_count;  // per level j / kLevels, the requests' counts summed
+  uint16_t *level_pos;   // per request and level j / kLevels, its position there
 };
+
+// the bisection's first kLevelBits steps can only reach the levels j / 2^kLevelBits (0 < j < 2^kLevelBits,
+// every one exact in float64, as are the steps' mids (low + high) / 2 on the way there)
+constexpr int kLevelBits = 10;
+constexpr int kLevels = 1 << kLevelBits;
 
 // per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts
 __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
@@ -541,6 +547,7 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   __shared__ int s_count[kOrderClasses], s_next[kOrderClasses];
   const int tid = threadIdx.x;
   const int rows = m.p.rows;
+  for (int j = tid; j < kLevels; j += kSortThreads) m.level_count[j] = 0;  // summed into by mm_levels_kernel
   if (tid < kOrderClasses) s_count[tid] = 0;
   __syncthreads();
   for (int r = tid; r < rows; r += kSortThreads) atomicAdd(&s_count[m.p.row_stat[r].n / kOrderStep], 1);
@@ -646,8 +653,46 @@ __global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) 
   }
 }
 
+// per request, one workgroup: its position and count at every level j / kLevels, the counts added
+// into level_count.  A count is the bisection's (its position among the request's shifted totals,
+// found on the totals staged in LDS), so the first kLevelBits steps of the bisection become a walk
+// over the summed counts, with every CU searching here rather than the bisection's one workgroup, and
+// the positions give the brackets that those steps leave.
+constexpr int kLevelThreads = 256;
+
+template <int CAP>
+__global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminParams m) {
+  __shared__ double s_tot[CAP];  // the request's running totals
+  const int r = blockIdx.x;
+  const MaxminRow mr = m.mrow[r];
+  const int open = mr.open;
+  const double *pre = m.prefix + (int64_t)r * m.p.width;
+  for (int i = threadIdx.x; i < open; i += kLevelThreads) s_tot[i] = pre[i];
+  __syncthreads();
+  const double shift = 2.0 * (double)r;
+  uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+  for (int j = 1 + threadIdx.x; j < kLevels; j += kLevelThreads) {
+    const double level = (double)j / kLevels;
+    const double need = level - mr.base;
+    const double q = (need - 1e-12) + shift;
+    int a = 0, b = open;
+    while (a < b) {  // first position whose shifted total is >= q
+      const int c = (a + b) >> 1;
+      if (s_tot[c] + shift < q) a = c + 1; else b = c;
+    }
+    pos_row[j] = (uint16_t)a;
+    const int count = need <= 1e-12 ? 0 : min(a + 1, open);
+    if (count > 0) atomicAdd(&m.level_count[j], count);  // integer sums: the order does not matter
+  }
+}
+
 // the level's bisection and the leftover, one workgroup
+// RPT: requests per thread (1, 2, 4 or 8 by the request count), so the common case keeps its state
+// in registers
+template <int RPT>
 __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminParams m) {
+  constexpr int kRowsPerThread = RPT;
+  static_assert(RPT >= 1 && RPT * kBisectThreads <= kMaxMaxminRows, "requests per thread");
   __shared__ long long s_red[kBisectThreads / kWave];
   __shared__ double s_best[kBisectThreads / kWave];
   __shared__ int s_best_row[kBisectThreads / kWave];
@@ -682,21 +727,140 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
     pos = a;
     return need <= 1e-12 ? 0 : min(a + 1, open[j]);
   };
-  double low = 0.0, high = 1.0;
-  for (int it = 0; it < 60; ++it) {
-    const double mid = (low + high) / 2;
-    long long local = 0;
+  // the first kLevelBits steps, over the summed counts at the levels j / kLevels
+  __shared__ int s_level[kLevels];
+  for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count[j];
+  __syncthreads();
+  int jl = 0, jh = kLevels;
+  for (int it = 0; it < kLevelBits; ++it) {
+    const int jm = (jl + jh) >> 1;
+    if ((long long)s_level[jm] <= free_blocks) jl = jm; else jh = jm;
+  }
+  double low = (double)jl / kLevels, high = (double)jh / kLevels;
+  // the brackets those steps leave: the positions at low and high, where each side has moved.  A
+  // request's count never falls as the level rises, so one whose counts at low and high agree keeps
+  // that count at every level between them.
+  int f_low[kRowsPerThread], f_high[kRowsPerThread], f_mid[kRowsPerThread];
 #pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j)
-      if (tid + j * kBisectThreads < p.rows) local += count_at(j, mid, mid_pos[j]);
-    const long long total = block_sum<kBisectThreads>(local, s_red);
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    f_low[j] = f_high[j] = f_mid[j] = 0;
+    if (tid + j * kBisectThreads >= p.rows) continue;
+    // the positions at the levels reached come from mm_levels_kernel; the ends 0 and 1 (never a
+    // step's level) are searched, for the counts there
+    const int r = tid + j * kBisectThreads;
+    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+    int pos_low, pos_high;
+    if (jl > 0) {
+      pos_low = pos_row[jl];
+      f_low[j] = (low - base[j]) <= 1e-12 ? 0 : min(pos_low + 1, open[j]);
+    } else {
+      f_low[j] = count_at(j, low, pos_low);
+      pos_low = 0;
+    }
+    if (jh < kLevels) {
+      pos_high = pos_row[jh];
+      f_high[j] = (high - base[j]) <= 1e-12 ? 0 : min(pos_high + 1, open[j]);
+    } else {
+      f_high[j] = count_at(j, high, pos_high);
+      pos_high = open[j];
+    }
+    lo[j] = pos_low;
+    hi[j] = pos_high;
+  }
+  int it = kLevelBits;
+  while (it < 60) {
+    const double mid = (low + high) / 2;
+    long long local = 0, active = 0;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      if (tid + j * kBisectThreads >= p.rows) continue;
+      active += f_low[j] != f_high[j] ? 1 : 0;
+      f_mid[j] = count_at(j, mid, mid_pos[j]);
+      local += f_mid[j];
+    }
+    // the count (below 2^32) and the requests still changing, in one sum
+    const long long packed = block_sum<kBisectThreads>(local + (active << 32), s_red);
+    const long long total = packed & 0xffffffffll;
     const bool up = total <= free_blocks;
     if (up) low = mid; else high = mid;
 #pragma unroll
     for (int j = 0; j < kRowsPerThread; ++j) {
       if (tid + j * kBisectThreads >= p.rows) continue;
-      if (up) lo[j] = mid_pos[j]; else hi[j] = mid_pos[j];
+      if (up) {
+        lo[j] = mid_pos[j];
+        f_low[j] = f_mid[j];
+      } else {
+        hi[j] = mid_pos[j];
+        f_high[j] = f_mid[j];
+      }
     }
+    ++it;
+    if ((packed >> 32) <= kWave) break;  // at most a wave's worth of requests can still change
+  }
+  if (it < 60) {
+    // the rest of the steps in wave 0 over the requests still changing, lane i taking the i-th; the
+    // others add a fixed count.  Their brackets stay with their owners, a superset of where the final
+    // count lies, which the count at the final level finds again.
+    __shared__ int s_nact, s_act_row[kWave], s_act_lo[kWave], s_act_hi[kWave], s_act_open[kWave];
+    __shared__ double s_act_base[kWave], s_level_pair[2];
+    if (tid == 0) s_nact = 0;
+    __syncthreads();
+    long long fixed_local = 0;
+#pragma unroll
+    for (int j = 0; j < kRowsPerThread; ++j) {
+      const int r = tid + j * kBisectThreads;
+      if (r >= p.rows) continue;
+      if (f_low[j] != f_high[j]) {
+        const int i = atomicAdd(&s_nact, 1);
+        s_act_row[i] = r;
+        s_act_lo[i] = lo[j];
+        s_act_hi[i] = hi[j];
+        s_act_open[i] = open[j];
+        s_act_base[i] = base[j];
+      } else {
+        fixed_local += f_low[j];
+      }
+    }
+    const long long fixed = block_sum<kBisectThreads>(fixed_local, s_red);  // its barriers publish the list
+    if (wave == 0) {
+      const bool mine = lane < s_nact;
+      const int r = mine ? s_act_row[lane] : 0;
+      int a_lo = mine ? s_act_lo[lane] : 0, a_hi = mine ? s_act_hi[lane] : 0;
+      const int a_open = mine ? s_act_open[lane] : 0;
+      const double a_base = mine ? s_act_base[lane] : 0.0;
+      const double shift = 2.0 * (double)r;
+      const double *pre = m.prefix + (int64_t)r * p.width;
+      for (; it < 60; ++it) {
+        const double mid = (low + high) / 2;
+        int f = 0, pos = a_lo;
+        if (mine) {
+          const double need = mid - a_base;
+          const double q = (need - 1e-12) + shift;
+          int a = a_lo, b = a_hi;
+          while (a < b) {  // first position whose shifted total is >= q
+            const int c = (a + b) >> 1;
+            if (pre[c] + shift < q) a = c + 1; else b = c;
+          }
+          pos = a;
+          f = need <= 1e-12 ? 0 : min(a + 1, a_open);
+        }
+        const bool up = fixed + (long long)wave_sum_int(f) <= free_blocks;
+        if (up) {
+          low = mid;
+          a_lo = pos;
+        } else {
+          high = mid;
+          a_hi = pos;
+        }
+      }
+      if (lane == 0) {
+        s_level_pair[0] = low;
+        s_level_pair[1] = high;
+      }
+    }
+    __syncthreads();
+    low = s_level_pair[0];
+    high = s_level_pair[1];
   }
   // counts at the final level, then the leftover to the lowest (retained, index) first
   int counts[kRowsPerThread];
@@ -842,7 +1006,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, order, vals_out, prefix, total;
+  size_t state, row_stat, mrow, order, level_count, level_pos, vals_out, prefix, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -859,6 +1023,10 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)rows * sizeof(alloc::MaxminRow));
   l.order = at;
   at = align256(at + (size_t)rows * sizeof(int32_t));
+  l.level_count = at;
+  at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
+  l.level_pos = at;
+  at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
@@ -910,6 +1078,8 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   m.vals_out = (int32_t *)(base + l.vals_out);
   m.prefix = (double *)(base + l.prefix);
   m.order = (int32_t *)(base + l.order);
+  m.level_count = (int32_t *)(base + l.level_count);
+  m.level_pos = (uint16_t *)(base + l.level_pos);
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
@@ -927,7 +1097,21 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3(rows), dim3(kWave), 0, s, m);
-  hipLaunchKernelGGL(alloc::mm_bisect_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  if (width <= 4096)
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<4096>, dim3(rows), dim3(alloc::kLevelThreads), 0, s, m);
+  else if (width <= 8192)
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<8192>, dim3(rows), dim3(alloc::kLevelThreads), 0, s, m);
+  else
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, dim3(rows), dim3(alloc::kLevelThreads), 0, s,
+                       m);
+  if (rows <= alloc::kBisectThreads)
+    hipLaunchKernelGGL(alloc::mm_bisect_kernel<1>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  else if (rows <= 2 * alloc::kBisectThreads)
+    hipLaunchKernelGGL(alloc::mm_bisect_kernel<2>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  else if (rows <= 4 * alloc::kBisectThreads)
+    hipLaunchKernelGGL(alloc::mm_bisect_kernel<4>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  else
+    hipLaunchKernelGGL(alloc::mm_bisect_kernel<8>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
   return check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
 }
