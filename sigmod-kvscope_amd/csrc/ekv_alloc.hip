@@ -12,9 +12,9 @@
 //
 // sum: keep the `free` unpinned blocks of highest weight * share, a tie going to the newer block,
 // then to the earlier request.  The threshold is found by a radix select over order-preserving
-// 64-bit keys of the float64 gains (eight passes of 8 bits over every open block, the gains
-// recomputed in each pass), then among the blocks at the threshold by a select over
-// (block desc, request asc) (four passes).  All state lives in a caller-provided workspace that a
+// 64-bit keys of the float64 gains (six passes of 11-bit digits over every open block, the gains
+// recomputed in each pass), then among the blocks at the threshold by a select over the 30-bit
+// (block desc, request asc) key (three passes).  All state lives in a caller-provided workspace that a
 // kernel clears first, so the launches need no host synchronisation and no memset.
 //
 // maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
@@ -47,8 +47,11 @@ constexpr int kMaxRows = 65535;  // the tie key holds the request in 16 bits
 
 enum Mode : int { kSelect = 0, kKeepAll = 1, kKeepOpen = 2, kPinnedOnly = 3 };
 
+constexpr int kDigitBits = 11;  // radix digits of the select: six gain passes and three tie passes
+constexpr int kBins = 1 << kDigitBits;
+
 struct State {
-  unsigned long long hist[256];
+  unsigned long long hist[kBins];
   unsigned long long prefix, mask, threshold;  // threshold: the gain key at the cut
   long long k_rem, free_blocks, must, sizes, open_total, requests, budget;
   int mode, error;
@@ -314,16 +317,18 @@ __device__ __forceinline__ unsigned long long tie_key(int r, int b) {
   return ((unsigned long long)b << 16) | (unsigned long long)(0xFFFF - r);  // newer block, then earlier request
 }
 
-// one radix pass: the digit histogram of the open blocks whose key matches the prefix so far
-// (tie passes: the blocks at the gain threshold, over the tie key).  Workgroup w takes rows
-// w, w + grid, ..., so each workgroup flushes its LDS histogram to the global one once.
+// one radix pass: the histogram of the `bits`-wide digit at `shift` over the open blocks whose key
+// matches the prefix so far (tie passes: the blocks at the gain threshold, over the tie key).
+// Workgroup w takes rows w, w + grid, ..., so each workgroup flushes its LDS histogram to the global
+// one once.
 template <bool TIE>
-__global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift) {
-  __shared__ unsigned int s_hist[256];
+__global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits) {
+  __shared__ unsigned int s_hist[kBins];
   const State *s = p.state;
   if (s->mode != kSelect || s->error) return;
-  s_hist[threadIdx.x] = 0u;
+  for (int i = threadIdx.x; i < kBins; i += kThreads) s_hist[i] = 0u;
   __syncthreads();
+  const unsigned int digit_mask = (1u << bits) - 1u;
   const unsigned long long prefix = s->prefix, mask = s->mask, threshold = s->threshold;
   for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
     const RowStat st = p.row_stat[r];
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
           }
           if (take && (key & mask) == prefix) {
             counted = true;
-            digit = (unsigned int)(key >> shift) & 255u;
+            digit = (unsigned int)(key >> shift) & digit_mask;
           }
         }
         // when every counting lane of the wave has one digit (the first passes), one add for all
@@ -365,20 +370,29 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
     }
   }
   __syncthreads();
-  const unsigned int c = s_hist[threadIdx.x];
-  if (c) atomicAdd(&p.state->hist[threadIdx.x], (unsigned long long)c);
+  for (int i = threadIdx.x; i < kBins; i += kThreads) {
+    const unsigned int c = s_hist[i];
+    if (c) atomicAdd(&p.state->hist[i], (unsigned long long)c);
+  }
 }
 
-// the digit where the k_rem-th largest key lies; the next pass's prefix
-__global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shift, int last_gain_pass) {
+// the digit where the k_rem-th largest key lies; the next pass's prefix.  Thread t holds the
+// kBins / kThreads digits below kBins - (kBins / kThreads) t, in descending order.
+__global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shift, int bits, int last_gain_pass) {
+  constexpr int kPer = kBins / kThreads;
   __shared__ long long s_scan[kThreads / kWave];
   State *s = p.state;
   if (s->mode != kSelect || s->error) return;
   const int t = threadIdx.x;
-  const long long h = (long long)s->hist[255 - t];  // thread t looks at digit 255 - t
-  // inclusive scan over the threads: the keys at digits >= 255 - t
+  long long h[kPer], mine = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    h[i] = (long long)s->hist[kBins - 1 - (kPer * t + i)];
+    mine += h[i];
+  }
+  // inclusive scan over the threads: the keys at digits >= this thread's lowest
   const int lane = lane_id(), wave = t / kWave;
-  long long inc = h;
+  long long inc = mine;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     const long long up = __shfl_up(inc, d, kWave);
@@ -389,17 +403,24 @@ __global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shif
   long long base = 0;
   for (int w = 0; w < wave; ++w) base += s_scan[w];
   inc += base;
-  const long long before = inc - h;
+  long long before = inc - mine;
   const long long k_rem = s->k_rem;
   __syncthreads();
   if (before < k_rem && inc >= k_rem) {
-    s->prefix |= (unsigned long long)(255 - t) << shift;
-    s->k_rem = k_rem - before;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (before < k_rem && before + h[i] >= k_rem) {
+        s->prefix |= (unsigned long long)(kBins - 1 - (kPer * t + i)) << shift;
+        s->k_rem = k_rem - before;
+      }
+      before += h[i];
+    }
   }
-  s->hist[t] = 0ull;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) s->hist[kBins - 1 - (kPer * t + i)] = 0ull;
   __syncthreads();
   if (t == 0) {
-    s->mask |= 255ull << shift;
+    s->mask |= ((1ull << bits) - 1ull) << shift;
     if (last_gain_pass) {  // the gain threshold is complete: the tie passes start
       s->threshold = s->prefix;
       s->prefix = 0ull;
@@ -991,13 +1012,18 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
-  for (int pass = 0; pass < 8; ++pass) {  // the gain threshold, 8 bits at a time from the top
-    hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, 56 - 8 * pass);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, 56 - 8 * pass, pass == 7);
+  // the gain threshold, kDigitBits at a time from the top of the 64-bit key
+  for (int top = 64; top > 0; top -= alloc::kDigitBits) {
+    const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
+    hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
+    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, shift == 0);
   }
-  for (int pass = 0; pass < 4; ++pass) {  // among the blocks at the threshold: newer block, earlier request
-    hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, 24 - 8 * pass);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, 24 - 8 * pass, 0);
+  // among the blocks at the threshold: newer block, earlier request (the 30-bit tie key)
+  static_assert(alloc::kMaxWidth <= (1 << 14), "the tie key's block field is 14 bits");
+  for (int top = 30; top > 0; top -= alloc::kDigitBits) {
+    const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
+    hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
+    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, 0);
   }
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
