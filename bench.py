@@ -46,6 +46,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
     ap.add_argument("--chunk-tiles", type=int, default=0)
     ap.add_argument("--profile-only", action="store_true", help="run the graph replays only (for rocprof)")
+    ap.add_argument("--objectives-only", action="store_true",
+                    help="time the 1024 x 8192 view build and the sum / maxmin objectives only (for rocprof)")
     return ap.parse_args()
 
 
@@ -316,6 +318,53 @@ def cpu_baseline(step: Step, bound_s: float) -> dict:
     }
 
 
+def view_build_config(handle: int, stream) -> dict:
+    """Medians (ms) of the view build (uniform ranking + compaction) and the sum / maxmin objectives on
+    1024 rows x U[1, 8192] blocks at budget 0.5."""
+    import numpy as np
+    import torch
+
+    import ekv_hip
+    import workloads
+    from observe.allocation import maxmin_keep, sum_keep
+
+    # ranking + compaction of 1024 rows x up to 8192 blocks
+    c4 = workloads.config4()
+    s4 = torch.from_numpy(c4["shares"]).cuda()
+    n4 = torch.from_numpy(c4["blocks"]).cuda()
+    t4 = torch.from_numpy(c4["table"]).cuda()
+    l4 = torch.from_numpy(c4["seq_lens"]).cuda()
+    k4 = torch.empty_like(s4, dtype=torch.uint8)
+    v4 = torch.empty_like(t4)
+    vl4 = torch.empty_like(l4)
+    sm4 = torch.zeros(6, dtype=torch.int64, device="cuda")
+
+    def rank_c4():
+        ekv_hip.call("ekv_rank_uniform", s4.data_ptr(), 8192, n4.data_ptr(), 0, 0, 0, 0, 0, 0, 0, 1024, 8192, 0.5,
+                     -1, k4.data_ptr(), 8192, sm4.data_ptr(), handle)
+
+    def compact_c4():
+        ekv_hip.call("ekv_compact_view", t4.data_ptr(), 8192, l4.data_ptr(), k4.data_ptr(), 8192, 1024, 8192, 16,
+                     v4.data_ptr(), 8192, vl4.data_ptr(), handle)
+
+    def view_build_c4():
+        rank_c4()
+        compact_c4()
+
+    view_build_c4()
+    out = {"view_build": float(np.median(time_events(view_build_c4, 20, stream))),
+           "rank": float(np.median(time_events(rank_c4, 20, stream))),
+           "compact": float(np.median(time_events(compact_c4, 20, stream)))}
+    # the other objectives on the same rows: sum (global top-k) and maxmin (water level)
+    s4_64 = s4.double()
+    b4 = int(np.ceil(0.5 * int(c4["blocks"].sum())))
+    sum_keep(s4_64, n4, budget=b4)
+    out["sum"] = float(np.median(time_events(lambda: sum_keep(s4_64, n4, budget=b4), 10, stream)))
+    maxmin_keep(s4_64, n4, budget=b4)
+    out["maxmin"] = float(np.median(time_events(lambda: maxmin_keep(s4_64, n4, budget=b4), 5, stream)))
+    return out
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -328,6 +377,11 @@ def main() -> None:
     import workloads
 
     torch.cuda.set_device(0)
+    if args.objectives_only:
+        stream = torch.cuda.current_stream()
+        times = view_build_config(int(stream.cuda_stream), stream)
+        print(json.dumps({"objectives_only": True, **{k + "_us": round(v * 1e3, 2) for k, v in times.items()}}))
+        return
     batch = workloads.config2_batch()
     step = Step(batch, args.chunk_tiles)
     stream = torch.cuda.current_stream()
@@ -426,44 +480,7 @@ def main() -> None:
                                  chunk_tiles=args.chunk_tiles), 10, stream)))
     all_gbs = audit_bytes(batch, batch.kv_heads) / (all_ms * 1e-3) / 1e9
 
-    # the view-build configuration: ranking + compaction of 1024 rows x up to 8192 blocks
-    c4 = workloads.config4()
-    s4 = torch.from_numpy(c4["shares"]).cuda()
-    n4 = torch.from_numpy(c4["blocks"]).cuda()
-    t4 = torch.from_numpy(c4["table"]).cuda()
-    l4 = torch.from_numpy(c4["seq_lens"]).cuda()
-    k4 = torch.empty_like(s4, dtype=torch.uint8)
-    v4 = torch.empty_like(t4)
-    vl4 = torch.empty_like(l4)
-    sm4 = torch.zeros(6, dtype=torch.int64, device="cuda")
-
-    def rank_c4():
-        step.ekv.call("ekv_rank_uniform", s4.data_ptr(), 8192, n4.data_ptr(), 0, 0, 0, 0, 0, 0, 0, 1024, 8192, 0.5,
-                      -1, k4.data_ptr(), 8192, sm4.data_ptr(), handle)
-
-    def compact_c4():
-        step.ekv.call("ekv_compact_view", t4.data_ptr(), 8192, l4.data_ptr(), k4.data_ptr(), 8192, 1024, 8192, 16,
-                      v4.data_ptr(), 8192, vl4.data_ptr(), handle)
-
-    def view_build_c4():
-        rank_c4()
-        compact_c4()
-
-    view_build_c4()
-    c4_ms = float(np.median(time_events(view_build_c4, 20, stream)))
-    c4_rank_ms = float(np.median(time_events(rank_c4, 20, stream)))
-    c4_compact_ms = float(np.median(time_events(compact_c4, 20, stream)))
-    # the other objectives on the same rows: sum (global top-k) and maxmin (water level)
-    from observe.allocation import maxmin_keep, sum_keep
-
-    s4_64 = s4.double()
-    b4 = int(np.ceil(0.5 * int(c4["blocks"].sum())))
-    sum_keep(s4_64, n4, budget=b4)
-    c4_sum_ms = float(np.median(time_events(lambda: sum_keep(s4_64, n4, budget=b4), 10, stream)))
-    maxmin_keep(s4_64, n4, budget=b4)
-    c4_maxmin_ms = float(np.median(time_events(lambda: maxmin_keep(s4_64, n4, budget=b4), 5, stream)))
-    del s4_64
-
+    c4_times = view_build_config(handle, stream)
     others = other_audit_shapes()
     peak = copy_peak_gbs()
     traffic = profiled_traffic()
@@ -512,11 +529,11 @@ def main() -> None:
                                 "gbs": round(all_gbs, 1), "frac": round(all_gbs / HBM_PEAK_GBS, 4)},
         "other_audit_shapes": others,
         "view_build_us": {"llama3_step_128_rows": round(view_ms * 1e3, 2),
-                          "config_1024x8192_budget_0.5": round(c4_ms * 1e3, 2),
-                          "config_1024x8192_rank": round(c4_rank_ms * 1e3, 2),
-                          "config_1024x8192_compact": round(c4_compact_ms * 1e3, 2),
-                          "config_1024x8192_sum_objective": round(c4_sum_ms * 1e3, 2),
-                          "config_1024x8192_maxmin_objective": round(c4_maxmin_ms * 1e3, 2)},
+                          "config_1024x8192_budget_0.5": round(c4_times["view_build"] * 1e3, 2),
+                          "config_1024x8192_rank": round(c4_times["rank"] * 1e3, 2),
+                          "config_1024x8192_compact": round(c4_times["compact"] * 1e3, 2),
+                          "config_1024x8192_sum_objective": round(c4_times["sum"] * 1e3, 2),
+                          "config_1024x8192_maxmin_objective": round(c4_times["maxmin"] * 1e3, 2)},
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu:
