@@ -161,6 +161,22 @@ int ekv_rank_uniform(const float *scores, int64_t scores_stride, const int32_t *
                      void *stream);
 
 /*
+ * ekv_rank_uniform followed by ekv_compact_view on the keep it writes, in one kernel: the view
+ * build of allocate(..., "uniform") (observe/allocation.py:39-91, with the controller's pins and
+ * budget, observe/controller.py:398-451) and compact_block_table (runtime/block_view.py:36-56).
+ * The reference runs the two as separate steps; here each row's workgroup compacts its table row
+ * from the keep bytes it has just decided, kept in LDS.  keep, summary, view_table and view_lens
+ * are written exactly as the two calls in sequence write them (rows of blocks[r] blocks for the
+ * ranking, of ceil(seq_lens[r] / block_size) for the view).  No explicit pinned / released masks.
+ */
+int ekv_rank_uniform_view(const float *scores, int64_t scores_stride, const int32_t *blocks,
+                          const uint8_t *measured, const int32_t *pin_from, int32_t recent_blocks,
+                          int32_t rows, int32_t width, double fraction, int64_t budget, uint8_t *keep,
+                          int64_t keep_stride, int64_t *summary, const int32_t *table, int64_t table_stride,
+                          const int32_t *seq_lens, int32_t block_size, int32_t *view_table, int64_t view_stride,
+                          int32_t *view_lens, void *stream);
+
+/*
  * ekv_rank_uniform with a caller-owned device workspace of 2 * rows int32, where a first
  * kernel counts each row's existing and pinned blocks when explicit masks are given.
  */

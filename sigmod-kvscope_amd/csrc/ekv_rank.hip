@@ -56,6 +56,14 @@ struct Params {
   uint8_t *keep;
   int64_t keep_stride;
   int64_t *summary;
+  // the view built from the keep (ekv_rank_uniform_view only)
+  const int32_t *table;
+  int64_t table_stride;
+  const int32_t *seq_lens;
+  int32_t block_size;
+  int32_t *view_table;
+  int64_t view_stride;
+  int32_t *view_lens;
 };
 
 struct RowInfo {
@@ -132,10 +140,85 @@ __device__ __forceinline__ void block_sums(long long (&v)[N], long long (*scratc
   __syncthreads();
 }
 
-// PER: blocks per thread (the row's width is at most kThreads * PER)
+// compact_block_table (runtime/block_view.py:36-56) of the row on the keep bytes in LDS, which the
+// ranking has just decided: keep'[b] = (keep[b] | b == 0 | b == n-1) & b < n for n = ceil(L / bs)
+// from the row's token length; the row's entries stably partitioned, keep' first, then the rest,
+// each in original order.  Thread t takes the contiguous run of PER entries from t * PER (16-byte
+// table loads), one block scan of the threads' kept counts places every entry, the row is assembled
+// in LDS and written with 16-byte stores.  (Loading the run at the kernel's entry, beside the
+// scores, was slower: 49 against 46 us at 1024 rows x 8192 blocks.)
 template <int PER>
+__device__ __forceinline__ void load_run(const Params &p, int row, int32_t (&entry)[PER]) {
+  static_assert(PER % 4 == 0, "runs of whole 16-byte groups");
+  const int W = p.width;
+  const int32_t *trow = p.table + (int64_t)row * p.table_stride;
+  const int b0 = threadIdx.x * PER;
+  if (b0 + PER <= W && ((uintptr_t)(trow + b0) & 15) == 0) {
+#pragma unroll
+    for (int g = 0; g < PER / 4; ++g) {
+      const int4 t4 = *reinterpret_cast<const int4 *>(trow + b0 + 4 * g);
+      entry[4 * g] = t4.x;
+      entry[4 * g + 1] = t4.y;
+      entry[4 * g + 2] = t4.z;
+      entry[4 * g + 3] = t4.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) entry[i] = b0 + i < W ? trow[b0 + i] : 0;
+  }
+}
+
+template <int PER>
+__device__ __forceinline__ void view_row(const Params &p, int row, int L, const int32_t (&entry)[PER],
+                                         const uint8_t *s_keep, int32_t *s_out, int *s_scan) {
+  const int tid = threadIdx.x;
+  const int W = p.width;
+  const long long n64 = L > 0 ? ((long long)L + p.block_size - 1) / p.block_size : 0;  // block_view.py:49
+  const int n = n64 > W + 1LL ? W + 1 : (int)n64;
+  const int b0 = tid * PER;
+  uint32_t kept_bits = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = b0 + i;
+    const bool k = b < W && s_keep[b] != 0;
+    kept_bits |= (b < W && (k || b == 0 || b == n - 1) && b < n) ? (1u << i) : 0u;
+  }
+  int total_kept;
+  int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = b0 + i;
+    if (b >= W) continue;
+    if ((kept_bits >> i) & 1u) s_out[before++] = entry[i];
+    else s_out[total_kept + (b - before)] = entry[i];  // dropped: after the kept ones, in order
+  }
+  __syncthreads();
+  int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
+  if (((uintptr_t)vrow & 15) == 0) {
+    for (int q = tid; 4 * q < W; q += kThreads) {
+      if (4 * q + 3 < W) {
+        *reinterpret_cast<int4 *>(vrow + 4 * q) =
+            make_int4(s_out[4 * q], s_out[4 * q + 1], s_out[4 * q + 2], s_out[4 * q + 3]);
+      } else {
+        for (int b = 4 * q; b < W; ++b) vrow[b] = s_out[b];
+      }
+    }
+  } else {
+    for (int b = tid; b < W; b += kThreads) vrow[b] = s_out[b];
+  }
+  if (tid == 0) {  // block_view.py:53-55
+    const int last = L - (int)(n64 - 1) * p.block_size;
+    p.view_lens[row] = n64 > 0 ? (total_kept - 1) * p.block_size + last : 0;
+  }
+}
+
+// PER: blocks per thread (the row's width is at most kThreads * PER).  VIEW: also build the row's
+// view from the keep it decides (ekv_rank_uniform_view).
+template <int PER, bool VIEW = false>
 __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   constexpr int kPer = PER;
+  __shared__ uint8_t s_keep[VIEW ? kPer * kThreads : 1];
+  __shared__ int32_t s_out[VIEW ? kPer * kThreads : 1];
   __shared__ long long s_red[5][kWaves];
   __shared__ int s_hist[2][256];
   __shared__ int s_count[kPer * kWaves];  // equal keys per (load, wave), then their exclusive scan
@@ -151,6 +234,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   // The loads are issued first and bounded by the width only, so that they overlap the row
   // counts' loads and reductions below instead of waiting for them.
   const RowInfo me = row_info(p, row);
+  const int view_len_in = VIEW ? p.seq_lens[row] : 0;
   const float *srow = p.scores + (int64_t)row * p.scores_stride;
   float sv[kPer];
   uint32_t gone_bits = 0, pin_mask_bits = 0;  // released / explicitly pinned, from the masks
@@ -216,7 +300,16 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
 
   uint8_t *keep_row = p.keep + (int64_t)row * p.keep_stride;
   if (!me.part || error) {  // rows without evidence read in full, controller.py:401
-    for (int b = tid; b < p.width; b += kThreads) keep_row[b] = 1;
+    for (int b = tid; b < p.width; b += kThreads) {
+      keep_row[b] = 1;
+      if constexpr (VIEW) s_keep[b] = 1;
+    }
+    if constexpr (VIEW) {
+      int32_t entry[kPer];
+      load_run<kPer>(p, row, entry);
+      __syncthreads();
+      view_row<kPer>(p, row, view_len_in, entry, s_keep, s_out, s_scan);
+    }
     return;
   }
 
@@ -383,6 +476,13 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     else if ((pin_bits >> i) & 1u) k = 1;
     else k = (open_keep >> i) & 1u;
     keep_row[b] = k;
+    if constexpr (VIEW) s_keep[b] = k;
+  }
+  if constexpr (VIEW) {
+    int32_t entry[kPer];
+    load_run<kPer>(p, row, entry);
+    __syncthreads();
+    view_row<kPer>(p, row, view_len_in, entry, s_keep, s_out, s_scan);
   }
 }
 
@@ -400,6 +500,56 @@ extern "C" int ekv_rank_uniform(const float *scores, int64_t scores_stride, cons
   return ekv_rank_uniform_ws(scores, scores_stride, blocks, measured, pinned, pinned_stride, pin_from,
                              recent_blocks, released, released_stride, rows, width, fraction, budget, keep,
                              keep_stride, summary, nullptr, stream);
+}
+
+extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride, const int32_t *blocks,
+                                     const uint8_t *measured, const int32_t *pin_from, int32_t recent_blocks,
+                                     int32_t rows, int32_t width, double fraction, int64_t budget, uint8_t *keep,
+                                     int64_t keep_stride, int64_t *summary, const int32_t *table,
+                                     int64_t table_stride, const int32_t *seq_lens, int32_t block_size,
+                                     int32_t *view_table, int64_t view_stride, int32_t *view_lens, void *stream) {
+  if (scores == nullptr || blocks == nullptr || keep == nullptr || table == nullptr || seq_lens == nullptr ||
+      view_table == nullptr || view_lens == nullptr)
+    return fail(EKV_EINVAL, "ekv_rank_uniform_view: null pointer");
+  if (rows < 0 || width < 1 || width > rank::kMaxWidth)
+    return fail(EKV_EINVAL, "ekv_rank_uniform_view: rows %d, width %d (at most %d)", rows, width, rank::kMaxWidth);
+  if (recent_blocks < 0) return fail(EKV_EINVAL, "ekv_rank_uniform_view: recent_blocks %d < 0", recent_blocks);
+  if (budget < 0 && !(fraction > 0.0 && fraction <= 1.0))
+    return fail(EKV_EINVAL, "ekv_rank_uniform_view: the budget fraction %g is not in (0, 1]", fraction);
+  if (block_size < 1) return fail(EKV_EINVAL, "ekv_rank_uniform_view: block size %d", block_size);
+  if (rows == 0) return EKV_OK;
+  rank::Params p{};
+  p.scores = scores;
+  p.scores_stride = scores_stride;
+  p.blocks = blocks;
+  p.measured = measured;
+  p.pin_from = pin_from;
+  p.recent = recent_blocks;
+  p.rows = rows;
+  p.width = width;
+  p.fraction = fraction;
+  p.budget_in = budget;
+  p.keep = keep;
+  p.keep_stride = keep_stride;
+  p.summary = summary;
+  p.table = table;
+  p.table_stride = table_stride;
+  p.seq_lens = seq_lens;
+  p.block_size = block_size;
+  p.view_table = view_table;
+  p.view_stride = view_stride;
+  p.view_lens = view_lens;
+  hipStream_t s = (hipStream_t)stream;
+  const int per = (width + rank::kThreads - 1) / rank::kThreads;
+  if (per <= 4)
+    hipLaunchKernelGGL((rank::rank_kernel<4, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (per <= 8)
+    hipLaunchKernelGGL((rank::rank_kernel<8, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (per <= 16)
+    hipLaunchKernelGGL((rank::rank_kernel<16, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((rank::rank_kernel<24, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  return check_hip(hipGetLastError(), "ekv_rank_uniform_view launch");
 }
 
 extern "C" int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_t *blocks,

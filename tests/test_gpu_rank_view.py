@@ -1,0 +1,81 @@
+"""The fused ranking + view (ekv_rank_uniform_view) against the two calls it replaces: the uniform
+keep (observe/allocation.py:39-91 with observe/controller.py:398-451) and compact_block_table on that
+keep (runtime/block_view.py:36-56).  keep, summary, view and lengths must be bit-identical, and the
+view must be the oracle's compaction of the keep."""
+
+import numpy as np
+import pytest
+import torch
+
+import workloads
+from observe.allocation import uniform_keep
+from oracle import block_view as obv
+from runtime.block_view import compact_block_table, uniform_view
+
+pytestmark = pytest.mark.gpu
+
+
+def both(scores, blocks, table, seq_lens, block_size, **kw):
+    keep, summary, view, lens = uniform_view(scores, blocks, table, seq_lens, block_size, **kw)
+    keep2, summary2 = uniform_keep(scores, blocks, **kw)
+    view2, lens2 = compact_block_table(table, seq_lens, keep2, block_size)
+    got = [t.cpu().numpy() for t in (keep, summary, view, lens)]
+    want = [t.cpu().numpy() for t in (keep2, summary2, view2, lens2)]
+    for name, g, w in zip(("keep", "summary", "view", "lens"), got, want):
+        assert np.array_equal(g, w), name
+    return got
+
+
+@pytest.mark.parametrize("fraction", [0.2, 0.5, 0.8])
+def test_view_build_configuration(fraction):
+    c = workloads.config4()
+    scores = torch.from_numpy(c["shares"]).cuda()
+    blocks = torch.from_numpy(c["blocks"]).cuda()
+    table = torch.from_numpy(c["table"]).cuda()
+    lens = torch.from_numpy(c["seq_lens"]).cuda()
+    keep, summary, view, view_lens = both(scores, blocks, table, lens, c["block_size"], fraction=fraction,
+                                          recent_blocks=4)
+    print(f"fraction {fraction}: budget {summary[0]}, kept {int(keep.sum())}", flush=True)
+    want_view, want_lens = obv.compact(c["table"], c["seq_lens"], keep.astype(bool), c["block_size"])
+    assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens)
+
+
+@pytest.mark.parametrize("width", [1, 7, 63, 2048, 2049, 4097, 8192, 12288])
+def test_every_row_layout_width(width):
+    # every register layout of the ranking (4 / 8 / 16 / 24 blocks per thread), rows whose token
+    # length disagrees with their block count (empty, shorter, past the width), rows that do not
+    # take part, explicit pin starts, and an exact budget
+    rng = np.random.default_rng(width)
+    rows, bs = 48, 16
+    blocks = rng.integers(0, width + 1, size=rows).astype(np.int32)
+    blocks[:3] = [0, width, 1]
+    lens = (blocks.astype(np.int64) * bs - rng.integers(0, bs, size=rows)).clip(0).astype(np.int32)
+    lens[3] = 0
+    lens[4] = (width + 3) * bs
+    lens[5] = max(int(blocks[5]) - 2, 0) * bs
+    scores = rng.random((rows, width), dtype=np.float32)
+    scores[6, : width // 2] = 0.25  # ties go to the lower block
+    table = rng.integers(0, 1 << 30, size=(rows, width)).astype(np.int32)
+    measured = (rng.random(rows) < 0.9).astype(np.uint8)
+    pin_from = rng.integers(0, width + 1, size=rows).astype(np.int32)
+    dev = {k: torch.from_numpy(v).cuda() for k, v in
+           dict(scores=scores, blocks=blocks, table=table, lens=lens, measured=measured, pin_from=pin_from).items()}
+    print(f"width {width}", flush=True)
+    for kw in (dict(fraction=0.5), dict(fraction=0.3, recent_blocks=2, measured=dev["measured"]),
+               dict(budget=int(blocks.sum()) // 3, pin_from=dev["pin_from"])):
+        keep, summary, view, view_lens = both(dev["scores"], dev["blocks"], dev["table"], dev["lens"], bs, **kw)
+        want_view, want_lens = obv.compact(table, lens, keep.astype(bool), bs)
+        assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens), kw
+
+
+def test_budget_below_the_pins_keeps_every_block():
+    rng = np.random.default_rng(3)
+    rows, width, bs = 20, 300, 16
+    blocks = np.full(rows, width, np.int32)
+    lens = (blocks * bs).astype(np.int32)
+    scores = torch.from_numpy(rng.random((rows, width), dtype=np.float32)).cuda()
+    table = torch.from_numpy(rng.integers(0, 1 << 20, size=(rows, width)).astype(np.int32)).cuda()
+    keep, summary, view, view_lens = both(scores, torch.from_numpy(blocks).cuda(), table,
+                                          torch.from_numpy(lens).cuda(), bs, budget=3, recent_blocks=8)
+    assert summary[3] == 1 and keep.all()
+    assert np.array_equal(view, table.cpu().numpy()) and np.array_equal(view_lens, lens)
