@@ -375,7 +375,7 @@ def view_build_config(handle: int, stream) -> dict:
 def main() -> None:
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this build has no multi-GPU path",
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); this library has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
     import numpy as np

@@ -1,8 +1,8 @@
 """Oracle: a CPU restatement of KVScope's audit / tile-share / ranking / view hot path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may import it, and only as the checker (or, in ``bench.py``, as the timed
-CPU baseline) -- never as the thing measured or shipped.  The product path is the HIP library
+leg of ``bench.py`` may import it, and only as the reference the results are compared with (or,
+in ``bench.py``, as the timed CPU baseline) -- never as the thing measured or shipped.  The product path is the HIP library
 (``sigmod-kvscope_amd/``) and fails loudly without it.
 
 Modules, each citing the reference file:line it follows:

@@ -1,7 +1,7 @@
 """CPU restatement of the budget split across requests (observe/allocation.py:39-166).
 
-TEST INFRASTRUCTURE ONLY: the checker of ``ekv_rank_uniform``, ``ekv_rank_sum`` and
-``ekv_rank_maxmin``, never the product path.
+TEST INFRASTRUCTURE ONLY: what the results of ``ekv_rank_uniform``, ``ekv_rank_sum`` and
+``ekv_rank_maxmin`` are compared with, never the product path.
 
 ``shares`` follows Request.shares (``:46-52``): scores clamped at 0 in float64 over their sum, or
 equal shares when the sum is not positive.  ``allocate_uniform`` follows allocate (``:55-67``)

@@ -1,6 +1,7 @@
 """The SGLang index-list compaction restated on the CPU (runtime/sglang_compact.py:22-106).
 
-TEST INFRASTRUCTURE ONLY: the checker of ``ekv_compact_slots``, never the product path.
+TEST INFRASTRUCTURE ONLY: what the results of ``ekv_compact_slots`` are compared with, never the product
+path.
 """
 
 from __future__ import annotations
