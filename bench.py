@@ -194,15 +194,15 @@ class Step:
         self.rank_view(stream)
 
     def rank_view(self, stream: int) -> None:
+        # the uniform ranking and DecodeView.build on its keep (live decoding rows, with the read
+        # counters), in one kernel: the same keep, view, lengths and counters as ekv_rank_uniform
+        # followed by ekv_build_view
         b = self.batch
         self.ekv.call(
-            "ekv_rank_uniform", self.shares.data_ptr(), b.width, self.blocks.data_ptr(), 0, 0, 0, 0, RECENT, 0, 0,
-            b.rows, b.width, FRACTION, -1, self.keep.data_ptr(), b.width, self.summary.data_ptr(), stream,
-        )
-        self.ekv.call(
-            "ekv_build_view", self.table.data_ptr(), b.width, self.lens.data_ptr(), self.keep.data_ptr(), b.width,
-            0, 0, 0, 0, 1, b.rows, b.width, b.block_size, self.view.data_ptr(), b.width, self.view_lens.data_ptr(),
-            self.counts.data_ptr(), stream,
+            "ekv_rank_uniform_view", self.shares.data_ptr(), b.width, self.blocks.data_ptr(), 0, 0, RECENT,
+            b.rows, b.width, FRACTION, -1, self.keep.data_ptr(), b.width, self.summary.data_ptr(),
+            self.table.data_ptr(), b.width, self.lens.data_ptr(), b.block_size, self.view.data_ptr(), b.width,
+            self.view_lens.data_ptr(), self.counts.data_ptr(), stream,
         )
 
     def run(self, stream: int) -> None:
@@ -354,7 +354,7 @@ def view_build_config(handle: int, stream) -> dict:
     def fused_c4():  # the same two results from one kernel (ekv_rank_uniform_view)
         ekv_hip.call("ekv_rank_uniform_view", s4.data_ptr(), 8192, n4.data_ptr(), 0, 0, 0, 1024, 8192, 0.5, -1,
                      k4.data_ptr(), 8192, sm4.data_ptr(), t4.data_ptr(), 8192, l4.data_ptr(), 16, v4.data_ptr(),
-                     8192, vl4.data_ptr(), handle)
+                     8192, vl4.data_ptr(), 0, handle)
 
     view_build_c4()
     fused_c4()

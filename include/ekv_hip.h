@@ -168,13 +168,16 @@ int ekv_rank_uniform(const float *scores, int64_t scores_stride, const int32_t *
  * from the keep bytes it has just decided, kept in LDS.  keep, summary, view_table and view_lens
  * are written exactly as the two calls in sequence write them (rows of blocks[r] blocks for the
  * ranking, of ceil(seq_lens[r] / block_size) for the view).  No explicit pinned / released masks.
+ * counts (int64[rows][5], NULL: none): DecodeView's read counters, accumulated as ekv_build_view
+ * accumulates them for live decoding rows outside the audit with the same keep
+ * (runtime/block_view.py:313-329); the view is then ekv_build_view's with that keep.
  */
 int ekv_rank_uniform_view(const float *scores, int64_t scores_stride, const int32_t *blocks,
                           const uint8_t *measured, const int32_t *pin_from, int32_t recent_blocks,
                           int32_t rows, int32_t width, double fraction, int64_t budget, uint8_t *keep,
                           int64_t keep_stride, int64_t *summary, const int32_t *table, int64_t table_stride,
                           const int32_t *seq_lens, int32_t block_size, int32_t *view_table, int64_t view_stride,
-                          int32_t *view_lens, void *stream);
+                          int32_t *view_lens, int64_t *counts, void *stream);
 
 /*
  * ekv_rank_uniform with a caller-owned device workspace of 2 * rows int32, where a first

@@ -64,6 +64,7 @@ struct Params {
   int32_t *view_table;
   int64_t view_stride;
   int32_t *view_lens;
+  long long *view_counts;  // [rows][5] DecodeView's read counters, accumulated (NULL: none)
 };
 
 struct RowInfo {
@@ -169,8 +170,9 @@ __device__ __forceinline__ void load_run(const Params &p, int row, int32_t (&ent
 }
 
 template <int PER>
-__device__ __forceinline__ void view_row(const Params &p, int row, int L, const int32_t (&entry)[PER],
-                                         const uint8_t *s_keep, int32_t *s_out, int *s_scan) {
+__device__ __forceinline__ void view_row(const Params &p, int row, int L, const long long (&c_in)[5],
+                                         const int32_t (&entry)[PER], const uint8_t *s_keep, int32_t *s_out,
+                                         int *s_scan) {
   const int tid = threadIdx.x;
   const int W = p.width;
   const long long n64 = L > 0 ? ((long long)L + p.block_size - 1) / p.block_size : 0;  // block_view.py:49
@@ -207,8 +209,21 @@ __device__ __forceinline__ void view_row(const Params &p, int row, int L, const 
     for (int b = tid; b < W; b += kThreads) vrow[b] = s_out[b];
   }
   if (tid == 0) {  // block_view.py:53-55
-    const int last = L - (int)(n64 - 1) * p.block_size;
-    p.view_lens[row] = n64 > 0 ? (total_kept - 1) * p.block_size + last : 0;
+    const int bs = p.block_size;
+    const int last = L - (int)(n64 - 1) * bs;
+    const int view_len = n64 > 0 ? (total_kept - 1) * bs + last : 0;
+    p.view_lens[row] = view_len;
+    if (p.view_counts != nullptr) {
+      // DecodeView._count for a live decoding row outside the audit (block_view.py:313-329): blocks
+      // read, blocks in full, none audited, reads of a whole row, none expired
+      const long long read = view_len > 0 ? ((long long)view_len + bs - 1) / bs : 0;
+      long long *c = p.view_counts + 5LL * row;
+      c[0] = c_in[0] + read;
+      c[1] = c_in[1] + n64;
+      c[2] = c_in[2];
+      c[3] = c_in[3] + (view_len == L ? read : 0);
+      c[4] = c_in[4];
+    }
   }
 }
 
@@ -235,6 +250,12 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   // counts' loads and reductions below instead of waiting for them.
   const RowInfo me = row_info(p, row);
   const int view_len_in = VIEW ? p.seq_lens[row] : 0;
+  // the row's own counter slot, loaded with the row's other loads (thread 0 updates it)
+  long long c_in[5] = {0, 0, 0, 0, 0};
+  if (VIEW && tid == 0 && p.view_counts != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) c_in[k] = p.view_counts[5LL * row + k];
+  }
   const float *srow = p.scores + (int64_t)row * p.scores_stride;
   float sv[kPer];
   uint32_t gone_bits = 0, pin_mask_bits = 0;  // released / explicitly pinned, from the masks
@@ -308,7 +329,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
       int32_t entry[kPer];
       load_run<kPer>(p, row, entry);
       __syncthreads();
-      view_row<kPer>(p, row, view_len_in, entry, s_keep, s_out, s_scan);
+      view_row<kPer>(p, row, view_len_in, c_in, entry, s_keep, s_out, s_scan);
     }
     return;
   }
@@ -482,7 +503,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     int32_t entry[kPer];
     load_run<kPer>(p, row, entry);
     __syncthreads();
-    view_row<kPer>(p, row, view_len_in, entry, s_keep, s_out, s_scan);
+    view_row<kPer>(p, row, view_len_in, c_in, entry, s_keep, s_out, s_scan);
   }
 }
 
@@ -507,7 +528,8 @@ extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride,
                                      int32_t rows, int32_t width, double fraction, int64_t budget, uint8_t *keep,
                                      int64_t keep_stride, int64_t *summary, const int32_t *table,
                                      int64_t table_stride, const int32_t *seq_lens, int32_t block_size,
-                                     int32_t *view_table, int64_t view_stride, int32_t *view_lens, void *stream) {
+                                     int32_t *view_table, int64_t view_stride, int32_t *view_lens,
+                                     int64_t *counts, void *stream) {
   if (scores == nullptr || blocks == nullptr || keep == nullptr || table == nullptr || seq_lens == nullptr ||
       view_table == nullptr || view_lens == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_uniform_view: null pointer");
@@ -539,6 +561,7 @@ extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride,
   p.view_table = view_table;
   p.view_stride = view_stride;
   p.view_lens = view_lens;
+  p.view_counts = (long long *)counts;
   hipStream_t s = (hipStream_t)stream;
   const int per = (width + rank::kThreads - 1) / rank::kThreads;
   if (per <= 4)

@@ -50,7 +50,7 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _p, _p, _p, _i64, _p, _i32, _p, _i64, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _p,
     ],
     "ekv_rank_uniform_view": [
-        _p, _i64, _p, _p, _p, _i32, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _p, _p,
+        _p, _i64, _p, _p, _p, _i32, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _p, _p, _p,
     ],
     "ekv_compact_view": [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _i64, _p, _p],
     "ekv_build_view": [

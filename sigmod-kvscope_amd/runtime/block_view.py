@@ -78,12 +78,15 @@ def uniform_view(
     recent_blocks: int = 0,
     measured: torch.Tensor | None = None,
     pin_from: torch.Tensor | None = None,
+    counts: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """The ``uniform`` ranking and the view built from it in one kernel: what
     ``observe.allocation.uniform_keep`` followed by ``compact_block_table`` on its keep returns
     (observe/allocation.py:39-91 with observe/controller.py:398-451, then runtime/block_view.py:36-56),
     as ``(keep, summary, view, view_lens)``.  Each row's workgroup compacts its table row from the keep
-    it has just decided.  Explicit pinned / released masks go through the two calls instead."""
+    it has just decided.  Explicit pinned / released masks go through the two calls instead.
+    ``counts`` (int64 [rows, 5]) accumulates DecodeView's read counters as ``DecodeView.build`` does for
+    live decoding rows outside the audit (runtime/block_view.py:313-329)."""
     _check_table(table, seq_lens)
     rows, width = int(scores.shape[0]), int(scores.shape[1])
     if scores.dtype != torch.float32 or scores.stride(1) != 1 or not scores.is_cuda:
@@ -96,6 +99,8 @@ def uniform_view(
         raise ValueError("measured must be a uint8 / bool [rows] mask")
     if pin_from is not None and (pin_from.dtype != torch.int32 or pin_from.shape != (rows,)):
         raise ValueError("pin_from must be int32 [rows]")
+    if counts is not None and (counts.dtype != torch.int64 or counts.shape != (rows, 5) or not counts.is_contiguous()):
+        raise ValueError("counts must be a contiguous int64 [rows, 5] tensor")
     keep = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
     summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
     view = torch.empty(rows, width, dtype=torch.int32, device=table.device)
@@ -105,7 +110,7 @@ def uniform_view(
         scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(measured), ekv_hip.ptr(pin_from),
         int(recent_blocks), rows, width, float(fraction), int(budget), keep.data_ptr(), keep.stride(0),
         summary.data_ptr(), table.data_ptr(), table.stride(0), seq_lens.data_ptr(), int(block_size),
-        view.data_ptr(), view.stride(0), lens.data_ptr(), ekv_hip.stream_handle(),
+        view.data_ptr(), view.stride(0), lens.data_ptr(), ekv_hip.ptr(counts), ekv_hip.stream_handle(),
     )
     return keep, summary, view, lens
 

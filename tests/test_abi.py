@@ -70,9 +70,9 @@ def test_shape_limits_are_refused_on_the_host():
     # ranking + view: the same width limit, and a block size below 1
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_rank_uniform_view", P, 20000, P, 0, 0, 0, 4, 20000, 0.5, -1, P, 20000, 0, P, 20000, P, 16,
-                     P, 20000, P, 0)
+                     P, 20000, P, 0, 0)
     with pytest.raises(ValueError, match="block size"):
-        ekv_hip.call("ekv_rank_uniform_view", P, 64, P, 0, 0, 0, 4, 64, 0.5, -1, P, 64, 0, P, 64, P, 0, P, 64, P, 0)
+        ekv_hip.call("ekv_rank_uniform_view", P, 64, P, 0, 0, 0, 4, 64, 0.5, -1, P, 64, 0, P, 64, P, 0, P, 64, P, 0, 0)
     # ranking: explicit masks without a workspace
     with pytest.raises(ValueError, match="workspace"):
         ekv_hip.call("ekv_rank_uniform", P, 8, P, 0, P, 8, 0, 0, 0, 0, 4, 8, 0.5, -1, P, 8, 0, 0)

@@ -10,6 +10,7 @@ import torch
 import workloads
 from observe.allocation import uniform_keep
 from oracle import block_view as obv
+import ekv_hip
 from runtime.block_view import compact_block_table, uniform_view
 
 pytestmark = pytest.mark.gpu
@@ -79,3 +80,30 @@ def test_budget_below_the_pins_keeps_every_block():
                                           torch.from_numpy(lens).cuda(), bs, budget=3, recent_blocks=8)
     assert summary[3] == 1 and keep.all()
     assert np.array_equal(view, table.cpu().numpy()) and np.array_equal(view_lens, lens)
+
+
+def test_counters_match_build_view():
+    # with counters, the view and the five read counters are ekv_build_view's for live decoding rows
+    # on the same keep, accumulated over calls
+    c = workloads.config4()
+    rows, width, bs = 256, 8192, c["block_size"]
+    scores = torch.from_numpy(np.ascontiguousarray(c["shares"][:rows])).cuda()
+    blocks = torch.from_numpy(np.ascontiguousarray(c["blocks"][:rows])).cuda()
+    table = torch.from_numpy(np.ascontiguousarray(c["table"][:rows])).cuda()
+    lens = torch.from_numpy(np.ascontiguousarray(c["seq_lens"][:rows])).cuda()
+    lens[7] = 0
+    counts = torch.zeros(rows, 5, dtype=torch.int64, device="cuda")
+    counts2 = torch.zeros_like(counts)
+    view2 = torch.empty_like(table)
+    lens2 = torch.empty_like(lens)
+    for fraction in (0.3, 0.7):
+        keep, summary, view, view_lens = uniform_view(scores, blocks, table, lens, bs, fraction=fraction,
+                                                      recent_blocks=4, counts=counts)
+        keep2, summary2 = uniform_keep(scores, blocks, fraction=fraction, recent_blocks=4)
+        ekv_hip.call("ekv_build_view", table.data_ptr(), width, lens.data_ptr(), keep2.data_ptr(), width, 0, 0, 0, 0,
+                     1, rows, width, bs, view2.data_ptr(), width, lens2.data_ptr(), counts2.data_ptr(),
+                     ekv_hip.stream_handle())
+        for name, g, w in (("keep", keep, keep2), ("summary", summary, summary2), ("view", view, view2),
+                           ("lens", view_lens, lens2), ("counts", counts, counts2)):
+            assert torch.equal(g, w), (fraction, name)
+    assert int(counts[:, 0].sum()) > 0
