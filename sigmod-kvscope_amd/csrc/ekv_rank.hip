@@ -218,11 +218,14 @@ __device__ __forceinline__ void view_row(const Params &p, int row, int L, const 
       // read, blocks in full, none audited, reads of a whole row, none expired
       const long long read = view_len > 0 ? ((long long)view_len + bs - 1) / bs : 0;
       long long *c = p.view_counts + 5LL * row;
-      c[0] = c_in[0] + read;
-      c[1] = c_in[1] + n64;
-      c[2] = c_in[2];
-      c[3] = c_in[3] + (view_len == L ? read : 0);
-      c[4] = c_in[4];
+      long long before[5];
+#pragma unroll
+      for (int k = 0; k < 5; ++k) before[k] = PER <= 16 ? c_in[k] : c[k];
+      c[0] = before[0] + read;
+      c[1] = before[1] + n64;
+      c[2] = before[2];
+      c[3] = before[3] + (view_len == L ? read : 0);
+      c[4] = before[4];
     }
   }
 }
@@ -250,9 +253,10 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   // counts' loads and reductions below instead of waiting for them.
   const RowInfo me = row_info(p, row);
   const int view_len_in = VIEW ? p.seq_lens[row] : 0;
-  // the row's own counter slot, loaded with the row's other loads (thread 0 updates it)
+  // the row's own counter slot, loaded with the row's other loads (thread 0 updates it); at 24 blocks
+  // per thread its registers would cost a workgroup per CU, so it is loaded at the end there
   long long c_in[5] = {0, 0, 0, 0, 0};
-  if (VIEW && tid == 0 && p.view_counts != nullptr) {
+  if (VIEW && kPer <= 16 && tid == 0 && p.view_counts != nullptr) {
 #pragma unroll
     for (int k = 0; k < 5; ++k) c_in[k] = p.view_counts[5LL * row + k];
   }

@@ -82,15 +82,26 @@ def test_budget_below_the_pins_keeps_every_block():
     assert np.array_equal(view, table.cpu().numpy()) and np.array_equal(view_lens, lens)
 
 
-def test_counters_match_build_view():
+@pytest.mark.parametrize("wide", [False, True])
+def test_counters_match_build_view(wide):
     # with counters, the view and the five read counters are ekv_build_view's for live decoding rows
-    # on the same keep, accumulated over calls
-    c = workloads.config4()
-    rows, width, bs = 256, 8192, c["block_size"]
-    scores = torch.from_numpy(np.ascontiguousarray(c["shares"][:rows])).cuda()
-    blocks = torch.from_numpy(np.ascontiguousarray(c["blocks"][:rows])).cuda()
-    table = torch.from_numpy(np.ascontiguousarray(c["table"][:rows])).cuda()
-    lens = torch.from_numpy(np.ascontiguousarray(c["seq_lens"][:rows])).cuda()
+    # on the same keep, accumulated over calls (16 and 24 blocks per thread)
+    if wide:
+        rng = np.random.default_rng(12)
+        rows, width, bs = 64, 12288, 16
+        n = rng.integers(1, width + 1, size=rows).astype(np.int32)
+        shares_np = rng.random((rows, width), dtype=np.float32)
+        table_np = rng.integers(0, 1 << 21, size=(rows, width)).astype(np.int32)
+        lens_np = (n.astype(np.int64) * bs - rng.integers(0, bs, size=rows)).clip(1).astype(np.int32)
+    else:
+        c = workloads.config4()
+        rows, width, bs = 256, 8192, c["block_size"]
+        n, shares_np, table_np, lens_np = (c["blocks"][:rows], c["shares"][:rows], c["table"][:rows],
+                                           c["seq_lens"][:rows])
+    scores = torch.from_numpy(np.ascontiguousarray(shares_np)).cuda()
+    blocks = torch.from_numpy(np.ascontiguousarray(n)).cuda()
+    table = torch.from_numpy(np.ascontiguousarray(table_np)).cuda()
+    lens = torch.from_numpy(np.ascontiguousarray(lens_np)).cuda()
     lens[7] = 0
     counts = torch.zeros(rows, 5, dtype=torch.int64, device="cuda")
     counts2 = torch.zeros_like(counts)
