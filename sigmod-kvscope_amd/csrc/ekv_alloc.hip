@@ -683,8 +683,14 @@ constexpr int kLevelThreads = 256;
 
 template <int CAP>
 __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminParams m) {
+  constexpr int kMine = (kLevels + kLevelThreads - 1) / kLevelThreads;  // levels per thread
   __shared__ double s_tot[CAP];  // the request's running totals
-  const int r = blockIdx.x;
+  // a workgroup takes requests blockIdx.x, + gridDim.x, ... and adds its counts once per level
+  int mine[kMine];
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) mine[i] = 0;
+  for (int r = blockIdx.x; r < m.p.rows; r += gridDim.x) {
+  __syncthreads();  // the previous request's searches are done before its totals are replaced
   const MaxminRow mr = m.mrow[r];
   const int open = mr.open;
   const double *pre = m.prefix + (int64_t)r * m.p.width;
@@ -692,7 +698,10 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
   __syncthreads();
   const double shift = 2.0 * (double)r;
   uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
-  for (int j = 1 + threadIdx.x; j < kLevels; j += kLevelThreads) {
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) {
+    const int j = i * kLevelThreads + threadIdx.x;
+    if (j < 1 || j >= kLevels) continue;
     const double level = (double)j / kLevels;
     const double need = level - mr.base;
     const double q = (need - 1e-12) + shift;
@@ -702,8 +711,13 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
       if (s_tot[c] + shift < q) a = c + 1; else b = c;
     }
     pos_row[j] = (uint16_t)a;
-    const int count = need <= 1e-12 ? 0 : min(a + 1, open);
-    if (count > 0) atomicAdd(&m.level_count[j], count);  // integer sums: the order does not matter
+    mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
+  }
+  }
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) {  // integer sums: the order does not matter
+    const int j = i * kLevelThreads + threadIdx.x;
+    if (j >= 1 && j < kLevels && mine[i] > 0) atomicAdd(&m.level_count[j], mine[i]);
   }
 }
 
@@ -1123,12 +1137,13 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  const dim3 level_grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 2));
   if (width <= 4096)
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<4096>, dim3(rows), dim3(alloc::kLevelThreads), 0, s, m);
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<4096>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
   else if (width <= 8192)
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<8192>, dim3(rows), dim3(alloc::kLevelThreads), 0, s, m);
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<8192>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
   else
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, dim3(rows), dim3(alloc::kLevelThreads), 0, s,
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, level_grid, dim3(alloc::kLevelThreads), 0, s,
                        m);
   if (rows <= alloc::kBisectThreads)
     hipLaunchKernelGGL(alloc::mm_bisect_kernel<1>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
