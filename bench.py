@@ -100,8 +100,9 @@ def other_audit_shapes() -> dict:
     pools = [workloads.device_pool(b3, torch.bfloat16, seed=b3.seed + i) for i in range(2)]
     q3 = torch.from_numpy(workloads.queries(b3, 8)).to(torch.bfloat16).cuda()
     plane = RecordingPlane(8, b3.rows, b3.width, b3.group_rows, b3.block_size)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    plane.attach([pool.data_ptr() for pool in pools])
     plane.select(np.ones(b3.rows, bool), np.arange(b3.rows))
+    plane.set(True)
     t3, l3 = torch.from_numpy(b3.table).cuda(), torch.from_numpy(b3.lens).cuda()
     us = graph_launch_us(lambda s: [plane.launch(layer, t3, l3, q3[layer], pools[layer % 2][:, 0],
                                                  b3.head_dim ** -0.5, stream=s) for layer in range(8)], 8, 10)
@@ -116,8 +117,9 @@ def other_audit_shapes() -> dict:
     pools = [workloads.device_pool(b5, fp8, seed=b5.seed + i) for i in range(2)]
     q5 = torch.from_numpy(workloads.queries(b5, LAYERS)).to(torch.bfloat16).cuda()
     plane = RecordingPlane(LAYERS, b5.rows, b5.width, b5.group_rows, b5.block_size, timer=True)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    plane.attach([pools[layer % 2].data_ptr() for layer in range(LAYERS)])
     plane.select(np.ones(b5.rows, bool), np.arange(b5.rows))
+    plane.set(True)
     t5, l5 = torch.from_numpy(b5.table).cuda(), torch.from_numpy(b5.lens).cuda()
     k_scale = b5.extra["k_scale"]
     us = graph_launch_us(lambda s: [plane.launch(layer, t5, l5, q5[layer], pools[layer % 2][:, 0],
@@ -155,8 +157,9 @@ class Step:
         self.lens = torch.from_numpy(batch.lens).to(dev)
         self.blocks = torch.from_numpy(batch.blocks.astype(np.int32)).to(dev)
         self.plane = RecordingPlane(LAYERS, batch.rows, batch.width, batch.group_rows, batch.block_size)
-        self.plane._copy_to_device(self.plane._flag_dev, np.array([1], dtype=np.uint32))
+        self.plane.attach([self.pools[layer % POOLS].data_ptr() for layer in range(LAYERS)])
         self.plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
+        self.plane.set(True)
         R, W = batch.rows, batch.width
         self.shares = torch.empty(R, W, dtype=torch.float32, device=dev)
         need = int(self.ekv.load().ekv_tile_shares_workspace(R, W, LAYERS))
@@ -480,8 +483,9 @@ def main() -> None:
     from runtime.audit_kernel import RecordingPlane
 
     all_plane = RecordingPlane(1, batch.rows, batch.width, batch.group_rows, batch.block_size, kv_heads=batch.kv_heads)
-    all_plane._copy_to_device(all_plane._flag_dev, np.array([1], dtype=np.uint32))
+    all_plane.attach([step.pools[0].data_ptr()])
     all_plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
+    all_plane.set(True)
     all_ms = float(np.median(time_events(
         lambda: all_plane.launch(0, step.table, step.lens, step.q[0], step.keys[0], step.scale,
                                  chunk_tiles=args.chunk_tiles), 10, stream)))

@@ -88,6 +88,43 @@ int ekv_audit_tile_lse(const void *q, int q_dtype, int64_t q_stride_token, int64
                        int32_t chunk_tiles, void *stream);
 
 /*
+ * The step plan of the audit: the work list every audit launch of one decode step shares.
+ * Replaces the per-launch part of RecordingPlane.launch that recomputes the tiles of the selected
+ * rows (runtime/audit_kernel.py:239-241 with the grid's early exits at :65-69): the launches of a
+ * step read the same view table, lengths, selected rows and query tokens (runtime/block_view.py
+ * :283-295 builds them once per step), so the list of (row, tile, block ids, query token) is built
+ * once here, by two kernels on `stream`, and each ekv_audit_tile_lse_planned launch reads its
+ * share of it.  With the flag off the plan is empty.
+ * ekv_audit_plan_bytes(plan_rows, plan_width): device bytes of a plan for any batch of at most
+ * plan_rows x plan_width on the current device (0 if too large); the buffer must be 256-byte
+ * aligned and must not be in use by a running launch when it is rebuilt.
+ */
+size_t ekv_audit_plan_bytes(int32_t plan_rows, int32_t plan_width);
+int ekv_audit_plan(const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow,
+                   const uint8_t *select, const uint32_t *flag, int32_t rows, int32_t width,
+                   int32_t block_size, int32_t tile_blocks, void *plan, size_t plan_bytes,
+                   int32_t plan_rows, int32_t plan_width, void *stream);
+
+/*
+ * ekv_audit_tile_lse reading its work list from a plan built by ekv_audit_plan from the same
+ * table, lengths, selection and query tokens: the same records and cycles, without the per-launch
+ * scan of the rows.  Replaces tile_lse_kernel + RecordingPlane.launch, runtime/audit_kernel.py
+ * :34-109 and :224-265, as ekv_audit_tile_lse does.  Shapes without an MFMA form (fp32 keys,
+ * 8-token blocks) run the self-contained kernel.
+ */
+int ekv_audit_tile_lse_planned(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                               const void *keys, int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos,
+                               int64_t k_stride_head, float k_scale, const int32_t *table,
+                               int64_t table_stride, const int32_t *lens, const int32_t *qrow,
+                               const uint8_t *select, const uint32_t *flag, float *lse,
+                               int64_t lse_plane_stride, int64_t lse_layer_stride, int64_t lse_row_stride,
+                               int32_t cells, uint64_t *cycles, int32_t cycles_rows, float scale,
+                               int32_t layer, int32_t group_first, int32_t groups, int32_t group_rows,
+                               int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
+                               int32_t head_dim, const void *plan, size_t plan_bytes, int32_t plan_rows,
+                               int32_t plan_width, void *stream);
+
+/*
  * Exact per-block attention shares of the chosen rows, from the statistic planes.
  * Replaces read_tile_rows + normalize_tile_lse (observe/tile_shares.py:129-173 and :58-103),
  * computing on the device what the reference copies to the host and normalises with NumPy.
@@ -159,6 +196,24 @@ int ekv_rank_uniform(const float *scores, int64_t scores_stride, const int32_t *
                      int64_t released_stride, int32_t rows, int32_t width, double fraction,
                      int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
                      void *stream);
+
+/*
+ * ekv_rank_uniform_ws for float64 scores, ranking the float64 shares themselves.  Replaces
+ * allocate(..., "uniform") on float64 Request.scores (observe/allocation.py:39-91, with
+ * Request.shares at :46-52) and the controller's pins and budget (observe/controller.py:398-451),
+ * as ekv_rank_uniform_ws does.  Each request's share of an open block is max(s, 0) / total with
+ * total NumPy's sum of the clamped scores of its existing blocks (1 / n for a total <= 0), so two
+ * scores that divide to one share tie and go to the lower block index as the reference's stable
+ * argsort orders them; NaN shares rank last.
+ * workspace: ekv_rank_uniform64_workspace(rows) bytes of device memory the call may overwrite.
+ */
+size_t ekv_rank_uniform64_workspace(int32_t rows);
+int ekv_rank_uniform64(const double *scores, int64_t scores_stride, const int32_t *blocks,
+                       const uint8_t *measured, const uint8_t *pinned, int64_t pinned_stride,
+                       const int32_t *pin_from, int32_t recent_blocks, const uint8_t *released,
+                       int64_t released_stride, int32_t rows, int32_t width, double fraction,
+                       int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                       void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * ekv_rank_uniform followed by ekv_compact_view on the keep it writes, in one kernel: the view

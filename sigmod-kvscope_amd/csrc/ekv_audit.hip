@@ -22,6 +22,7 @@
 //    vector 64-bit atomic (the pass's per-row timer, mlir_pass/lib/eKVTimer.cpp:1348-1387).
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "ekv_common.hpp"
@@ -777,6 +778,393 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The step plan.  Every audit launch of a decode step reads the same view buffers (block
+// table, lengths, selected rows, query tokens); only the layer, its queries and its keys
+// change.  So the work list the self-contained kernel rebuilds in every launch -- the tiles of
+// each selected row, their scan, each tile's row and block ids -- is built once per step, by two
+// small kernels, into a plan buffer that holds, for each workgroup of the audit grid, the count
+// of its tiles and their descriptors, contiguous.  A planned launch then starts with one load of
+// the wave's first descriptor before its first key requests, and reads its later descriptors
+// one tile ahead, as the self-contained kernel reads them from LDS.
+//
+// Plan buffer (PlanLayout): wg[kMaxGrid] int2 = (tiles, first row), first[kMaxGrid + 1] = the
+// split points of the flat tile list over the grid, row_off[rows + 1] = each row's first tile,
+// desc[grid][cap] = the tiles of each workgroup in flat order.
+// ---------------------------------------------------------------------------------------
+constexpr int kMaxGrid = 1024;
+constexpr int kSplitThreads = 1024;
+constexpr int kFillThreads = 256;
+
+struct TileDesc {
+  int32_t row, k, valid, qtok, id0, id1, pad0, pad1;  // valid: tokens of the tile the row reaches
+};
+static_assert(sizeof(TileDesc) == 32, "a descriptor is two 16-byte loads");
+
+struct PlanLayout {
+  int64_t wg, first, row_off, desc, bytes;
+  int32_t cap;  // descriptors per workgroup
+};
+
+inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+inline int64_t plan_max_tiles(int rows, int width) {
+  return (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks);
+}
+
+// The layout of a plan for batches of at most rows x width on a grid of `grid` workgroups.  The
+// split gives workgroup b the tiles [T b / grid, T (b + 1) / grid) of the T live tiles, at most
+// ceil(T / grid) of them.
+inline PlanLayout plan_layout(int rows, int width, int grid) {
+  PlanLayout L;
+  const int64_t max_tiles = plan_max_tiles(rows, width);
+  L.cap = (int32_t)std::max<int64_t>(1, (max_tiles + grid - 1) / grid);
+  L.wg = 0;
+  L.first = align_up(L.wg + (int64_t)sizeof(int2) * kMaxGrid, 256);
+  L.row_off = align_up(L.first + 4 * (int64_t)(kMaxGrid + 1), 256);
+  L.desc = align_up(L.row_off + 4 * ((int64_t)rows + 1), 256);
+  L.bytes = align_up(L.desc + (int64_t)grid * L.cap * (int64_t)sizeof(TileDesc), 256);
+  return L;
+}
+
+struct PlanArgs {
+  const int32_t *table;
+  int64_t table_stride;
+  const int32_t *lens;
+  const int32_t *qrow;
+  const uint8_t *select;
+  const uint32_t *flag;
+  int32_t rows, width, block_size, grid, cap;
+  int2 *wg;
+  int32_t *first;
+  int32_t *row_off;
+  TileDesc *desc;
+};
+
+__device__ __forceinline__ int plan_row_tiles(const PlanArgs &a, int r) {
+  const int tile_tokens = kTileBlocks * a.block_size;
+  if (a.select[r] == 0) return 0;
+  const int len = min(max(a.lens[r], 0), a.width * a.block_size);
+  return (len + tile_tokens - 1) / tile_tokens;  // runtime/audit_kernel.py:65-69
+}
+
+// One workgroup: the live tiles of every row (none with the flag off), their exclusive scan,
+// and the grid's split points and per-workgroup counts.
+__global__ __launch_bounds__(kSplitThreads) void plan_split_kernel(const PlanArgs a) {
+  __shared__ int s_scan[kSplitThreads / kWave];
+  const bool on = *(volatile const uint32_t *)a.flag != 0u;
+  const int per = (a.rows + kSplitThreads - 1) / kSplitThreads;
+  const int r0 = min((int)threadIdx.x * per, a.rows);
+  const int r1 = min(r0 + per, a.rows);
+  int local = 0;
+  if (on)
+    for (int r = r0; r < r1; ++r) local += plan_row_tiles(a, r);
+  int total = 0;
+  int base = block_exclusive_scan<kSplitThreads>(local, s_scan, total);
+  for (int r = r0; r < r1; ++r) {
+    a.row_off[r] = base;
+    if (on) base += plan_row_tiles(a, r);
+  }
+  if (threadIdx.x == 0) a.row_off[a.rows] = total;
+  for (int b = threadIdx.x; b <= kMaxGrid; b += kSplitThreads) {
+    const int f = b <= a.grid ? (int)((int64_t)total * b / a.grid) : total;
+    a.first[b] = f;
+    if (b < kMaxGrid) {
+      const int next = b + 1 <= a.grid ? (int)((int64_t)total * (b + 1) / a.grid) : total;
+      a.wg[b] = make_int2(next - f, 0);
+    }
+  }
+}
+
+// One workgroup per row: each of the row's tiles goes to the workgroup whose split holds it, at
+// its place there; the workgroup's first tile also names its first row.
+__global__ __launch_bounds__(kFillThreads) void plan_fill_kernel(const PlanArgs a) {
+  __shared__ int s_first[kMaxGrid + 1];
+  for (int b = threadIdx.x; b <= a.grid; b += kFillThreads) s_first[b] = a.first[b];
+  __syncthreads();
+  const int tile_tokens = kTileBlocks * a.block_size;
+  for (int row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const int off = a.row_off[row];
+    const int tiles = a.row_off[row + 1] - off;
+    if (tiles <= 0) continue;
+    const int len = min(max(a.lens[row], 0), a.width * a.block_size);
+    const int nb = (len + a.block_size - 1) / a.block_size;
+    const int qtok = a.qrow[row];
+    const int32_t *trow = a.table + (int64_t)row * a.table_stride;
+    for (int k = threadIdx.x; k < tiles; k += kFillThreads) {
+      const int t = off + k;
+      int lo = 0, hi = a.grid;  // the workgroup b with first[b] <= t < first[b + 1]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_first[mid] <= t) lo = mid; else hi = mid;
+      }
+      TileDesc d;
+      d.row = row;
+      d.k = k;
+      d.valid = min(len - k * tile_tokens, tile_tokens);
+      d.qtok = qtok;
+      d.id0 = trow[kTileBlocks * k];
+      d.id1 = kTileBlocks * k + 1 < nb ? trow[kTileBlocks * k + 1] : d.id0;  // past the row: stands in
+      d.pad0 = d.pad1 = 0;
+      a.desc[(int64_t)lo * a.cap + (t - s_first[lo])] = d;
+      if (t == s_first[lo]) a.wg[lo].y = row;
+    }
+  }
+}
+
+struct PlanView {
+  const int2 *wg;
+  const TileDesc *desc;
+  int32_t cap;
+};
+
+// A descriptor into VGPRs with a vector load (the offset register keeps it one: a scalar load
+// would be waited for with the wave's LDS traffic, both being counted by lgkmcnt).
+__device__ __forceinline__ void load_desc(const TileDesc *d, u32x4 &lo, u32x4 &hi) {
+  uint32_t o = 0;
+  asm volatile("" : "+v"(o));
+  const char *src = reinterpret_cast<const char *>(d) + o;
+  lo = *reinterpret_cast<const u32x4 *>(src);
+  hi = *reinterpret_cast<const u32x4 *>(src + 16);
+}
+
+// The planned form of tile_lse_cu_kernel: the same chunks, dots, records and timer; the tiles
+// of workgroup b are its plan's descriptors, wave w starting at item w and the waves then taking
+// items from an LDS counter, one ahead.  An item is (tile, audited head), tile-major.
+template <int MODE, int HEAD_DIM, int MT>
+__global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Params p, const PlanView plan) {
+  using S = MfmaShape<MODE, HEAD_DIM>;
+  using C = CuShape<MODE, HEAD_DIM, MT>;
+  constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
+  constexpr int NW = C::kWaves;
+
+  __shared__ int s_next;
+  __shared__ u32x4 s_tr[NW][C::kStash];
+  __shared__ unsigned long long s_cycles[kCycleSlots];
+
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int groups = p.groups;
+  const TileDesc *dl = plan.desc + (int64_t)blockIdx.x * plan.cap;
+  // the flag, the workgroup's count and first row, and the wave's first descriptor: one latency
+  // (a relaxed load: a volatile one is completed before the next load is issued)
+  uint32_t flag = __hip_atomic_load(p.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int2 wg = plan.wg[blockIdx.x];
+  // wave w starts at item w; the rest come from the LDS counter
+  u32x4 d_lo, d_hi;
+  load_desc(dl + min(groups == 1 ? wave : wave / groups, plan.cap - 1), d_lo, d_hi);
+  // all four are waited for here, together: otherwise the compiler tests the flag before it
+  // issues the other loads, a second memory latency before the first key request
+  asm volatile("" : "+v"(flag), "+v"(wg.x), "+v"(wg.y) : "v"(d_lo), "v"(d_hi));
+  // the parameters of the first key and query requests, read with the others (a scalar-cache miss
+  // after the barrier would be one more latency)
+  const char *keys_base = p.keys, *q_base = p.q;
+  int64_t k_block = p.k_stride_block, k_pos = p.k_stride_pos, k_head = p.k_stride_head;
+  int64_t q_tok = p.q_stride_token, q_head = p.q_stride_head;
+  asm volatile("" : "+s"(keys_base), "+s"(q_base), "+s"(k_block), "+s"(k_pos), "+s"(k_head), "+s"(q_tok),
+               "+s"(q_head));
+  if (flag == 0u) return;  // runtime/audit_kernel.py:64
+  if (threadIdx.x == 0) s_next = NW;
+  if (p.cycles != nullptr)
+    for (int k = threadIdx.x; k < kCycleSlots; k += kCuThreads) s_cycles[k] = 0ull;
+  const int items = __builtin_amdgcn_readfirstlane(min(wg.x, plan.cap)) * groups;
+  const int row0 = __builtin_amdgcn_readfirstlane(wg.y);
+  __syncthreads();  // s_next and the timer slots are set before any take
+
+  const int n = lane & 15;  // A: token of the M-tile; B / C: query row
+  const int c = lane >> 4;  // dim piece within a k-step; C: token quad
+  const int nsub = p.nsub;  // chunks per tile
+  const int bs = p.block_size;
+  const int G = p.group_rows;
+  u32x4 *tr = s_tr[wave];
+  const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
+  const int piece = lane % S::kPieces;
+  uint32_t voff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * k_pos + piece * 16);
+  const float scale2 = p.scale * kLog2e;
+
+  struct Tile {
+    int row, h, k, valid, id0, id1, qtok;
+  };
+  auto describe = [&](const u32x4 &lo, const u32x4 &hi, int item) -> Tile {
+    Tile t;
+    t.row = __builtin_amdgcn_readfirstlane((int)lo[0]);
+    t.k = __builtin_amdgcn_readfirstlane((int)lo[1]);
+    t.valid = __builtin_amdgcn_readfirstlane((int)lo[2]);
+    t.qtok = __builtin_amdgcn_readfirstlane((int)lo[3]);
+    t.id0 = __builtin_amdgcn_readfirstlane((int)hi[0]);
+    t.id1 = __builtin_amdgcn_readfirstlane((int)hi[1]);
+    t.h = groups == 1 ? 0 : item % groups;
+    return t;
+  };
+  auto take = [&]() -> int {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  auto load_chunk = [&](u32x4 (&D)[MT * NLD], const Tile &T, int sub) {
+    const int64_t head_off = (int64_t)(p.group_first + T.h) * k_head;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int tpos = sub * CH + 16 * mt;
+      const int id = tpos < bs ? T.id0 : T.id1;
+      const char *src = keys_base + (int64_t)id * k_block + head_off + (int64_t)(tpos % bs) * k_pos;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        uint32_t o = voff[j];
+        asm volatile("" : "+v"(o));
+        D[mt * NLD + j] = __builtin_nontemporal_load((const u32x4 *)(src + o));
+      }
+    }
+  };
+  auto load_query = [&](u32x4 (&Q)[KS], const Tile &T) {
+    const char *qrow = q_base + (int64_t)T.qtok * q_tok + (int64_t)((p.group_first + T.h) * G + n) * q_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
+      Q[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
+    }
+  };
+  auto stash_chunk = [&](const u32x4 (&L)[MT * NLD]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) tr[mt * 16 * S::kPieces + tr_slot<S>(j * S::kTPI + row_in, piece)] = L[mt * NLD + j];
+  };
+  auto mma_stashed = [&](const u32x4 (&Q)[KS], f32x4_t (&acc)[MT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      u32x4 D[NLD];
+#pragma unroll
+      for (int s = 0; s < NLD; ++s) D[s] = tr[mt * 16 * S::kPieces + tr_slot<S>(n, 4 * s + c)];
+      acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (S::kFp8) {
+#pragma unroll
+        for (int s = 0; s < NLD; ++s) {
+          u32x4 lo4, hi4;
+          widen_fp8(D[s], lo4, hi4);
+          acc[mt] = mfma_step<kModeBF16>(lo4, Q[2 * s], acc[mt]);
+          acc[mt] = mfma_step<kModeBF16>(hi4, Q[2 * s + 1], acc[mt]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc[mt] = mfma_step<MODE>(D[s], Q[s], acc[mt]);
+      }
+    }
+  };
+
+  const bool timed = p.cycles != nullptr;
+  // the timer: a run of one row's and head's tiles is timed once, where it ends
+  auto time_tile = [&](const Tile &T, uint64_t &mark) {
+    const uint64_t now = __builtin_amdgcn_s_memtime();
+    if (T.h == 0 && T.row < p.cycles_rows && lane == 0) {
+      const int slot = T.row - row0;
+      if (slot >= 0 && slot < kCycleSlots) atomicAdd(&s_cycles[slot], (unsigned long long)(now - mark));
+      else atomicAdd((unsigned long long *)(p.cycles + T.row), (unsigned long long)(now - mark));
+    }
+    mark = now;
+  };
+  // the chunk's tile max and sum, folded into the tile's running (m, l); at the tile's last chunk
+  // its record goes into each of its blocks the row reaches (runtime/audit_kernel.py:97-109)
+  auto reduce_chunk = [&](const f32x4_t (&acc)[MT], const Tile &T, int sub, float &m_run, float &l_run) {
+    const int tok0 = sub * CH;  // within the tile
+    float sc[4 * MT];
+    if (tok0 + CH <= T.valid) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[4 * mt + e] = acc[mt][e] * scale2;
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int tok = tok0 + 16 * mt + 4 * c + e;
+          sc[4 * mt + e] = tok < T.valid ? acc[mt][e] * scale2 : -INFINITY;
+        }
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int e = 1; e < 4 * MT; ++e) mx = fmaxf(mx, sc[e]);
+    mx = rows_max(mx);
+    float sum = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int e = 0; e < 4 * MT; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
+    }
+    sum = rows_sum(sum);
+    const float M = fmaxf(m_run, mx);
+    if (M != -INFINITY) {
+      const float a = m_run == -INFINITY ? 0.0f : l_run * __builtin_amdgcn_exp2f(m_run - M);
+      const float b = mx == -INFINITY ? 0.0f : sum * __builtin_amdgcn_exp2f(mx - M);
+      l_run = a + b;
+      m_run = M;
+    }
+    if (sub == nsub - 1) {
+      const int blk = kTileBlocks * T.k + c;
+      if (c < kTileBlocks && n < G && c * bs < T.valid) {
+        float *cell = p.lse + (int64_t)T.row * p.row_stride + T.h * G + (int64_t)blk * p.cells + n;
+        cell[0] = m_run * kLn2;
+        cell[p.plane_stride] = l_run;
+      }
+      m_run = -INFINITY;
+      l_run = 0.0f;
+    }
+  };
+
+  if (wave < items) {
+    Tile T = describe(d_lo, d_hi, wave);
+    int ahead = take();  // the wave's next item, its descriptor read a tile early
+    if (ahead < items) load_desc(dl + ahead / groups, d_lo, d_hi);
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4_t acc[MT];
+    // one chunk in flight per wave: it goes to LDS when it arrives and the next is requested at once
+    u32x4 A[MT * NLD], qb[KS], qn[KS];
+    load_query(qb, T);
+    load_chunk(A, T, 0);
+    int sub = 0;
+    uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
+    while (true) {
+      Tile N = T;
+      int nsub_next = sub + 1;
+      bool more = true, new_query = false;
+      if (nsub_next == nsub) {
+        more = ahead < items;
+        if (more) {
+          N = describe(d_lo, d_hi, ahead);
+          nsub_next = 0;
+          ahead = take();
+          if (ahead < items) load_desc(dl + ahead / groups, d_lo, d_hi);
+          new_query = N.row != T.row || N.h != T.h;
+        }
+      }
+      stash_chunk(A);  // waits for the chunk
+      if (more) {
+        load_chunk(A, N, nsub_next);
+        if (new_query) load_query(qn, N);
+      }
+      mma_stashed(qb, acc);
+      reduce_chunk(acc, T, sub, m_run, l_run);
+      if (timed && sub == nsub - 1 && (!more || N.row != T.row || N.h != T.h)) time_tile(T, mark);
+      if (!more) break;
+      if (new_query) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qb[s] = qn[s];
+      }
+      T = N;
+      sub = nsub_next;
+    }
+  }
+  if (p.cycles != nullptr) {
+    __syncthreads();
+    if (threadIdx.x < kCycleSlots) {
+      const unsigned long long cyc = s_cycles[threadIdx.x];
+      if (cyc != 0ull) atomicAdd((unsigned long long *)(p.cycles + row0 + threadIdx.x), cyc);
+    }
+  }
+}
+
 using KernelFn = void (*)(const Params);
 
 template <int MODE, int HD, int NL, int GP>
@@ -894,15 +1282,57 @@ int dtype_bytes(int dtype) {
 using namespace ekv;
 using namespace ekv::audit;
 
-extern "C" int ekv_audit_tile_lse(
-    const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head, const void *keys,
-    int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head, float k_scale,
-    const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow,
-    const uint8_t *select, const uint32_t *flag, float *lse, int64_t lse_plane_stride,
-    int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells, uint64_t *cycles,
-    int32_t cycles_rows, float scale, int32_t layer, int32_t group_first, int32_t groups,
-    int32_t group_rows, int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
-    int32_t head_dim, int32_t chunk_tiles, void *stream) {
+namespace ekv {
+namespace audit {
+
+using PlannedFn = void (*)(const Params, const PlanView);
+
+template <int MODE, int HD>
+PlannedFn pick_planned_mt(bool wide) {
+  constexpr int kRowBytes = MfmaShape<MODE, HD>::kRowBytes;
+  if constexpr (kRowBytes <= 128) {
+    if (wide) return tile_lse_planned_kernel<MODE, HD, chunk_mtiles(kRowBytes, true)>;
+  }
+  return tile_lse_planned_kernel<MODE, HD, chunk_mtiles(kRowBytes, false)>;
+}
+
+template <int MODE>
+PlannedFn pick_planned_hd(int hd, bool wide) {
+  switch (hd) {
+    case 64: return pick_planned_mt<MODE, 64>(wide);
+    case 128: return pick_planned_mt<MODE, 128>(wide);
+    case 256: return pick_planned_mt<MODE, 256>(wide);
+  }
+  return nullptr;
+}
+
+PlannedFn pick_planned(int mode, int hd, bool wide) {
+  switch (mode) {
+    case kModeF16: return pick_planned_hd<kModeF16>(hd, wide);
+    case kModeBF16: return pick_planned_hd<kModeBF16>(hd, wide);
+    case kModeFp8Bf16: return pick_planned_hd<kModeFp8Bf16>(hd, wide);
+  }
+  return nullptr;
+}
+
+// The kernel choice and launch shape of one audit call.
+struct Launch {
+  KernelFn fn = nullptr;
+  PlannedFn planned = nullptr;  // the planned form, for the MFMA shapes
+  int threads = kThreads;
+  size_t lds = 0;
+  int64_t blocks = 0;
+};
+
+// Checks the arguments of an audit call and fills its kernel parameters and launch shape.
+int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head, const void *keys,
+                int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head, float k_scale,
+                const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow,
+                const uint8_t *select, const uint32_t *flag, float *lse, int64_t lse_plane_stride,
+                int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells, uint64_t *cycles,
+                int32_t cycles_rows, float scale, int32_t layer, int32_t group_first, int32_t groups,
+                int32_t group_rows, int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
+                int32_t head_dim, int32_t chunk_tiles, Params &p, Launch &L) {
   if (q == nullptr || keys == nullptr || table == nullptr || lens == nullptr || qrow == nullptr ||
       select == nullptr || flag == nullptr || lse == nullptr)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: null pointer argument");
@@ -919,7 +1349,6 @@ extern "C" int ekv_audit_tile_lse(
                 groups, group_first, groups * group_rows, cells);
   if (((kTileBlocks * block_size) & (kTileBlocks * block_size - 1)) != 0)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: a tile must hold a power of two of tokens");
-  if (rows == 0) return EKV_OK;
 
   int mode;
   if (kv_dtype == EKV_F32 && q_dtype == EKV_F32) mode = kModeF32;
@@ -941,14 +1370,13 @@ extern "C" int ekv_audit_tile_lse(
   // keys, block size 8) the dot products run on the VALU.
   const bool use_mfma = mode != kModeF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
                         tile_tokens % 32 == 0;
-  KernelFn fn = nullptr;
   int nsub = 1;
-  int threads = kThreads;  // per workgroup
   if (use_mfma) {
     const bool wide = tile_tokens % 64 == 0;
-    fn = pick_mfma(mode, head_dim, wide);
+    L.fn = pick_mfma(mode, head_dim, wide);
+    L.planned = pick_planned(mode, head_dim, wide);
     nsub = tile_tokens / (16 * chunk_mtiles(row_bytes, wide));  // chunks of up to 8 KB of keys
-    threads = kCuThreads;
+    L.threads = kCuThreads;
   } else {
     // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
     // instruction must sit inside one block, and a chunk inside one tile.
@@ -957,10 +1385,11 @@ extern "C" int ekv_audit_tile_lse(
                   block_size, tpi);
     const int nl = tile_tokens / tpi >= 8 ? 8 : tile_tokens / tpi;
     const int gp = group_rows <= 4 ? 4 : (group_rows <= 8 ? 8 : 16);
-    fn = pick(mode, head_dim, nl, gp);
+    L.fn = pick(mode, head_dim, nl, gp);
     nsub = tile_tokens / (nl * tpi);
+    L.threads = kThreads;
   }
-  if (fn == nullptr)
+  if (L.fn == nullptr)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, block size %d",
                 kv_dtype, head_dim, block_size);
   // 16-byte loads of key rows and query slices
@@ -974,7 +1403,6 @@ extern "C" int ekv_audit_tile_lse(
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: key position stride %lld (positive, 16 positions in 2 GiB)",
                 (long long)k_stride_pos);
 
-  Params p;
   p.q = (const char *)q;
   p.q_stride_token = q_stride_token * qbytes;
   p.q_stride_head = q_stride_head * qbytes;
@@ -1009,18 +1437,139 @@ extern "C" int ekv_audit_tile_lse(
   // One resident wave per slot the GPU has: the work list is split evenly over the grid, so a
   // second round of workgroups would only add a tail.  chunk_tiles bounds the grid for small
   // batches (at least that many tiles per wave).
-  const size_t lds = (size_t)(use_mfma ? 2 * rows + 1 : rows + 1) * sizeof(int);
+  L.lds = (size_t)(use_mfma ? 2 * rows + 1 : rows + 1) * sizeof(int);
   const int64_t max_tiles = (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks) * groups;
   const int64_t min_per_wave = p.chunk_tiles;
-  const int waves = threads / kWave;
+  const int waves = L.threads / kWave;
   int64_t blocks = (max_tiles + min_per_wave * waves - 1) / (min_per_wave * waves);
-  const int resident = resident_blocks(fn, lds, threads);
+  const int resident = resident_blocks(L.fn, L.lds, L.threads);
   if (resident < 1)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: a workgroup of %d threads with %zu bytes of row data does "
-                "not fit a compute unit (rows %d)", threads, lds, rows);
+                "not fit a compute unit (rows %d)", L.threads, L.lds, rows);
   const int64_t cap = (int64_t)cu_count() * resident;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(threads), lds, (hipStream_t)stream, p);
+  L.blocks = blocks;
+  return EKV_OK;
+}
+
+// The grid of a planned launch and of the plan it reads: one workgroup per compute unit.
+int plan_grid() { return std::min(cu_count(), kMaxGrid); }
+
+int check_plan(const void *plan, size_t plan_bytes, int32_t plan_rows, int32_t plan_width, int32_t rows,
+               int32_t width, const char *who) {
+  if (plan == nullptr) return fail(EKV_EINVAL, "%s: null plan", who);
+  if (plan_rows <= 0 || plan_width <= 0 || rows > plan_rows || width > plan_width)
+    return fail(EKV_EINVAL, "%s: a batch of %d x %d does not fit a plan for %d x %d", who, rows, width, plan_rows,
+                plan_width);
+  if (plan_max_tiles(plan_rows, plan_width) > INT32_MAX / 2)
+    return fail(EKV_EINVAL, "%s: a plan for %d x %d holds more tiles than 32-bit indices count", who, plan_rows,
+                plan_width);
+  const PlanLayout Lp = plan_layout(plan_rows, plan_width, plan_grid());
+  if ((int64_t)plan_bytes < Lp.bytes)
+    return fail(EKV_EINVAL, "%s: the plan has %zu bytes, %lld are needed", who, plan_bytes, (long long)Lp.bytes);
+  if (((uintptr_t)plan & 255) != 0) return fail(EKV_EINVAL, "%s: the plan must be 256-byte aligned", who);
+  return EKV_OK;
+}
+
+}  // namespace audit
+}  // namespace ekv
+
+extern "C" int ekv_audit_tile_lse(
+    const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head, const void *keys,
+    int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head, float k_scale,
+    const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow,
+    const uint8_t *select, const uint32_t *flag, float *lse, int64_t lse_plane_stride,
+    int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells, uint64_t *cycles,
+    int32_t cycles_rows, float scale, int32_t layer, int32_t group_first, int32_t groups,
+    int32_t group_rows, int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
+    int32_t head_dim, int32_t chunk_tiles, void *stream) {
+  Params p;
+  Launch L;
+  const int rc = audit_setup(q, q_dtype, q_stride_token, q_stride_head, keys, kv_dtype, k_stride_block, k_stride_pos,
+                             k_stride_head, k_scale, table, table_stride, lens, qrow, select, flag, lse,
+                             lse_plane_stride, lse_layer_stride, lse_row_stride, cells, cycles, cycles_rows, scale,
+                             layer, group_first, groups, group_rows, rows, width, block_size, tile_blocks, head_dim,
+                             chunk_tiles, p, L);
+  if (rc != EKV_OK || rows == 0) return rc;
+  hipLaunchKernelGGL(L.fn, dim3((unsigned)L.blocks), dim3(L.threads), L.lds, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_audit_tile_lse launch");
+}
+
+extern "C" size_t ekv_audit_plan_bytes(int32_t rows, int32_t width) {
+  if (rows <= 0 || width <= 0 || plan_max_tiles(rows, width) > INT32_MAX / 2) return 0;
+  return (size_t)plan_layout(rows, width, plan_grid()).bytes;
+}
+
+extern "C" int ekv_audit_plan(const int32_t *table, int64_t table_stride, const int32_t *lens,
+                              const int32_t *qrow, const uint8_t *select, const uint32_t *flag, int32_t rows,
+                              int32_t width, int32_t block_size, int32_t tile_blocks, void *plan,
+                              size_t plan_bytes, int32_t plan_rows, int32_t plan_width, void *stream) {
+  if (table == nullptr || lens == nullptr || qrow == nullptr || select == nullptr || flag == nullptr)
+    return fail(EKV_EINVAL, "ekv_audit_plan: null pointer argument");
+  if (tile_blocks != kTileBlocks)
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_plan: tiles of %d blocks; the kernel records tiles of %d",
+                tile_blocks, kTileBlocks);
+  if (rows < 0 || width <= 0 || block_size <= 0 || (int64_t)width * block_size > INT32_MAX)
+    return fail(EKV_EINVAL, "ekv_audit_plan: rows %d, width %d, block %d out of range", rows, width, block_size);
+  const int rc = check_plan(plan, plan_bytes, plan_rows, plan_width, rows, width, "ekv_audit_plan");
+  if (rc != EKV_OK) return rc;
+  const int grid = plan_grid();
+  const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
+  char *base = (char *)plan;
+  PlanArgs a;
+  a.table = table;
+  a.table_stride = table_stride;
+  a.lens = lens;
+  a.qrow = qrow;
+  a.select = select;
+  a.flag = flag;
+  a.rows = rows;
+  a.width = width;
+  a.block_size = block_size;
+  a.grid = grid;
+  a.cap = Lp.cap;
+  a.wg = (int2 *)(base + Lp.wg);
+  a.first = (int32_t *)(base + Lp.first);
+  a.row_off = (int32_t *)(base + Lp.row_off);
+  a.desc = (TileDesc *)(base + Lp.desc);
+  hipLaunchKernelGGL(plan_split_kernel, dim3(1), dim3(kSplitThreads), 0, (hipStream_t)stream, a);
+  int rc2 = check_hip(hipGetLastError(), "ekv_audit_plan split launch");
+  if (rc2 != EKV_OK || rows == 0) return rc2;
+  const int fill_blocks = std::min(rows, 4096);
+  hipLaunchKernelGGL(plan_fill_kernel, dim3(fill_blocks), dim3(kFillThreads), 0, (hipStream_t)stream, a);
+  return check_hip(hipGetLastError(), "ekv_audit_plan fill launch");
+}
+
+extern "C" int ekv_audit_tile_lse_planned(
+    const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head, const void *keys,
+    int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head, float k_scale,
+    const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow,
+    const uint8_t *select, const uint32_t *flag, float *lse, int64_t lse_plane_stride,
+    int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells, uint64_t *cycles,
+    int32_t cycles_rows, float scale, int32_t layer, int32_t group_first, int32_t groups,
+    int32_t group_rows, int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
+    int32_t head_dim, const void *plan, size_t plan_bytes, int32_t plan_rows, int32_t plan_width,
+    void *stream) {
+  Params p;
+  Launch L;
+  int rc = audit_setup(q, q_dtype, q_stride_token, q_stride_head, keys, kv_dtype, k_stride_block, k_stride_pos,
+                       k_stride_head, k_scale, table, table_stride, lens, qrow, select, flag, lse, lse_plane_stride,
+                       lse_layer_stride, lse_row_stride, cells, cycles, cycles_rows, scale, layer, group_first,
+                       groups, group_rows, rows, width, block_size, tile_blocks, head_dim, 0, p, L);
+  if (rc != EKV_OK) return rc;
+  rc = check_plan(plan, plan_bytes, plan_rows, plan_width, rows, width, "ekv_audit_tile_lse_planned");
+  if (rc != EKV_OK || rows == 0) return rc;
+  if (L.planned == nullptr) {  // the VALU shapes have no planned form: the self-contained kernel
+    hipLaunchKernelGGL(L.fn, dim3((unsigned)L.blocks), dim3(L.threads), L.lds, (hipStream_t)stream, p);
+    return check_hip(hipGetLastError(), "ekv_audit_tile_lse_planned launch");
+  }
+  const int grid = plan_grid();
+  const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
+  PlanView v;
+  v.wg = (const int2 *)((const char *)plan + Lp.wg);
+  v.desc = (const TileDesc *)((const char *)plan + Lp.desc);
+  v.cap = Lp.cap;
+  hipLaunchKernelGGL(L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v);
+  return check_hip(hipGetLastError(), "ekv_audit_tile_lse_planned launch");
 }

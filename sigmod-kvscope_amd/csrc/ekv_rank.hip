@@ -21,11 +21,19 @@
 // every share NaN (all tie -> index order); a +inf score makes the total +inf, so the finite
 // blocks get share 0 (tie, first) and the +inf blocks NaN (last); a total <= 0 gives equal
 // shares (index order).
+//
+// float64 scores (ekv_rank_uniform64) rank the float64 shares themselves: there two distinct
+// scores can divide to one share and tie, so a per-row kernel first takes each request's total
+// over its existing blocks with NumPy's own pairwise summation, and the ranking keys are the shares
+// clamp(s) / total (1 / n when total <= 0; NaN last), 64 bits wide, selected 8 bits a pass.
 #pragma clang fp contract(off)
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "ekv_common.hpp"
+#include "ekv_pairwise.hpp"
 
 namespace ekv {
 namespace rank {
@@ -36,11 +44,12 @@ constexpr int kMaxPer = 24;                  // blocks per thread, block tid + k
 constexpr int kMaxWidth = kThreads * kMaxPer;  // 12288: a row lives in registers
 static_assert(kMaxWidth < 65536, "a row's block counts fit 16-bit fields");
 constexpr int kRowRegs = 4;                  // rows per thread whose open count stays in registers
-constexpr uint32_t kClosed = 0xFFFFFFFFu;  // key of a block that is not open
 
 struct Params {
   const float *scores;
   int64_t scores_stride;
+  const double *scores64;  // float64 scores (ekv_rank_uniform64), with each request's NumPy total
+  const double *totals;
   const int32_t *blocks;
   const uint8_t *measured;
   const uint8_t *pinned;
@@ -119,6 +128,38 @@ __global__ __launch_bounds__(256) void count_kernel(const Params p, int32_t *cou
     counts[2 * r] = ex;
     counts[2 * r + 1] = pn;
   }
+}
+
+// Each request's float64 total for ekv_rank_uniform64: NumPy's sum of the clamped scores of its
+// existing blocks, in block order (Request.shares over the scores the controller passes, which
+// leave released blocks out: observe/allocation.py:46-52, observe/controller.py:425-431).  One
+// wave per row; with a released mask the existing blocks are listed in LDS first.
+__global__ __launch_bounds__(kWave) void total64_kernel(const Params p, double *totals) {
+  __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
+  __shared__ double s_leaf[kMaxLeaves];
+  __shared__ int s_map[kMaxWidth];
+  const int r = blockIdx.x;
+  const int lane = lane_id();
+  const int n = min(max(p.blocks[r], 0), p.width);
+  const double *srow = p.scores64 + (int64_t)r * p.scores_stride;
+  double total;
+  if (p.released == nullptr) {
+    total = numpy_sum([&](int i) { return clamp0(srow[i]); }, n, s_start, s_len, s_leaf);
+  } else {
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int m = 0;
+    for (int base = 0; base < n; base += kWave) {
+      const int b = base + lane;
+      const bool e = b < n && exists(p, r, b);
+      const uint64_t ballot = __ballot(e);
+      if (e) s_map[m + __popcll(ballot & below)] = b;
+      m += __popcll(ballot);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    total = numpy_sum([&](int i) { return clamp0(srow[s_map[i]]); }, m, s_start, s_len, s_leaf);
+  }
+  if (lane == 0) totals[r] = total;
 }
 
 // Sum of N values over the workgroup in one pass (every thread receives the sums).
@@ -232,9 +273,13 @@ __device__ __forceinline__ void view_row(const Params &p, int row, int L, const 
 
 // PER: blocks per thread (the row's width is at most kThreads * PER).  VIEW: also build the row's
 // view from the keep it decides (ekv_rank_uniform_view).
-template <int PER, bool VIEW = false>
+template <int PER, bool VIEW = false, bool F64 = false>
 __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   constexpr int kPer = PER;
+  using Score = typename std::conditional<F64, double, float>::type;
+  using Key = typename std::conditional<F64, unsigned long long, uint32_t>::type;
+  constexpr Key kClosedKey = ~Key(0);  // key of a block that is not open
+  constexpr int kPasses = F64 ? 8 : 4;  // 8-bit digits
   __shared__ uint8_t s_keep[VIEW ? kPer * kThreads : 1];
   __shared__ int32_t s_out[VIEW ? kPer * kThreads : 1];
   __shared__ long long s_red[5][kWaves];
@@ -260,14 +305,17 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
 #pragma unroll
     for (int k = 0; k < 5; ++k) c_in[k] = p.view_counts[5LL * row + k];
   }
-  const float *srow = p.scores + (int64_t)row * p.scores_stride;
-  float sv[kPer];
+  const Score *srow;
+  if constexpr (F64) srow = p.scores64 + (int64_t)row * p.scores_stride;
+  else srow = p.scores + (int64_t)row * p.scores_stride;
+  const double row_total = F64 ? p.totals[row] : 0.0;
+  Score sv[kPer];
   uint32_t gone_bits = 0, pin_mask_bits = 0;  // released / explicitly pinned, from the masks
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int b = tid + i * kThreads;
     const bool in = b < p.width;
-    sv[i] = in ? srow[b] : 0.0f;
+    sv[i] = in ? srow[b] : Score(0);
     if (p.released != nullptr)
       gone_bits |= (in && p.released[(int64_t)row * p.released_stride + b] != 0) ? (1u << i) : 0u;
     if (p.pinned != nullptr)
@@ -377,8 +425,8 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   // key mode of the row's shares: allocation.py:46-52 over the existing blocks
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    if ((exist_bits >> i) & 1u) {
-      const float s = sv[i];
+    if (!F64 && ((exist_bits >> i) & 1u)) {
+      const float s = (float)sv[i];
       q3[2] += __builtin_isnan(s) ? 1ll : 0ll;
       q3[2] += (__builtin_isinf(s) && s > 0.0f) ? 1ll << 16 : 0ll;
       q3[2] += s > 0.0f ? 1ll << 32 : 0ll;
@@ -397,16 +445,31 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   const long long open_count = (q3[2] >> 48) & 0xffff;
   const int mode = has_nan ? 0 : (has_inf ? 2 : (has_pos ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
 
-  // ---- keys of the open blocks (order-preserving, larger first), kClosed elsewhere ----------
-  uint32_t key[kPer];
+  // ---- keys of the open blocks (order-preserving, larger first), kClosedKey elsewhere -------
+  Key key[kPer];
+  if constexpr (F64) {
+    // the request's float64 shares, allocation.py:46-52: clamp(s) / total, or 1 / n for a total <= 0
+    // (n its existing blocks); a NaN share sorts last (key 0), +0 and -0 are one key
+    const double uniform = 1.0 / (double)(me.exist > 0 ? me.exist : 1);
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    key[i] = kClosed;
-    if (((exist_bits & ~pin_bits) >> i) & 1u) {
-      const float s = sv[i];
-      if (mode == 1) key[i] = s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
-      else if (mode == 2) key[i] = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
-      else key[i] = 0u;
+    for (int i = 0; i < kPer; ++i) {
+      key[i] = kClosedKey;
+      if (((exist_bits & ~pin_bits) >> i) & 1u) {
+        double v = row_total <= 0.0 ? uniform : clamp0((double)sv[i]) / row_total;
+        if (v == 0.0) v = 0.0;
+        key[i] = v != v ? 0ull : __builtin_bit_cast(unsigned long long, v) + 1ull;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      key[i] = kClosedKey;
+      if (((exist_bits & ~pin_bits) >> i) & 1u) {
+        const float s = (float)sv[i];
+        if (mode == 1) key[i] = s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
+        else if (mode == 2) key[i] = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
+        else key[i] = 0u;
+      }
     }
   }
 
@@ -419,18 +482,18 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     // double-buffered so that clearing the next one needs no extra barrier.  The select stops
     // early once the quota ends exactly at the end of a digit's bucket: every key with that
     // prefix is kept and no tie needs ranking.
-    uint32_t prefix = 0, mask = 0;
+    Key prefix = 0, mask = 0;
     int k_rem = (int)quota;
     bool whole = false;
     if (tid < 256) s_hist[0][tid] = 0;
     __syncthreads();
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int shift = 8 * (kPasses - 1) - 8 * pass;
       int *hist = s_hist[pass & 1];
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
-        if (key[i] != kClosed && (key[i] & mask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255], 1);
+        if (key[i] != kClosedKey && (key[i] & mask) == prefix) atomicAdd(&hist[(int)(key[i] >> shift) & 255], 1);
       if (tid < 256) s_hist[(pass & 1) ^ 1][tid] = 0;
       __syncthreads();
       if (wave == 0) {
@@ -456,8 +519,8 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
         }
       }
       __syncthreads();
-      prefix |= (uint32_t)s_digit << shift;
-      mask |= 255u << shift;
+      prefix |= (Key)s_digit << shift;
+      mask |= (Key)255 << shift;
       k_rem = s_krem;
       whole = __builtin_amdgcn_readfirstlane(s_whole) != 0;
       if (whole) break;
@@ -466,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
       // the quota is every key whose top bits are at least the prefix
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
-        open_keep |= (key[i] != kClosed && (key[i] & mask) >= prefix) ? (1u << i) : 0u;
+        open_keep |= (key[i] != kClosedKey && (key[i] & mask) >= prefix) ? (1u << i) : 0u;
     } else {
       // keep every key above the threshold and the first k_rem equal keys by block index
       const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -485,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const bool kept = key[i] != kClosed &&
+        const bool kept = key[i] != kClosedKey &&
                           (key[i] > prefix || (key[i] == prefix && s_count[i * kWaves + wave] + eq_rank[i] < k_rem));
         open_keep |= kept ? (1u << i) : 0u;
       }
@@ -630,4 +693,74 @@ extern "C" int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, c
   else
     hipLaunchKernelGGL(rank::rank_kernel<24>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_rank_uniform launch");
+}
+
+namespace {
+// workspace of ekv_rank_uniform64: the rows' float64 totals, then 2 * rows ints of mask counts
+size_t uniform64_totals_bytes(int32_t rows) { return ((size_t)(rows > 0 ? rows : 1) * 8 + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" size_t ekv_rank_uniform64_workspace(int32_t rows) {
+  if (rows < 0) return 0;
+  return uniform64_totals_bytes(rows) + (size_t)(rows > 0 ? rows : 1) * 2 * sizeof(int32_t);
+}
+
+extern "C" int ekv_rank_uniform64(const double *scores, int64_t scores_stride, const int32_t *blocks,
+                                  const uint8_t *measured, const uint8_t *pinned, int64_t pinned_stride,
+                                  const int32_t *pin_from, int32_t recent_blocks, const uint8_t *released,
+                                  int64_t released_stride, int32_t rows, int32_t width, double fraction,
+                                  int64_t budget, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                                  void *workspace, size_t workspace_bytes, void *stream) {
+  if (scores == nullptr || blocks == nullptr || keep == nullptr || workspace == nullptr)
+    return fail(EKV_EINVAL, "ekv_rank_uniform64: null pointer");
+  if (rows < 0 || width < 1 || width > rank::kMaxWidth)
+    return fail(EKV_EINVAL, "ekv_rank_uniform64: rows %d, width %d (at most %d)", rows, width, rank::kMaxWidth);
+  if (recent_blocks < 0) return fail(EKV_EINVAL, "ekv_rank_uniform64: recent_blocks %d < 0", recent_blocks);
+  if (budget < 0 && !(fraction > 0.0 && fraction <= 1.0))
+    return fail(EKV_EINVAL, "ekv_rank_uniform64: the budget fraction %g is not in (0, 1]", fraction);
+  if (workspace_bytes < ekv_rank_uniform64_workspace(rows))
+    return fail(EKV_EINVAL, "ekv_rank_uniform64: a workspace of %zu bytes, %zu needed", workspace_bytes,
+                ekv_rank_uniform64_workspace(rows));
+  if (rows == 0) return EKV_OK;
+  rank::Params p{};
+  p.scores64 = scores;
+  p.scores_stride = scores_stride;
+  p.blocks = blocks;
+  p.measured = measured;
+  p.pinned = pinned;
+  p.pinned_stride = pinned_stride;
+  p.pin_from = pin_from;
+  p.recent = recent_blocks;
+  p.released = released;
+  p.released_stride = released_stride;
+  p.rows = rows;
+  p.width = width;
+  p.fraction = fraction;
+  p.budget_in = budget;
+  p.keep = keep;
+  p.keep_stride = keep_stride;
+  p.summary = summary;
+  double *totals = (double *)workspace;
+  int32_t *counts = (int32_t *)((char *)workspace + uniform64_totals_bytes(rows));
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(rank::total64_kernel, dim3(rows), dim3(kWave), 0, s, p, totals);
+  int rc = check_hip(hipGetLastError(), "ekv_rank_uniform64 totals launch");
+  if (rc != EKV_OK) return rc;
+  p.totals = totals;
+  if (pinned != nullptr || released != nullptr) {
+    hipLaunchKernelGGL(rank::count_kernel, dim3(rows), dim3(256), 0, s, p, counts);
+    rc = check_hip(hipGetLastError(), "ekv_rank_uniform64 count launch");
+    if (rc != EKV_OK) return rc;
+    p.counts = counts;
+  }
+  const int per = (width + rank::kThreads - 1) / rank::kThreads;
+  if (per <= 4)
+    hipLaunchKernelGGL((rank::rank_kernel<4, false, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (per <= 8)
+    hipLaunchKernelGGL((rank::rank_kernel<8, false, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (per <= 16)
+    hipLaunchKernelGGL((rank::rank_kernel<16, false, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((rank::rank_kernel<24, false, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  return check_hip(hipGetLastError(), "ekv_rank_uniform64 launch");
 }

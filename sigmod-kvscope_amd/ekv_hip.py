@@ -39,6 +39,24 @@ _SIGNATURES: dict[str, list] = {
         _i32, _i32, _i32, _i32, _i32, _i32,  # rows, width, block_size, tile_blocks, head_dim, chunk_tiles
         _p,  # stream
     ],
+    "ekv_audit_plan_bytes": [_i32, _i32],
+    "ekv_audit_plan": [
+        _p, _i64, _p, _p, _p, _p,  # table, stride, lens, qrow, select, flag
+        _i32, _i32, _i32, _i32,  # rows, width, block_size, tile_blocks
+        _p, _sz, _i32, _i32,  # plan, plan bytes, plan rows, plan width
+        _p,  # stream
+    ],
+    "ekv_audit_tile_lse_planned": [
+        _p, _i32, _i64, _i64,  # q, q dtype, strides
+        _p, _i32, _i64, _i64, _i64, _f32,  # keys, kv dtype, strides, k_scale
+        _p, _i64, _p, _p, _p, _p,  # table, stride, lens, qrow, select, flag
+        _p, _i64, _i64, _i64, _i32,  # lse, plane / layer / row strides, cells
+        _p, _i32,  # cycles, cycles_rows
+        _f32, _i32, _i32, _i32, _i32,  # scale, layer, group_first, groups, group_rows
+        _i32, _i32, _i32, _i32, _i32,  # rows, width, block_size, tile_blocks, head_dim
+        _p, _sz, _i32, _i32,  # plan, plan bytes, plan rows, plan width
+        _p,  # stream
+    ],
     "ekv_tile_shares": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_tile_shares_workspace": [_i32, _i32, _i32],
     "ekv_tile_shares_ws": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _sz, _p],
@@ -48,6 +66,10 @@ _SIGNATURES: dict[str, list] = {
     ],
     "ekv_rank_uniform_ws": [
         _p, _i64, _p, _p, _p, _i64, _p, _i32, _p, _i64, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _p,
+    ],
+    "ekv_rank_uniform64_workspace": [_i32],
+    "ekv_rank_uniform64": [
+        _p, _i64, _p, _p, _p, _i64, _p, _i32, _p, _i64, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _sz, _p,
     ],
     "ekv_rank_uniform_view": [
         _p, _i64, _p, _p, _p, _i32, _i32, _i32, _f64, _i64, _p, _i64, _p, _p, _i64, _p, _i32, _p, _i64, _p, _p, _p,
@@ -92,7 +114,7 @@ def load() -> ctypes.CDLL:
         fn.argtypes = args
         if name == "ekv_last_error":
             fn.restype = ctypes.c_char_p
-        elif name.endswith("_workspace"):
+        elif name.endswith("_workspace") or name.endswith("_bytes"):
             fn.restype = ctypes.c_size_t
         else:
             fn.restype = ctypes.c_int

@@ -11,8 +11,14 @@ to the lowest request first (``ekv_rank_maxmin``).  Pinned
 blocks (by default the first and the last) always count against the budget, and a budget below
 them is an error.
 
-The device ranks float32 shares.  For float32 scores that order is exactly the reference's stable
-argsort of the float64 ``shares()``; float64 scores are rounded to float32 first.
+``uniform`` ranks float32 scores by value -- for float32 scores that order is exactly the
+reference's stable argsort of the float64 ``shares()`` -- and float64 scores by their float64 shares
+``max(s, 0) / total`` themselves (``ekv_rank_uniform64``, the total being NumPy's pairwise sum), so
+that two scores that divide to one share tie as they do in the reference.  ``allocate`` always takes
+the float64 path.
+
+Every device wrapper checks its tensors on the host (device, dtype, shape, contiguous rows) and
+raises ``ValueError`` before any launch.
 """
 
 from __future__ import annotations
@@ -27,6 +33,50 @@ import torch
 import ekv_hip
 
 Objective = Literal["sum", "maxmin", "uniform"]
+_MASK_DTYPES = (torch.uint8, torch.bool)
+
+
+def check_tensors(*specs) -> torch.device | None:
+    """Refuse, with ValueError, tensors a kernel would misread.  ``specs`` are ``(name, tensor, dtypes,
+    shape)``, ``tensor`` None for an absent optional one.  Every tensor's shape, dtype and row
+    contiguity are checked first, then that all are on one GPU; returns that device."""
+    present = [(name, t, dtypes, shape) for name, t, dtypes, shape in specs if t is not None]
+    for name, t, dtypes, shape in present:
+        if not isinstance(t, torch.Tensor):
+            raise ValueError(f"{name} must be a torch tensor")
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+        if t.dtype not in (dtypes if isinstance(dtypes, tuple) else (dtypes,)):
+            raise ValueError(f"{name} must be {dtypes}, got {t.dtype}")
+        if t.ndim and t.stride(-1) != 1:
+            raise ValueError(f"{name} must have contiguous rows")
+    device = None
+    for name, t, _, _ in present:
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a device tensor")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"{name} is on {t.device}, the others on {device}")
+    return device
+
+
+def _out(out: torch.Tensor | None, rows: int, width: int, device) -> torch.Tensor:
+    if out is None:
+        return torch.empty(rows, width, dtype=torch.uint8, device=device)
+    if check_tensors(("out", out, torch.uint8, (rows, width))) != device:
+        raise ValueError(f"out must be on {device}")
+    return out
+
+
+def _workspace(name: str, workspace: torch.Tensor | None, need: int, device) -> torch.Tensor:
+    if workspace is None:
+        return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if not (workspace.is_cuda and workspace.dtype == torch.uint8 and workspace.is_contiguous()):
+        raise ValueError(f"{name} must be a contiguous uint8 device tensor")
+    if workspace.device != device or workspace.numel() < need:
+        raise ValueError(f"{name} must hold at least {need} bytes on {device}")
+    return workspace
 
 
 @dataclass(frozen=True)
@@ -106,6 +156,12 @@ def _maxmin_on_device(requests: Sequence[Request], pinned: list[np.ndarray], bud
     return [keep[i, : sizes[i]].astype(bool) for i in range(len(requests))]
 
 
+def _rows_width(scores) -> tuple[int, int]:
+    if not isinstance(scores, torch.Tensor) or scores.ndim != 2:
+        raise ValueError("scores must be a [rows, width] tensor")
+    return int(scores.shape[0]), int(scores.shape[1])
+
+
 def maxmin_keep(
     scores: torch.Tensor,
     blocks: torch.Tensor,
@@ -113,32 +169,39 @@ def maxmin_keep(
     budget: int,
     pinned: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The ``maxmin`` keep mask ``uint8[rows, width]`` on the device (observe/allocation.py:126-166)
-    and the int64 summary (budget, blocks, pinned, status, requests, free); arguments as sum_keep."""
-    if scores.dtype == torch.float32:
-        scores = scores.double()
-    if scores.dtype != torch.float64 or scores.stride(1) != 1:
-        raise ValueError("scores must be float64 (or float32) with contiguous rows")
-    rows, width = int(scores.shape[0]), int(scores.shape[1])
-    if blocks.dtype != torch.int32 or blocks.shape != (rows,):
-        raise ValueError("blocks must be int32 [rows]")
-    if pinned is not None and (pinned.dtype not in (torch.uint8, torch.bool) or pinned.stride(-1) != 1):
-        raise ValueError("pinned must be a uint8 / bool mask with contiguous rows")
+    and the int64 summary (budget, blocks, pinned, status, requests, free); arguments as sum_keep.
+    ``workspace``: a uint8 device tensor of at least ``maxmin_workspace_bytes(rows, width)`` bytes
+    (allocated here when None)."""
+    rows, width = _rows_width(scores)
+    dev = check_tensors(("scores", scores, (torch.float32, torch.float64), (rows, width)),
+                        ("blocks", blocks, torch.int32, (rows,)), ("pinned", pinned, _MASK_DTYPES, (rows, width)))
+    scores = scores.double() if scores.dtype == torch.float32 else scores
     if budget < 0:
         raise ValueError("the budget cannot be negative")
-    if out is None:
-        out = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
-    summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
-    need = int(ekv_hip.load().ekv_rank_maxmin_workspace(rows, width))
-    workspace = torch.empty(need, dtype=torch.uint8, device=scores.device)
+    out = _out(out, rows, width, dev)
+    summary = torch.zeros(6, dtype=torch.int64, device=dev)
+    need = maxmin_workspace_bytes(rows, width)
+    workspace = _workspace("workspace", workspace, need, dev)
     ekv_hip.call(
         "ekv_rank_maxmin", scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(pinned),
         pinned.stride(0) if pinned is not None else 0, rows, width, int(budget), out.data_ptr(), out.stride(0),
-        summary.data_ptr(), workspace.data_ptr(), need, ekv_hip.stream_handle(stream),
+        summary.data_ptr(), workspace.data_ptr(), workspace.numel(), ekv_hip.stream_handle(stream),
     )
     return out, summary
+
+
+def maxmin_workspace_bytes(rows: int, width: int) -> int:
+    """Device bytes ``maxmin_keep`` needs as its workspace."""
+    return int(ekv_hip.load().ekv_rank_maxmin_workspace(int(rows), int(width)))
+
+
+def sum_workspace_bytes(rows: int) -> int:
+    """Device bytes ``sum_keep`` needs as its workspace."""
+    return int(ekv_hip.load().ekv_rank_sum_workspace(int(rows)))
 
 
 def sum_keep(
@@ -149,57 +212,40 @@ def sum_keep(
     weights: torch.Tensor | None = None,
     pinned: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The ``sum`` keep mask ``uint8[rows, width]`` on the device (observe/allocation.py:94-123) and
     the int64 summary (budget, blocks, pinned, status, requests, free).
 
     ``scores`` float64 [rows, width] (float32 is widened, exactly); ``blocks`` int32 [rows];
-    ``weights`` float64 [rows] (default 1.0); ``pinned`` a uint8 / bool mask (default: the first
-    and the last block of each row)."""
-    if scores.dtype == torch.float32:
-        scores = scores.double()
-    if scores.dtype != torch.float64 or scores.stride(1) != 1:
-        raise ValueError("scores must be float64 (or float32) with contiguous rows")
-    rows, width = int(scores.shape[0]), int(scores.shape[1])
-    if blocks.dtype != torch.int32 or blocks.shape != (rows,):
-        raise ValueError("blocks must be int32 [rows]")
-    if weights is not None and (weights.dtype != torch.float64 or weights.shape != (rows,)):
-        raise ValueError("weights must be float64 [rows]")
-    if pinned is not None and (pinned.dtype not in (torch.uint8, torch.bool) or pinned.stride(-1) != 1):
-        raise ValueError("pinned must be a uint8 / bool mask with contiguous rows")
+    ``weights`` float64 [rows] (default 1.0); ``pinned`` a uint8 / bool [rows, width] mask (default:
+    the first and the last block of each row); ``workspace`` a uint8 device tensor of at least
+    ``sum_workspace_bytes(rows)`` bytes (allocated here when None)."""
+    rows, width = _rows_width(scores)
+    dev = check_tensors(("scores", scores, (torch.float32, torch.float64), (rows, width)),
+                        ("blocks", blocks, torch.int32, (rows,)), ("weights", weights, torch.float64, (rows,)),
+                        ("pinned", pinned, _MASK_DTYPES, (rows, width)))
+    scores = scores.double() if scores.dtype == torch.float32 else scores
     if budget < 0:
         raise ValueError("the budget cannot be negative")
-    if out is None:
-        out = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
-    summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
-    need = int(ekv_hip.load().ekv_rank_sum_workspace(rows))
-    workspace = torch.empty(need, dtype=torch.uint8, device=scores.device)
+    out = _out(out, rows, width, dev)
+    summary = torch.zeros(6, dtype=torch.int64, device=dev)
+    need = sum_workspace_bytes(rows)
+    workspace = _workspace("workspace", workspace, need, dev)
     ekv_hip.call(
         "ekv_rank_sum", scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(weights),
         ekv_hip.ptr(pinned), pinned.stride(0) if pinned is not None else 0, rows, width, int(budget),
-        out.data_ptr(), out.stride(0), summary.data_ptr(), workspace.data_ptr(), need,
+        out.data_ptr(), out.stride(0), summary.data_ptr(), workspace.data_ptr(), workspace.numel(),
         ekv_hip.stream_handle(stream),
     )
     return out, summary
 
 
 def _uniform_on_device(requests: Sequence[Request], pinned: list[np.ndarray], budget: int) -> list[np.ndarray]:
-    rows = len(requests)
-    sizes = [len(r.scores) for r in requests]
-    width = max(max(sizes, default=1), 1)
-    scores = np.zeros((rows, width), dtype=np.float32)
-    pins = np.zeros((rows, width), dtype=np.uint8)
-    for i, (req, pin) in enumerate(zip(requests, pinned)):
-        scores[i, : sizes[i]] = np.asarray(req.scores, dtype=np.float32)
-        pins[i, : sizes[i]] = pin
-    keep = uniform_keep(
-        torch.from_numpy(scores).cuda(),
-        torch.tensor(sizes, dtype=torch.int32).cuda(),
-        pinned=torch.from_numpy(pins).cuda(),
-        budget=budget,
-    )[0].cpu().numpy()
-    return [keep[i, : sizes[i]].astype(bool) for i in range(rows)]
+    scores, pins, blocks, sizes = _padded(requests, pinned)
+    keep = uniform_keep(scores, blocks, pinned=pins, budget=budget)[0].cpu().numpy()
+    return [keep[i, : sizes[i]].astype(bool) for i in range(len(requests))]
 
 
 def uniform_keep(
@@ -214,43 +260,46 @@ def uniform_keep(
     fraction: float = 1.0,
     budget: int = -1,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """The ``uniform`` keep mask ``uint8[rows, width]`` of every row, on the device, and the int64
     summary (budget, total, pinned floor, status, requests, free).
 
-    ``scores`` float32 [rows, width]; ``blocks`` int32 [rows] blocks per row.  Pins are ``pinned``
-    when given (Request.pinned), else block 0, the ``recent_blocks`` newest after the last, and
-    blocks >= ``pin_from`` (observe/controller.py:420-424).  ``budget < 0`` takes the controller's
-    ``max(floor, ceil(fraction * total))`` (observe/controller.py:435-437)."""
-    rows, width = int(scores.shape[0]), int(scores.shape[1])
-    if scores.dtype != torch.float32 or scores.stride(1) != 1:
-        raise ValueError("scores must be float32 with contiguous rows")
-    if blocks.dtype != torch.int32 or blocks.shape != (rows,):
-        raise ValueError("blocks must be int32 [rows]")
-    for name, t in (("measured", measured), ("pinned", pinned), ("released", released)):
-        if t is not None and (t.dtype not in (torch.uint8, torch.bool) or t.stride(-1) != 1):
-            raise ValueError(f"{name} must be a uint8 / bool mask with contiguous rows")
-    if measured is not None and measured.shape != (rows,):
-        raise ValueError("measured must be [rows]")
-    for name, t in (("pinned", pinned), ("released", released)):
-        if t is not None and t.shape != (rows, width):
-            raise ValueError(f"{name} must be [rows, width] like scores")
-    if pin_from is not None and (pin_from.dtype != torch.int32 or pin_from.shape != (rows,)):
-        raise ValueError("pin_from must be int32 [rows]")
-    if out is None:
-        out = torch.empty(rows, width, dtype=torch.uint8, device=scores.device)
-    summary = torch.zeros(6, dtype=torch.int64, device=scores.device)
-    workspace = None
-    if pinned is not None or released is not None:
-        workspace = torch.empty(2 * max(rows, 1), dtype=torch.int32, device=scores.device)
-    ekv_hip.call(
-        "ekv_rank_uniform_ws",
+    ``scores`` float32 or float64 [rows, width] (float64 ranks the float64 shares); ``blocks`` int32
+    [rows] blocks per row.  Pins are ``pinned`` when given (Request.pinned), else block 0, the
+    ``recent_blocks`` newest after the last, and blocks >= ``pin_from`` (observe/controller.py:420-424).
+    ``budget < 0`` takes the controller's ``max(floor, ceil(fraction * total))``
+    (observe/controller.py:435-437).  ``workspace``: a uint8 device tensor of at least
+    ``uniform_workspace_bytes(rows, scores.dtype)`` bytes (allocated here when None and needed)."""
+    rows, width = _rows_width(scores)
+    dev = check_tensors(("scores", scores, (torch.float32, torch.float64), (rows, width)),
+                        ("blocks", blocks, torch.int32, (rows,)), ("measured", measured, _MASK_DTYPES, (rows,)),
+                        ("pinned", pinned, _MASK_DTYPES, (rows, width)),
+                        ("released", released, _MASK_DTYPES, (rows, width)),
+                        ("pin_from", pin_from, torch.int32, (rows,)))
+    out = _out(out, rows, width, dev)
+    summary = torch.zeros(6, dtype=torch.int64, device=dev)
+    wide = scores.dtype == torch.float64
+    need = uniform_workspace_bytes(rows, scores.dtype) if (wide or pinned is not None or released is not None) else 0
+    ws = _workspace("workspace", workspace, need, dev) if need else None
+    common = (
         scores.data_ptr(), scores.stride(0), blocks.data_ptr(), ekv_hip.ptr(measured),
         ekv_hip.ptr(pinned), pinned.stride(0) if pinned is not None else 0,
         ekv_hip.ptr(pin_from), int(recent_blocks),
         ekv_hip.ptr(released), released.stride(0) if released is not None else 0,
         rows, width, float(fraction), int(budget), out.data_ptr(), out.stride(0), summary.data_ptr(),
-        ekv_hip.ptr(workspace), ekv_hip.stream_handle(stream),
     )
+    if wide:
+        ekv_hip.call("ekv_rank_uniform64", *common, ws.data_ptr(), ws.numel(), ekv_hip.stream_handle(stream))
+    else:
+        ekv_hip.call("ekv_rank_uniform_ws", *common, ekv_hip.ptr(ws), ekv_hip.stream_handle(stream))
     return out, summary
+
+
+def uniform_workspace_bytes(rows: int, dtype=torch.float32) -> int:
+    """Device bytes ``uniform_keep`` needs as its workspace: the per-row totals of float64 scores
+    and the mask counts (float32 scores need it only with pinned or released masks)."""
+    if dtype == torch.float64:
+        return int(ekv_hip.load().ekv_rank_uniform64_workspace(int(rows)))
+    return 8 * max(int(rows), 1)

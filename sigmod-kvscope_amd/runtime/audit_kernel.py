@@ -73,6 +73,11 @@ class RecordingPlane(AuditPlane):
         ekv_hip.memset(self._table_dev, 0, layers * 8)
         self._select = torch.zeros(rows, dtype=torch.uint8, device="cuda")
         self._token = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        # the step plan: the work list of the step's launches, built at its first layer
+        self._plan_bytes = int(ekv_hip.load().ekv_audit_plan_bytes(rows, width))
+        self._plan = self._allocate(self._plan_bytes) if self._plan_bytes else 0
+        if self._plan:
+            ekv_hip.memset(self._plan, 0, self._plan_bytes)  # an empty plan until the first is built
         self.timer = _enabled("EKV_TIMER") if timer is None else bool(timer)
         self._cycles_dev = 0
         if self.timer:
@@ -191,7 +196,35 @@ class RecordingPlane(AuditPlane):
         if kv_cache.shape[2] != self.block_size:
             raise ValueError("the KV cache's block size differs from the view's")
         layer = self._layer_of.setdefault(layer_name, len(self._layer_of))
-        self.launch(layer, table, lens, query, kv_cache[:, 0], scale)
+        planned = bool(self._plan)
+        if planned and layer == 0:  # the step's first layer: every layer of the step reads these buffers
+            self.plan(table, lens)
+        self.launch(layer, table, lens, query, kv_cache[:, 0], scale, planned=planned)
+
+    def _batch_shape(self, table: torch.Tensor, lens: torch.Tensor) -> tuple[int, int]:
+        for name, t in (("table", table), ("lens", lens)):
+            if not t.is_cuda:
+                raise ValueError(f"{name} must be a device tensor")
+        if table.dtype != torch.int32 or lens.dtype != torch.int32:
+            raise ValueError("the block table and lengths must be int32")
+        if table.ndim != 2 or table.stride(1) != 1 or lens.ndim != 1 or lens.stride(0) != 1:
+            raise ValueError("the block table rows and the lengths must be contiguous")
+        return min(self.rows, table.shape[0], lens.shape[0]), min(self.width, table.shape[1])
+
+    def plan(self, table: torch.Tensor, lens: torch.Tensor, *, stream=None) -> None:
+        """Build the step plan from the view buffers and the selected rows: each audit workgroup's
+        tiles with their rows, block ids and query tokens, the work list every launch of the step
+        shares (``launch(..., planned=True)``).  Launched on the stream like the audits, so a graph
+        that captures a step captures it."""
+        if not self._plan:
+            raise RuntimeError("this plane is too large for a step plan")
+        rows, width = self._batch_shape(table, lens)
+        ekv_hip.call(
+            "ekv_audit_plan",
+            table.data_ptr(), table.stride(0), lens.data_ptr(), self._token.data_ptr(), self._select.data_ptr(),
+            self._flag_dev, rows, width, self.block_size, TILE_BLOCKS,
+            self._plan, self._plan_bytes, self.rows, self.width, ekv_hip.stream_handle(stream),
+        )
 
     def launch(
         self,
@@ -204,10 +237,13 @@ class RecordingPlane(AuditPlane):
         *,
         k_scale: float = 1.0,
         chunk_tiles: int = 0,
+        planned: bool = False,
         stream=None,
     ) -> None:
         """Launch the audit kernel for ``layer``; ``keys`` is the key cache [blocks, block, heads, dim]
-        (runtime/audit_kernel.py:224-265).  ``k_scale`` dequantises an fp8 key cache."""
+        (runtime/audit_kernel.py:224-265).  ``k_scale`` dequantises an fp8 key cache.  ``planned``
+        reads the work list ``plan`` built from the same table, lengths and selection; otherwise the
+        launch builds it itself."""
         if layer >= self._layers:
             raise RuntimeError(f"more attention layers ran than the {self._layers} the plane was sized for")
         kv_heads, dim = keys.shape[2], keys.shape[3]
@@ -217,24 +253,20 @@ class RecordingPlane(AuditPlane):
             raise ValueError(f"the plane records {self.kv_heads} KV heads, the cache has {kv_heads}")
         if keys.shape[1] != self.block_size:
             raise ValueError("the key cache's block size differs from the plane's")
-        for name, t in (("table", table), ("lens", lens), ("query", query), ("keys", keys)):
+        for name, t in (("query", query), ("keys", keys)):
             if not t.is_cuda:
                 raise ValueError(f"{name} must be a device tensor")
-        if table.dtype != torch.int32 or lens.dtype != torch.int32:
-            raise ValueError("the block table and lengths must be int32")
-        if table.ndim != 2 or table.stride(1) != 1 or lens.ndim != 1 or lens.stride(0) != 1:
-            raise ValueError("the block table rows and the lengths must be contiguous")
+        rows, width = self._batch_shape(table, lens)
         if query.stride(2) != 1 or keys.stride(3) != 1:
             raise ValueError("query and key rows must be contiguous in the head dimension")
-        rows = min(self.rows, table.shape[0], lens.shape[0])
-        width = min(self.width, table.shape[1])
+        if planned and not self._plan:
+            raise RuntimeError("this plane is too large for a step plan")
         plane, layer_stride, row_stride = self.strides
         if self.kv_heads is None:
             group_first, groups = layer % kv_heads, 1  # runtime/audit_kernel.py:250
         else:
             group_first, groups = 0, kv_heads
-        ekv_hip.call(
-            "ekv_audit_tile_lse",
+        common = (
             query.data_ptr(), ekv_hip.dtype_code(query.dtype), query.stride(0), query.stride(1),
             keys.data_ptr(), ekv_hip.dtype_code(keys.dtype), keys.stride(0), keys.stride(1), keys.stride(2),
             float(k_scale),
@@ -243,6 +275,10 @@ class RecordingPlane(AuditPlane):
             self._lse, plane, layer_stride, row_stride, self.cells,
             self._cycles_dev, self.rows if self._cycles_dev else 0,
             float(scale), layer, group_first, groups, self.group_rows,
-            rows, width, self.block_size, TILE_BLOCKS, dim, int(chunk_tiles),
-            ekv_hip.stream_handle(stream),
+            rows, width, self.block_size, TILE_BLOCKS, dim,
         )
+        if planned:
+            ekv_hip.call("ekv_audit_tile_lse_planned", *common, self._plan, self._plan_bytes, self.rows, self.width,
+                         ekv_hip.stream_handle(stream))
+        else:
+            ekv_hip.call("ekv_audit_tile_lse", *common, int(chunk_tiles), ekv_hip.stream_handle(stream))

@@ -63,3 +63,10 @@ def random_requests(rng: np.random.Generator, count: int, max_blocks: int, ties:
         scores.append(s)
         pinned.append(p)
     return scores, pinned
+
+
+def audit_on(plane, caches=()) -> None:
+    """Switch a recording plane on the way the engine does (runtime/block_view.py:283-288 with
+    runtime/audit.py:86-113): the layer table first, then the flag."""
+    plane.attach([int(c.data_ptr()) for c in caches] or [0])
+    plane.set(True)

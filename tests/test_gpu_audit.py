@@ -16,7 +16,9 @@ LSE_TOL = 1e-3
 
 
 def flag(plane, on=True):
-    plane._copy_to_device(plane._flag_dev, np.array([1 if on else 0], dtype=np.uint32))
+    """The audit flag through the engine's protocol: attach once, then set."""
+    plane.attach([0])
+    plane.set(on)
 
 
 def record(plane, layer, table, lens, q, keys, scale, select=None, **kw):

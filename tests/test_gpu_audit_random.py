@@ -12,6 +12,7 @@ import torch
 from oracle import audit as oa
 from oracle import tile_shares as ots
 from runtime.audit_kernel import RecordingPlane
+from cases import audit_on
 
 pytestmark = pytest.mark.gpu
 FP8 = getattr(torch, "float8_e4m3fn", None)
@@ -68,7 +69,7 @@ def test_random_batch_against_the_oracle(seed):
     q = torch.from_numpy(rng.standard_normal((c["tokens"], hkv * G, d), dtype=np.float32)).to(qdtype)
     layers = c["layer"] + 1
     plane = RecordingPlane(layers, rows, c["width"], G, bs, kv_heads=hkv if c["every_head"] else None)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    audit_on(plane)
     plane.select(c["select"], c["qrow"])
     scale = d ** -0.5
     plane.launch(c["layer"], torch.from_numpy(c["table"]).cuda(), torch.from_numpy(c["lens"]).cuda(), q.cuda(),

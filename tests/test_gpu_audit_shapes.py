@@ -10,6 +10,7 @@ import torch
 from oracle import audit as oa
 from oracle import tile_shares as ots
 from runtime.audit_kernel import RecordingPlane
+from cases import audit_on
 
 pytestmark = pytest.mark.gpu
 FP8 = getattr(torch, "float8_e4m3fn", None)
@@ -56,7 +57,7 @@ def test_shapes_against_the_oracle(dtype, d, bs, G):
     lens, table, width, kv, q, k_scale = case(torch_dtype, d, bs, G, seed=d * 100 + bs * 10 + G)
     rows = len(lens)
     plane = RecordingPlane(1, rows, width, G, bs)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    audit_on(plane)
     plane.select(np.ones(rows, bool), np.arange(rows))
     scale = d ** -0.5
     kv_d, q_d = kv.cuda(), q.cuda()
@@ -107,7 +108,7 @@ def test_the_largest_row_count(dtype, d):
     q = torch.from_numpy(rng.standard_normal((rows, hkv * G, d), dtype=np.float32)).to(torch.bfloat16)
     select = rng.random(rows) < 0.9
     plane = RecordingPlane(1, rows, width, G, bs)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
+    audit_on(plane)
     plane.select(select, np.arange(rows))
     scale = d ** -0.5
     plane.launch(0, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), q.cuda(), kv.cuda()[:, 0], scale,

@@ -23,13 +23,15 @@ def test_controller_reads_the_planes_of_another_process(tmp_path, monkeypatch):
     monkeypatch.setenv("EKV_RUNTIME_DIR", str(tmp_path))
     batch, kv, q = workloads.config1()
     plane = RecordingPlane(3, batch.rows, batch.width, batch.group_rows, batch.block_size)
-    plane._copy_to_device(plane._flag_dev, np.array([1], dtype=np.uint32))
-    plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
     kv_t = torch.from_numpy(kv).cuda()
+    # the engine's protocol: two of the three layers' caches attached (the controller counts the
+    # filled entries as the layers that ran), the rows selected, the flag set
+    plane.attach([kv_t.data_ptr(), kv_t.data_ptr() + 1])
+    plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
+    plane.set(True)
     table, lens = torch.from_numpy(batch.table).cuda(), torch.from_numpy(batch.lens).cuda()
     for layer in range(2):  # two of the three layers run
         plane.record(f"layer.{layer}", table, lens, torch.from_numpy(q).cuda(), kv_t, batch.head_dim ** -0.5)
-    plane.attach([kv_t.data_ptr(), kv_t.data_ptr() + 1])
     torch.cuda.synchronize()
     row_blocks = batch.blocks.copy()
     row_blocks[1] = 0  # a row without blocks is not read

@@ -95,3 +95,48 @@ def test_uniform_keep_rejects_masks_of_another_shape():
         allocation.uniform_keep(scores, blocks, released=torch.zeros(3, 8, dtype=torch.uint8))
     with pytest.raises(ValueError):
         allocation.uniform_keep(scores, blocks, measured=torch.zeros(3, dtype=torch.uint8))
+
+
+def test_device_wrappers_refuse_host_tensors_and_wrong_shapes():
+    # every device wrapper checks its tensors before any launch: a host tensor or a short mask is a
+    # ValueError, not a device read of a host address or past a buffer (runs without a GPU)
+    import torch
+
+    from runtime.block_view import compact_block_table, uniform_view
+
+    s = torch.zeros(3, 8)
+    n = torch.ones(3, dtype=torch.int32)
+    t = torch.zeros(3, 8, dtype=torch.int32)
+    with pytest.raises(ValueError, match="device"):
+        allocation.uniform_keep(s, n)
+    with pytest.raises(ValueError, match="device"):
+        allocation.uniform_keep(s.double(), n)
+    with pytest.raises(ValueError, match="device"):
+        allocation.sum_keep(s, n, budget=3)
+    with pytest.raises(ValueError, match="device"):
+        allocation.maxmin_keep(s, n, budget=3)
+    with pytest.raises(ValueError, match="device"):
+        uniform_view(s, n, t, n, 16)
+    with pytest.raises(ValueError, match="device"):
+        compact_block_table(t, n, torch.ones(3, 8, dtype=torch.bool), 16)
+    with pytest.raises(ValueError):
+        allocation.uniform_keep(torch.zeros(3, 8, dtype=torch.int32), n)  # integer scores
+    with pytest.raises(ValueError):
+        allocation.uniform_keep(s.reshape(-1), n)  # not [rows, width]
+
+
+def test_shape_checks_name_the_tensor():
+    # shapes and dtypes are checked before the device: a pinned mask narrower than the scores, a
+    # blocks vector of another length, weights of another dtype, rows that are not contiguous
+    import torch
+
+    s = torch.zeros(4, 8)
+    n = torch.ones(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="pinned must have shape"):
+        allocation.uniform_keep(s, n, pinned=torch.ones(4, 7, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="blocks must have shape"):
+        allocation.uniform_keep(s, torch.ones(3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="weights must be"):
+        allocation.sum_keep(s, n, budget=4, weights=torch.ones(4, dtype=torch.float32))
+    with pytest.raises(ValueError, match="contiguous"):
+        allocation.uniform_keep(torch.zeros(8, 4).t(), n)
