@@ -22,27 +22,40 @@ import ekv_hip
 COUNTS = 5  # blocks read, blocks a full read would read, read in audits, read untrimmed, read without a live policy
 
 
+def _capacity(need: int) -> int:
+    """The next power of two at or above ``need`` (at least 1): buffers grow by doubling."""
+    return 1 << max(0, int(need) - 1).bit_length()
+
+
 class SlotCompactor:
-    """The buffers of the compaction, kept from step to step (runtime/sglang_compact.py:109-167).
-    They grow when a batch needs more and never shrink."""
+    """Device scratch of the compaction and the read counters, for one view (the contract of
+    runtime/sglang_compact.py:99-167).
+
+    The scratch -- the new offsets, lengths and block tables of the rows, and the gathered list --
+    lives across steps so that a step allocates nothing once the batches have been seen; it grows to
+    the next power of two when a batch needs more rows, entries or a wider slot type."""
 
     def __init__(self, width: int, block_tokens: int, device: torch.device) -> None:
+        if width <= 0 or block_tokens <= 0:
+            raise ValueError(f"a view of {width} blocks of {block_tokens} tokens is empty")
         self.width, self.block_tokens, self.device = width, block_tokens, device
-        self.counts = torch.zeros(COUNTS, dtype=torch.int64, device=device)
-        self.no_audit = torch.zeros(1, dtype=torch.uint8, device=device)
-        self._rows = 0
-        self.new_indptr = self.lens = self.table = torch.empty(0, dtype=torch.int32, device=device)
-        self._out: torch.Tensor = torch.empty(0, dtype=torch.int64, device=device)
+        self.counts = torch.zeros(COUNTS, dtype=torch.int64, device=device)  # accumulated by the kernels
+        self._row_room = 0
+        self._plan: dict[str, torch.Tensor] = {}
+        self._gathered = torch.empty(0, dtype=torch.int64, device=device)
 
-    def _reserve(self, rows: int, entries: int, dtype: torch.dtype) -> None:
-        if rows > self._rows:
-            self._rows = rows
-            self.new_indptr = torch.empty(rows + 1, dtype=torch.int32, device=self.device)
-            self.lens = torch.empty(rows, dtype=torch.int32, device=self.device)
-            self.table = torch.empty(rows, self.width, dtype=torch.int32, device=self.device)
-        entries = max(entries, 1)  # the device buffer is never empty
-        if entries > self._out.shape[0] or dtype != self._out.dtype:
-            self._out = torch.empty(max(entries, self._out.shape[0]), dtype=dtype, device=self.device)
+    def _room_for(self, rows: int, entries: int, slot_dtype: torch.dtype) -> None:
+        if rows > self._row_room:
+            self._row_room = _capacity(rows)
+            n, dev = self._row_room, self.device
+            self._plan = {
+                "indptr": torch.empty(n + 1, dtype=torch.int32, device=dev),
+                "lens": torch.empty(n, dtype=torch.int32, device=dev),
+                "table": torch.empty(n, self.width, dtype=torch.int32, device=dev),
+            }
+        if entries > self._gathered.numel() or slot_dtype != self._gathered.dtype:
+            self._gathered = torch.empty(_capacity(max(entries, self._gathered.numel())), dtype=slot_dtype,
+                                         device=self.device)
 
     def compact(
         self,
@@ -55,27 +68,34 @@ class SlotCompactor:
         n_rows: int,
         entries: int,
     ) -> torch.Tensor:
-        """Rewrite ``indptr[:n_rows + 1]`` and ``slots[:entries]`` in place to the view, and return the new lengths.
+        """The view of one decode batch, written over the engine's list: ``indptr[:n_rows + 1]`` and
+        ``slots[:entries]`` are rewritten in place on the stream, and the rows' new token counts are
+        returned (a device view of this object's scratch, valid until the next call).
 
-        ``keep`` is the bool ``[rows, width]`` policy of the view, ``audit`` the uint8 rows audited in this step
-        (or ``None``), and ``entries`` the length of the engine's list, ``indptr[n_rows]``, which the host knows.
-        Entries of ``slots`` past the new list keep their old values."""
+        ``keep`` bool / uint8 ``[rows, width]``: the committed blocks of each row; ``audit`` (uint8 /
+        bool per row, or None): the rows read whole for this step's audit; ``active``: the lease holds;
+        rows from ``n_real`` on are a graph's padding and read whole; ``entries`` = ``indptr[n_rows]``,
+        which the host knows.  Entries of ``slots`` past the new list keep what they held."""
         if indptr.dtype != torch.int32 or indptr.stride(0) != 1:
-            raise ValueError("indptr must be contiguous int32")
+            raise ValueError("indptr must be a contiguous int32 vector")
         if slots.dtype not in (torch.int32, torch.int64) or slots.stride(0) != 1:
-            raise ValueError("slots must be contiguous int32 or int64")
+            raise ValueError("slots must be a contiguous int32 or int64 vector")
         if keep.dtype not in (torch.bool, torch.uint8) or keep.dim() != 2 or keep.stride(1) != 1:
-            raise ValueError("keep must be a bool [rows, width] mask with contiguous rows")
-        if keep.shape[1] < self.width and n_rows > 0:
-            raise ValueError(f"keep has {keep.shape[1]} columns, the view is {self.width} blocks wide")
+            raise ValueError("keep must be a [rows, width] bool / uint8 mask with contiguous rows")
+        if n_rows > 0 and keep.shape[1] < self.width:
+            raise ValueError(f"keep has {keep.shape[1]} blocks per row, the view {self.width}")
         if audit is not None and (audit.dtype not in (torch.bool, torch.uint8) or audit.stride(0) != 1):
-            raise ValueError("audit must be a contiguous uint8 / bool vector")
-        self._reserve(max(n_rows, 1), entries, slots.dtype)
+            raise ValueError("audit must be a contiguous bool / uint8 vector")
+        for name, t in (("indptr", indptr), ("slots", slots), ("keep", keep), ("audit", audit)):
+            if t is not None and not t.is_cuda:
+                raise ValueError(f"{name} must be a device tensor")
+        self._room_for(max(n_rows, 1), max(entries, 1), slots.dtype)
+        plan = self._plan
         ekv_hip.call(
             "ekv_compact_slots",
             indptr.data_ptr(), slots.data_ptr(), slots.element_size(), keep.data_ptr(), keep.stride(0),
             ekv_hip.ptr(audit), int(bool(active)), int(n_real), int(n_rows), self.width, self.block_tokens,
-            int(entries), self.new_indptr.data_ptr(), self.lens.data_ptr(), self.table.data_ptr(),
-            self.table.stride(0), self._out.data_ptr(), self.counts.data_ptr(), 1, ekv_hip.stream_handle(),
+            int(entries), plan["indptr"].data_ptr(), plan["lens"].data_ptr(), plan["table"].data_ptr(),
+            plan["table"].stride(0), self._gathered.data_ptr(), self.counts.data_ptr(), 1, ekv_hip.stream_handle(),
         )
-        return self.lens[:n_rows]
+        return plan["lens"][:n_rows]
