@@ -41,18 +41,17 @@ class SlotCompactor:
         self.width, self.block_tokens, self.device = width, block_tokens, device
         self.counts = torch.zeros(COUNTS, dtype=torch.int64, device=device)  # accumulated by the kernels
         self._row_room = 0
-        self._plan: dict[str, torch.Tensor] = {}
+        # the plan of the last call, per row: new offsets, new token counts, kept block ids
+        self.new_indptr = self.lens = self.table = torch.empty(0, dtype=torch.int32, device=device)
         self._gathered = torch.empty(0, dtype=torch.int64, device=device)
 
     def _room_for(self, rows: int, entries: int, slot_dtype: torch.dtype) -> None:
         if rows > self._row_room:
             self._row_room = _capacity(rows)
             n, dev = self._row_room, self.device
-            self._plan = {
-                "indptr": torch.empty(n + 1, dtype=torch.int32, device=dev),
-                "lens": torch.empty(n, dtype=torch.int32, device=dev),
-                "table": torch.empty(n, self.width, dtype=torch.int32, device=dev),
-            }
+            self.new_indptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+            self.lens = torch.empty(n, dtype=torch.int32, device=dev)
+            self.table = torch.empty(n, self.width, dtype=torch.int32, device=dev)
         if entries > self._gathered.numel() or slot_dtype != self._gathered.dtype:
             self._gathered = torch.empty(_capacity(max(entries, self._gathered.numel())), dtype=slot_dtype,
                                          device=self.device)
@@ -90,12 +89,11 @@ class SlotCompactor:
             if t is not None and not t.is_cuda:
                 raise ValueError(f"{name} must be a device tensor")
         self._room_for(max(n_rows, 1), max(entries, 1), slots.dtype)
-        plan = self._plan
         ekv_hip.call(
             "ekv_compact_slots",
             indptr.data_ptr(), slots.data_ptr(), slots.element_size(), keep.data_ptr(), keep.stride(0),
             ekv_hip.ptr(audit), int(bool(active)), int(n_real), int(n_rows), self.width, self.block_tokens,
-            int(entries), plan["indptr"].data_ptr(), plan["lens"].data_ptr(), plan["table"].data_ptr(),
-            plan["table"].stride(0), self._gathered.data_ptr(), self.counts.data_ptr(), 1, ekv_hip.stream_handle(),
+            int(entries), self.new_indptr.data_ptr(), self.lens.data_ptr(), self.table.data_ptr(),
+            self.table.stride(0), self._gathered.data_ptr(), self.counts.data_ptr(), 1, ekv_hip.stream_handle(),
         )
-        return plan["lens"][:n_rows]
+        return self.lens[:n_rows]
