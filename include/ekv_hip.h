@@ -160,6 +160,25 @@ int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_l
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * ekv_tile_shares_ws without a workspace argument and without allocating: the split form's
+ * partials go to a scratch array of EKV_TILE_SHARES_SCRATCH_BYTES that the library holds on every
+ * device it runs on, from the first call on that device until the process ends.  The same
+ * kernels, so the same shares as ekv_tile_shares_ws, bit for bit.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * A call whose ekv_tile_shares_workspace(nrows, width, layers) exceeds the scratch is refused
+ * with EKV_EINVAL (e.g. 128 rows x 512 blocks x 32 layers need 8.4 MB and fit).  Every call on one
+ * device uses that device's one scratch: calls that overlap on one device (two streams, two
+ * threads, two graphs replayed at once) race and must be ordered by the caller.
+ */
+#define EKV_TILE_SHARES_SCRATCH_BYTES (16u << 20)
+int ekv_tile_shares_noalloc(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
+                            int64_t lse_row_stride, int32_t layers, int32_t cells, int32_t width,
+                            const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
+                            int32_t tile_blocks, int32_t aggregate, float *shares, int64_t shares_stride,
+                            void *stream);
+
+/*
  * The same normalisation from u values already formed, u[layer][row][block][cell]
  * (normalize_tile_lse's own input, observe/tile_shares.py:58-103).
  */

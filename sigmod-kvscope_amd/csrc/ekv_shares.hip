@@ -32,9 +32,16 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "ekv_common.hpp"
+
+// The scratch of ekv_tile_shares_noalloc: the split form's partials and contributor counts, held
+// by the library on every device it runs on until the process ends.  Host code never passes this
+// name to a kernel (on the host it is only a stand-in for the symbol): it uses the device address
+// that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[EKV_TILE_SHARES_SCRATCH_BYTES];
 
 namespace ekv {
 namespace shares {
@@ -689,6 +696,69 @@ extern "C" int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, in
   p.shares = shares;
   p.shares_stride = shares_stride;
   return shares::launch(p, nrows, workspace, workspace_bytes, stream);
+}
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+void *g_scratch_ptr[kMaxScratchDevices] = {nullptr};
+std::mutex g_scratch_lock;
+
+// The current device's copy of `scratch`, looked up once per device with that device current.
+int device_scratch(void **out) {
+  int device = -1;
+  int rc = check_hip(hipGetDevice(&device), "hipGetDevice");
+  if (rc != EKV_OK) return rc;
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(EKV_EUNSUPPORTED, "ekv_tile_shares_noalloc: device %d (at most %d devices)", device,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_ptr[device] == nullptr) {
+    void *ptr = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc != EKV_OK) return rc;
+    if (ptr == nullptr) return fail(EKV_ELAUNCH, "ekv_tile_shares_noalloc: no device address for the scratch");
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return EKV_OK;
+}
+
+}  // namespace
+
+extern "C" int ekv_tile_shares_noalloc(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
+                                       int64_t lse_row_stride, int32_t layers, int32_t cells, int32_t width,
+                                       const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
+                                       int32_t tile_blocks, int32_t aggregate, float *shares,
+                                       int64_t shares_stride, void *stream) {
+  if (lse == nullptr || shares == nullptr) return fail(EKV_EINVAL, "ekv_tile_shares_noalloc: null pointer");
+  if (nrows < 0 || width < 1 || layers < 1)
+    return fail(EKV_EINVAL, "ekv_tile_shares_noalloc: rows %d, width %d, layers %d", nrows, width, layers);
+  const size_t need = shares::split_workspace(nrows, width, layers);
+  if (need > (size_t)EKV_TILE_SHARES_SCRATCH_BYTES)
+    return fail(EKV_EINVAL,
+                "ekv_tile_shares_noalloc: %d rows x %d blocks x %d layers need %zu bytes of scratch, the "
+                "library holds %zu per device (use ekv_tile_shares_ws with a workspace)",
+                nrows, width, layers, need, (size_t)EKV_TILE_SHARES_SCRATCH_BYTES);
+  void *ws = nullptr;
+  const int rc = device_scratch(&ws);
+  if (rc != EKV_OK) return rc;
+  shares::Params p{};
+  p.m = lse;
+  p.l = lse + lse_plane_stride;
+  p.layer_stride = lse_layer_stride;
+  p.row_stride = lse_row_stride;
+  p.layers = layers;
+  p.cells = cells;
+  p.width = width;
+  p.row_ids = row_ids;
+  p.row_blocks = row_blocks;
+  p.tile_blocks = tile_blocks;
+  p.aggregate = aggregate;
+  p.from_u = 0;
+  p.shares = shares;
+  p.shares_stride = shares_stride;
+  return shares::launch(p, nrows, ws, (size_t)EKV_TILE_SHARES_SCRATCH_BYTES, stream);
 }
 
 extern "C" int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row_stride,

@@ -60,6 +60,7 @@ _SIGNATURES: dict[str, list] = {
     "ekv_tile_shares": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_tile_shares_workspace": [_i32, _i32, _i32],
     "ekv_tile_shares_ws": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _sz, _p],
+    "ekv_tile_shares_noalloc": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_normalize_tile_lse": [_p, _i64, _i64, _i32, _i32, _i32, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_rank_uniform": [
         _p, _i64, _p, _p, _p, _i64, _p, _i32, _p, _i64, _i32, _i32, _f64, _i64, _p, _i64, _p, _p,

@@ -43,7 +43,7 @@ def test_argument_errors_map_to_value_error():
     assert raised and "null" in raised
 
 
-COMPUTE = ("ekv_audit_tile_lse", "ekv_tile_shares", "ekv_tile_shares_ws", "ekv_normalize_tile_lse",
+COMPUTE = ("ekv_audit_tile_lse", "ekv_tile_shares", "ekv_tile_shares_ws", "ekv_tile_shares_noalloc", "ekv_normalize_tile_lse",
            "ekv_rank_uniform", "ekv_rank_uniform_ws", "ekv_rank_uniform_view", "ekv_rank_sum", "ekv_rank_maxmin", "ekv_compact_view",
            "ekv_build_view", "ekv_compact_slots")
 
