@@ -6,14 +6,17 @@ is one decode step's worth of the path: the audit kernel after each of the 32 la
 KV group L mod 8 of its own cache; the caches rotate over 4 distinct pools so that the 144 MB a
 launch reads is never served by the 256 MB Infinity Cache), the share normalisation over the 32
 layers, the uniform ranking at budget 0.5 (first block and 4 newest pinned) and the block-table
-view build.  The step is captured once into a HIP graph and replayed (the launches are identical
-every step; the audit flag lives on the device).
+view build.  The audits read a step plan (each audit workgroup's tiles, built once per step from
+the view buffers by ekv_audit_plan, as RecordingPlane.record builds it at the step's first layer).
+The step is captured once into a HIP graph and replayed (the launches are identical every step;
+the audit flag lives on the device).
 
 value = audited KV bytes (algorithmic, below) per step / step time.  Per audit launch:
   B = sum_r L_r*d*2 (keys) + sum_r n_r*4 (table) + R*G*d*2 (queries) + R*8 (lengths, token)
       + 2*sum_r n_r*G*4 (m and l cells written)
 roofline.achieved = B / the mean duration of an audit launch, timed with HIP events on the launch
-stream.  The CPU baseline is the oracle's PyTorch-CPU form of the audit on a bounded sample.
+stream.  The CPU baseline is the reference's CPU path restated by the oracle (PyTorch-CPU audit,
+NumPy normalisation, ranking and compaction) on the same step, each stage the median of 5 runs.
 
 Only one GPU is used: ``--gpus N`` with N > 1 exits with a message.
 """
@@ -43,7 +46,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--cpu-repeats", type=int, default=5, help="timed repetitions of each CPU-baseline stage")
     ap.add_argument("--chunk-tiles", type=int, default=0)
     ap.add_argument("--profile-only", action="store_true", help="run the graph replays only (for rocprof)")
     ap.add_argument("--objectives-only", action="store_true",
@@ -104,8 +107,10 @@ def other_audit_shapes() -> dict:
     plane.select(np.ones(b3.rows, bool), np.arange(b3.rows))
     plane.set(True)
     t3, l3 = torch.from_numpy(b3.table).cuda(), torch.from_numpy(b3.lens).cuda()
+    plane.plan(t3, l3)  # the step plan the launches share
     us = graph_launch_us(lambda s: [plane.launch(layer, t3, l3, q3[layer], pools[layer % 2][:, 0],
-                                                 b3.head_dim ** -0.5, stream=s) for layer in range(8)], 8, 10)
+                                                 b3.head_dim ** -0.5, planned=True, stream=s) for layer in range(8)],
+                         8, 10)
     bytes3 = audit_bytes(b3)
     out["skewed_long_context_bf16"] = {"bytes_per_launch": bytes3, "us": round(us, 2),
                                        "gbs": round(bytes3 / us / 1e3, 1), "frac": round(bytes3 / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -122,8 +127,9 @@ def other_audit_shapes() -> dict:
     plane.set(True)
     t5, l5 = torch.from_numpy(b5.table).cuda(), torch.from_numpy(b5.lens).cuda()
     k_scale = b5.extra["k_scale"]
+    plane.plan(t5, l5)
     us = graph_launch_us(lambda s: [plane.launch(layer, t5, l5, q5[layer], pools[layer % 2][:, 0],
-                                                 b5.head_dim ** -0.5, k_scale=k_scale, stream=s)
+                                                 b5.head_dim ** -0.5, k_scale=k_scale, planned=True, stream=s)
                                     for layer in range(LAYERS)], LAYERS, 5)
     bytes5 = audit_bytes(b5, key_bytes=1)
     out["full_step_fp8_256_rows"] = {"bytes_per_launch": bytes5, "us_per_layer": round(us, 2),
@@ -171,20 +177,13 @@ class Step:
         self.counts = torch.zeros(R, 5, dtype=torch.int64, device=dev)  # per-row view counters
         self.scale = batch.head_dim ** -0.5
 
-    def audit(self, layer: int, stream: int) -> None:
-        b, p = self.batch, self.plane
-        plane_stride, layer_stride, row_stride = p.strides
-        q, keys = self.q[layer], self.keys[layer % POOLS]
-        self.ekv.call(
-            "ekv_audit_tile_lse",
-            q.data_ptr(), self.ekv.BF16, q.stride(0), q.stride(1),
-            keys.data_ptr(), self.ekv.BF16, keys.stride(0), keys.stride(1), keys.stride(2), 1.0,
-            self.table.data_ptr(), self.table.stride(0), self.lens.data_ptr(), p._token.data_ptr(),
-            p._select.data_ptr(), p._flag_dev,
-            p.lse_address, plane_stride, layer_stride, row_stride, p.cells, 0, 0,
-            self.scale, layer, layer % b.kv_heads, 1, b.group_rows,
-            b.rows, b.width, b.block_size, 2, b.head_dim, self.chunk, stream,
-        )
+    def plan(self, stream: int) -> None:
+        # the step plan: the work list the 32 launches share, built once from the view buffers
+        self.plane.plan(self.table, self.lens, stream=stream)
+
+    def audit(self, layer: int, stream: int, planned: bool = True) -> None:
+        self.plane.launch(layer, self.table, self.lens, self.q[layer], self.keys[layer % POOLS], self.scale,
+                          planned=planned, chunk_tiles=self.chunk, stream=stream)
 
     def shares_rank_view(self, stream: int) -> None:
         b, p = self.batch, self.plane
@@ -209,6 +208,7 @@ class Step:
         )
 
     def run(self, stream: int) -> None:
+        self.plan(stream)
         for layer in range(LAYERS):
             self.audit(layer, stream)
         self.shares_rank_view(stream)
@@ -259,65 +259,97 @@ def profiled_traffic() -> int | None:
     return None
 
 
-def cpu_baseline(step: Step, bound_s: float) -> dict:
-    """The oracle's PyTorch-CPU audit on a bounded sample of the step's layers (all 128 rows each)."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(step: Step, repeats: int) -> dict:
+    """The reference's CPU path on the same step, stage by stage: the oracle's PyTorch-CPU audit of
+    the 32 layer launches (gather through the table, matmul, tile max / sum exp), the float64 NumPy
+    read and normalisation of the 32 layers' records, the controller's uniform ranking (budget 0.5,
+    block 0 and the 4 newest pinned) and the compaction of the block table.  Each stage is timed as
+    the median of ``repeats`` runs after one warm-up, in this process, on the same seeded inputs."""
     import numpy as np
     import torch
 
     from oracle import audit as oracle_audit
-    import workloads
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    b = step.batch
-    planes = oracle_audit.new_planes(LAYERS, b.rows, b.width, b.group_rows)
-    host = {}
-    launches, busy = 0, 0.0
-    while busy < bound_s:  # whole passes over the 32 layers until the bound
-        for layer in range(LAYERS):
-            pool, group = layer % POOLS, layer % b.kv_heads
-            if (pool, group) not in host:
-                keys, table = workloads.host_keys(b, step.pools[pool], heads=[group])
-                host[(pool, group)] = (torch.from_numpy(keys).to(torch.bfloat16), table)
-            keys, table = host[(pool, group)]
-            q = step.q[layer].cpu()
-            t0 = time.perf_counter()
-            oracle_audit.tile_lse_torch(planes, q, keys, table, b.lens, np.arange(b.rows), np.ones(b.rows), layer,
-                                        step.scale, b.block_size, b.group_rows, group, key_head=0)
-            busy += time.perf_counter() - t0
-            launches += 1
-    # the sample's records agree with the device's (same layers)
-    got = step.plane.read_planes()
-    live = ~np.isnan(planes[0])
-    err = float(np.abs(got[0][live] - planes[0][live]).max())
-    # the rest of the step on the host, as the reference runs it: the planes' read and float64
-    # normalisation, the controller's uniform ranking (budget 0.5, 4 recent blocks pinned) and the
-    # compaction of the block table
     from oracle import block_view as oracle_view
     from oracle import controller as oracle_controller
     from oracle import tile_shares as oracle_shares
+    import workloads
 
-    t0 = time.perf_counter()
-    shares = oracle_shares.normalize(oracle_shares.read_rows(got, LAYERS, np.arange(b.rows), 2), b.blocks, 2)
-    t1 = time.perf_counter()
-    keep, _ = oracle_controller.keep_rows(shares.astype(np.float32), b.blocks, np.ones(b.rows), FRACTION, RECENT, 0)
-    t2 = time.perf_counter()
-    oracle_view.compact(b.table, b.lens, keep.astype(bool), b.block_size)
-    t3 = time.perf_counter()
+    # the host's CPU share for this process: its affinity, capped by OMP_NUM_THREADS when set
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, omp) if omp > 0 else affinity
+    torch.set_num_threads(threads)
+    b = step.batch
+    host = {}
+    for layer in range(LAYERS):  # the keys each launch reads, gathered to host memory once (not timed)
+        pool, group = layer % POOLS, layer % b.kv_heads
+        if (pool, group) not in host:
+            keys, table = workloads.host_keys(b, step.pools[pool], heads=[group])
+            host[(pool, group)] = (torch.from_numpy(keys).to(torch.bfloat16), table)
+    queries = [step.q[layer].cpu() for layer in range(LAYERS)]
+    planes = oracle_audit.new_planes(LAYERS, b.rows, b.width, b.group_rows)
+
+    def audit_step() -> None:
+        for layer in range(LAYERS):
+            group = layer % b.kv_heads
+            keys, table = host[(layer % POOLS, group)]
+            oracle_audit.tile_lse_torch(planes, queries[layer], keys, table, b.lens, np.arange(b.rows),
+                                        np.ones(b.rows), layer, step.scale, b.block_size, b.group_rows, group,
+                                        key_head=0)
+
+    got = step.plane.read_planes()
+    shares = None
+    keep = None
+
+    def normalise() -> None:
+        nonlocal shares
+        shares = oracle_shares.normalize(oracle_shares.read_rows(got, LAYERS, np.arange(b.rows), 2), b.blocks, 2)
+
+    def rank() -> None:
+        nonlocal keep
+        keep, _ = oracle_controller.keep_rows(shares.astype(np.float32), b.blocks, np.ones(b.rows), FRACTION,
+                                              RECENT, 0)
+
+    def compact() -> None:
+        oracle_view.compact(b.table, b.lens, keep.astype(bool), b.block_size)
+
+    stages = {}
+    for name, fn in (("audit_32_layers", audit_step), ("normalise_32_layers", normalise), ("uniform_rank", rank),
+                     ("compact", compact)):
+        fn()  # warm-up
+        times = []
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        stages[name] = float(np.median(times))
+    live = ~np.isnan(planes[0])
+    err = float(np.abs(got[0][live] - planes[0][live]).max())  # the CPU records agree with the device's
+    audit_s = stages["audit_32_layers"]
     return {
-        "value": round(launches * audit_bytes(b) / busy / 1e9, 3),
+        "value": round(LAYERS * audit_bytes(b) / audit_s / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{launches // LAYERS} passes over the 32 layer launches of the step (all 128 rows, one KV group "
-                  f"each) with oracle.audit.tile_lse_torch (gather, matmul, tile max / sum exp), {busy:.1f} s of "
-                  f"audit time; tile max agrees with the GPU to {err:.1e}",
-        "step_stages_s": {
-            "audit_32_layers": round(busy / (launches / LAYERS), 4),
-            "normalise_32_layers": round(t1 - t0, 4),
-            "uniform_rank": round(t2 - t1, 4),
-            "compact": round(t3 - t2, 4),
-        },
+        "sample": f"the whole step: the 32 layer launches (all 128 rows, one KV group each) with "
+                  f"oracle.audit.tile_lse_torch, median of {repeats} passes after one warm-up; tile max agrees "
+                  f"with the GPU to {err:.1e}",
+        "cpu_model": cpu_model(),
+        "host_logical_cpus": os.cpu_count(),
+        "affinity_cpus": affinity,
+        "step_stages_s": {k: round(v, 4) for k, v in stages.items()},
+        "step_s": round(sum(stages.values()), 4),
     }
 
 
@@ -449,24 +481,30 @@ def main() -> None:
     wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
 
-    # mean duration of an audit launch: a graph of the 32 launches of a step, replayed and timed
-    # with events on the stream it runs on, divided by the launches
-    audit_graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(audit_graph):
-        capture = int(torch.cuda.current_stream().cuda_stream)
-        for layer in range(LAYERS):
-            step.audit(layer, capture)
-    for _ in range(3):
-        audit_graph.replay()
-    torch.cuda.synchronize()
-    reps = max(10, args.steps // 2)
-    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a0.record(stream)
-    for _ in range(reps):
-        audit_graph.replay()
-    a1.record(stream)
-    torch.cuda.synchronize()
-    audit_ms = a0.elapsed_time(a1) / (reps * LAYERS)
+    # mean duration of an audit launch: a graph of the 32 planned launches of a step (their plan
+    # built by the steps above), replayed and timed with events on the stream it runs on, divided
+    # by the launches; the same for the self-contained kernel, which builds its work list itself
+    def launch_ms(planned: bool) -> float:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            capture = int(torch.cuda.current_stream().cuda_stream)
+            for layer in range(LAYERS):
+                step.audit(layer, capture, planned=planned)
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        reps = max(10, args.steps // 2)
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        a1.record(stream)
+        torch.cuda.synchronize()
+        return a0.elapsed_time(a1) / (reps * LAYERS)
+
+    audit_ms = launch_ms(True)
+    self_contained_ms = launch_ms(False)
+    plan_ms = float(np.median(time_events(lambda: step.plan(handle), 20, stream)))
     # the other stages of the step
     shares_ms = float(np.median(time_events(lambda: step.ekv.call(
         "ekv_tile_shares_ws", step.plane.lse_address, *step.plane.strides, LAYERS, step.plane.cells, batch.width, 0,
@@ -486,9 +524,10 @@ def main() -> None:
     all_plane.attach([step.pools[0].data_ptr()])
     all_plane.select(np.ones(batch.rows, bool), np.arange(batch.rows))
     all_plane.set(True)
+    all_plane.plan(step.table, step.lens)
     all_ms = float(np.median(time_events(
-        lambda: all_plane.launch(0, step.table, step.lens, step.q[0], step.keys[0], step.scale,
-                                 chunk_tiles=args.chunk_tiles), 10, stream)))
+        lambda: all_plane.launch(0, step.table, step.lens, step.q[0], step.keys[0], step.scale, planned=True),
+        10, stream)))
     all_gbs = audit_bytes(batch, batch.kv_heads) / (all_ms * 1e-3) / 1e9
 
     c4_times = view_build_config(handle, stream)
@@ -524,7 +563,7 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "ekv_audit_tile_lse (one KV group)",
+            "kernel": "ekv_audit_tile_lse_planned (tile_lse_planned_kernel, one KV group)",
             "mean_launch_us": round(audit_ms * 1e3, 2),
             "traffic_source": "profiles/tile_lse_llama3_decode_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                               "scaled by a 256 MiB streaming kernel)",
@@ -533,6 +572,8 @@ def main() -> None:
         },
         "stages_us": {
             "audit_per_layer": round(audit_ms * 1e3, 2),
+            "audit_plan_per_step": round(plan_ms * 1e3, 2),
+            "audit_per_layer_self_contained": round(self_contained_ms * 1e3, 2),
             "shares_32_layers": round(shares_ms * 1e3, 2),
             "rank_and_view": round(view_ms * 1e3, 2),
         },
@@ -549,7 +590,7 @@ def main() -> None:
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(step, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(step, max(5, args.cpu_repeats))
     print(json.dumps(out), flush=True)
 
 
