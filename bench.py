@@ -407,6 +407,22 @@ def view_build_config(handle: int, stream) -> dict:
     return out
 
 
+def calibration_copy() -> int:
+    """A plain streaming kernel of known size (one read and one write of 256 MiB, the only negation
+    in a profiling run), to scale the memory counters of the kernels around it; returns its bytes
+    each way."""
+    import torch
+
+    calib_bytes = 256 << 20
+    src = torch.ones(calib_bytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    return calib_bytes
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -421,6 +437,7 @@ def main() -> None:
     torch.cuda.set_device(0)
     if args.objectives_only:
         stream = torch.cuda.current_stream()
+        calibration_copy()
         times = view_build_config(int(stream.cuda_stream), stream)
         print(json.dumps({"objectives_only": True, **{k + "_us": round(v * 1e3, 2) for k, v in times.items()}}))
         return
@@ -453,19 +470,14 @@ def main() -> None:
                 raise RuntimeError("a graph replay differs from the eager step")
 
     if args.profile_only:
-        # a plain streaming kernel of known size first (one read and one write of 256 MiB, the
-        # only negation in the run), to scale the memory counters of the kernels that follow
-        calib_bytes = 256 << 20
-        src = torch.ones(calib_bytes // 4, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+        calib_bytes = calibration_copy()
         for _ in range(args.warmup + args.steps):
             graph.replay()
         torch.cuda.synchronize()
-        print(json.dumps({"profile_only": True, "steps": args.steps, "calibration_copy_bytes": calib_bytes}))
+        # the event-timed mean of one audit launch in the same run, for comparison with the trace
+        launch_us = graph_launch_us(lambda s: [step.audit(layer, s) for layer in range(LAYERS)], LAYERS, 10)
+        print(json.dumps({"profile_only": True, "steps": args.steps, "calibration_copy_bytes": calib_bytes,
+                          "audit_launch_us_events": round(launch_us, 2)}))
         return
 
     for _ in range(args.warmup):

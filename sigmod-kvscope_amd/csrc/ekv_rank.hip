@@ -574,6 +574,355 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   }
 }
 
+
+// The fused ranking and view for float scores without masks (ekv_rank_uniform_view), sized for four
+// 512-thread workgroups per compute unit (at most 64 VGPRs), so that 1024 rows run in one round.
+// Every workgroup takes the controller's budget and its row's largest-remainder quota from every
+// row's counts (32-bit sums: the launch routes rows * width >= 2^31 to rank_kernel), keeps the
+// quota's best open blocks by a radix select, and builds the view on that keep.  Thread t owns the
+// contiguous run of blocks t * PER .. t * PER + PER - 1 of both the scores and the table: both are
+// read with 16-byte loads (the scores' live part only), the keep decisions stay in the thread's
+// registers for the view, and the ties of the select and the view's placement are each one
+// workgroup scan of the threads' counts.  During the select the keys wait in LDS, lane-consecutive
+// (slot i of thread t at i * kThreads + t), which leaves the registers to the table run, and the
+// same LDS then holds the view row being assembled.  The decisions are those of rank_kernel<PER,
+// true>.  (One workgroup computing every row's quota first was slower: 11 us for it against the ~5
+// us of the sums it saves each workgroup.)
+template <int PER>
+__device__ __forceinline__ void load_scores_run(const Params &p, int row, int n, uint32_t (&key)[PER]) {
+  const float *srow = p.scores + (int64_t)row * p.scores_stride;
+  const int b0 = threadIdx.x * PER;
+  if (b0 + PER <= p.width && ((uintptr_t)(srow + b0) & 15) == 0) {
+#pragma unroll
+    for (int g = 0; g < PER / 4; ++g) {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (b0 + 4 * g < n) v = *reinterpret_cast<const uint4 *>(srow + b0 + 4 * g);
+      key[4 * g] = v.x;
+      key[4 * g + 1] = v.y;
+      key[4 * g + 2] = v.z;
+      key[4 * g + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) key[i] = b0 + i < n ? __builtin_bit_cast(uint32_t, srow[b0 + i]) : 0u;
+  }
+}
+
+// Sum of N values over a workgroup of NT threads in one pass (every thread receives the sums).
+template <int NT, int N, class T>
+__device__ __forceinline__ void block_sums_n(T (&v)[N], T (*scratch)[NT / kWave]) {
+  constexpr int NW = NT / kWave;
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    if constexpr (std::is_same<T, int>::value) v[j] = wave_sum_int(v[j]);
+    else v[j] = wave_sum_i64(v[j]);
+    if (lane_id() == 0) scratch[j][wave] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    T s = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += scratch[j][w];
+    v[j] = s;
+  }
+  __syncthreads();
+}
+
+template <int PER>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void rank_view_kernel(
+    const Params p) {
+  // the row's keys during the select, then the view row being assembled
+  __shared__ uint32_t s_row[PER * kThreads];
+  int32_t *s_out = reinterpret_cast<int32_t *>(s_row);
+  __shared__ int s_red[5][kWaves];
+  __shared__ int s_hist[2][256];
+  __shared__ int s_scan[kWaves];
+  __shared__ int s_digit, s_krem, s_whole;
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int W = p.width;
+  const int b0 = tid * PER;
+
+  // ---- the row's counts and token length, every row's counts for the budget, then the row's
+  // live scores ---------------------------------------------------------------------------------
+  const RowInfo me = row_info(p, row);
+  const int L = p.seq_lens[row];
+  constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
+  int open_reg[kRegRows];
+  int t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
+#pragma unroll
+  for (int i = 0; i < kRegRows; ++i) {
+    const int r = tid + i * kThreads;
+    open_reg[i] = -1;  // not taking part
+    if (r < p.rows) {
+      const RowInfo ri = row_info(p, r);
+      if (ri.part) {
+        t5[0] += ri.n;
+        t5[1] += ri.pinned;
+        t5[2] += ri.exist;
+        t5[3] += ri.exist - ri.pinned;
+        t5[4] += 1;
+        open_reg[i] = ri.exist - ri.pinned;
+      }
+    }
+  }
+  const int n = __builtin_amdgcn_readfirstlane(me.n);
+  uint32_t key[PER];  // the raw score bits
+  load_scores_run<PER>(p, row, n, key);
+  for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
+    const RowInfo ri = row_info(p, r);
+    if (!ri.part) continue;
+    t5[0] += ri.n;
+    t5[1] += ri.pinned;
+    t5[2] += ri.exist;
+    t5[3] += ri.exist - ri.pinned;
+    t5[4] += 1;
+  }
+  block_sums_n<kThreads>(t5, s_red);
+  const long long total = t5[0], floor_pins = t5[1], sizes = t5[2], open_total = t5[3], nreq = t5[4];
+  long long budget = p.budget_in;
+  if (budget < 0) {  // controller.py:435-437
+    const long long want = (long long)ceil(p.fraction * (double)total);
+    budget = want > floor_pins ? want : floor_pins;
+  }
+  const bool error = floor_pins > budget && budget < sizes;  // allocation.py:64-65
+  const bool keep_all = budget >= sizes;                      // allocation.py:66-67
+  const long long free_blocks = budget - floor_pins;
+  if (row == 0 && tid == 0 && p.summary != nullptr) {
+    p.summary[0] = budget;
+    p.summary[1] = total;
+    p.summary[2] = floor_pins;
+    p.summary[3] = error ? 1 : 0;
+    p.summary[4] = nreq;
+    p.summary[5] = free_blocks;
+  }
+
+  // open blocks: existing (every block below n) and not pinned (block 0, blocks >= pin_at)
+  uint32_t open_bits = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = b0 + i;
+    open_bits |= (b < n && b != 0 && b < me.pin_at) ? (1u << i) : 0u;
+  }
+  uint32_t keep_bits = ~0u;  // rows without evidence read in full, controller.py:401
+  int32_t entry[PER];        // the table run
+  if (!me.part || error) {
+    load_run<PER>(p, row, entry);
+  } else {
+    // the key mode's counts from the scores in registers; the scores then wait in LDS (slot i of
+    // thread t at i * kThreads + t: lane-consecutive, free of bank conflicts), and the table run
+    // is requested once they are there, to arrive during the select
+    int nan_c = 0, inf_c = 0, pos_c = 0;  // key mode of the row's shares: allocation.py:46-52
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const float s = __builtin_bit_cast(float, key[i]);
+      const bool live = b0 + i < n;
+      nan_c += (live && __builtin_isnan(s)) ? 1 : 0;
+      inf_c += (live && __builtin_isinf(s) && s > 0.0f) ? 1 : 0;
+      pos_c += (live && s > 0.0f) ? 1 : 0;
+      s_row[i * kThreads + tid] = key[i];
+    }
+    // ---- this row's quota: largest remainder in IEEE double, allocation.py:79-86 -------------
+    const long long my_open = me.exist - me.pinned;
+    const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
+    const long long my_floor = (long long)my_exact;
+    const double my_frac = my_exact - (double)my_floor;
+    // [0] floors, [1] rows ahead in the leftover order, [2] [3] counts of the row's blocks in
+    // 16-bit fields: NaN, +inf and positive scores, and open blocks (int sums: the floors add up
+    // to at most the budget)
+    int q4[4] = {0, 0, nan_c + (inf_c << 16), pos_c + ((int)__popc(open_bits) << 16)};
+    if (!keep_all) {
+      auto visit = [&](int r, int open) {
+        const double exact = open_total > 0 ? (double)(free_blocks * open) / (double)open_total : 0.0;
+        const int fl = (int)exact;
+        const double frac = exact - (double)fl;
+        q4[0] += fl;
+        q4[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
+      };
+#pragma unroll
+      for (int i = 0; i < kRegRows; ++i)
+        if (open_reg[i] >= 0) visit(tid + i * kThreads, open_reg[i]);
+      for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
+        const RowInfo ri = row_info(p, r);
+        if (ri.part) visit(r, ri.exist - ri.pinned);
+      }
+    }
+    block_sums_n<kThreads>(q4, s_red);
+    load_run<PER>(p, row, entry);  // after the barriers: with the scores still in flight it would not fit
+    long long quota;
+    if (keep_all) {
+      quota = my_open;
+    } else {
+      const long long leftover = free_blocks - q4[0];
+      quota = my_floor + (q4[1] < leftover ? 1 : 0);
+    }
+    const int has_nan = q4[2] & 0xffff, has_inf = (q4[2] >> 16) & 0xffff, has_pos = q4[3] & 0xffff;
+    const int open_count = (q4[3] >> 16) & 0xffff;
+    const int mode = has_nan ? 0 : (has_inf ? 2 : (has_pos ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
+
+    // keys of the open blocks (order-preserving, larger first), ~0 elsewhere; each thread
+    // rewrites its own slots
+    constexpr uint32_t kClosedKey = ~0u;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t bits = s_row[i * kThreads + tid];
+      const float s = __builtin_bit_cast(float, bits);
+      uint32_t k = kClosedKey;
+      if ((open_bits >> i) & 1u) {
+        if (mode == 1) k = s > 0.0f ? bits : 0u;
+        else if (mode == 2) k = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
+        else k = 0u;
+      }
+      s_row[i * kThreads + tid] = k;
+    }
+    uint32_t open_keep = 0;
+    if (quota >= open_count) {
+      open_keep = ~0u;
+    } else if (quota > 0) {
+      // radix select of the quota-th largest key, 8 bits at a time from the top; the histogram is
+      // double-buffered, and the select stops once the quota ends at the end of a digit's bucket
+      uint32_t prefix = 0, mask = 0;
+      int k_rem = (int)quota;
+      bool whole = false;
+      if (tid < 256) s_hist[0][tid] = 0;
+      __syncthreads();
+#pragma unroll 1
+      for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        int *hist = s_hist[pass & 1];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const uint32_t k = s_row[i * kThreads + tid];
+          if (k != kClosedKey && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1);
+        }
+        if (tid < 256) s_hist[(pass & 1) ^ 1][tid] = 0;
+        __syncthreads();
+        if (wave == 0) {
+          // lane l holds digits 255 - 4l .. 252 - 4l; a scan over the lanes counts the keys above
+          int c[4], s4 = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            c[j] = hist[255 - 4 * lane - j];
+            s4 += c[j];
+          }
+          const int inc = wave_inclusive_scan(s4);
+          int acc = inc - s4;
+          if (acc < k_rem && inc >= k_rem) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              if (acc < k_rem && acc + c[j] >= k_rem) {
+                s_digit = 255 - 4 * lane - j;
+                s_krem = k_rem - acc;
+                s_whole = acc + c[j] == k_rem ? 1 : 0;
+              }
+              acc += c[j];
+            }
+          }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s_digit << shift;
+        mask |= 255u << shift;
+        k_rem = s_krem;
+        whole = __builtin_amdgcn_readfirstlane(s_whole) != 0;
+        if (whole) break;
+      }
+      if (whole) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const uint32_t k = s_row[i * kThreads + tid];
+          open_keep |= (k != kClosedKey && (k & mask) >= prefix) ? (1u << i) : 0u;
+        }
+      } else {
+        // every key above the threshold and the first k_rem equal keys by block index: the equal
+        // keys before a thread's run are one scan of the threads' counts
+        uint32_t eq_bits = 0, above_bits = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const uint32_t k = s_row[i * kThreads + tid];
+          eq_bits |= k == prefix ? (1u << i) : 0u;
+          above_bits |= (k != kClosedKey && k > prefix) ? (1u << i) : 0u;
+        }
+        int eq_total;
+        int before = block_exclusive_scan<kThreads>(__popc(eq_bits), s_scan, eq_total);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const bool eq = (eq_bits >> i) & 1u;
+          const bool kept = ((above_bits >> i) & 1u) || (eq && before < k_rem);
+          before += eq ? 1 : 0;
+          open_keep |= kept ? (1u << i) : 0u;
+        }
+      }
+    }
+    keep_bits = ~open_bits | open_keep;  // past the row, pinned: 1; open: decided
+  }
+  uint8_t *keep_row = p.keep + (int64_t)row * p.keep_stride;
+  if (b0 + PER <= W && ((uintptr_t)(keep_row + b0) & 3) == 0) {
+#pragma unroll
+    for (int g = 0; g < PER / 4; ++g) {
+      const uint32_t k4 = ((keep_bits >> (4 * g)) & 1u) | (((keep_bits >> (4 * g + 1)) & 1u) << 8) |
+                          (((keep_bits >> (4 * g + 2)) & 1u) << 16) | (((keep_bits >> (4 * g + 3)) & 1u) << 24);
+      *reinterpret_cast<uint32_t *>(keep_row + b0 + 4 * g) = k4;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (b0 + i < W) keep_row[b0 + i] = (keep_bits >> i) & 1u;
+  }
+  __syncthreads();  // every key is read before the view row overwrites them
+
+  // ---- compact_block_table (runtime/block_view.py:36-56) of the row on that keep ------------
+  const int bs = p.block_size;
+  const long long n64 = L > 0 ? ((long long)L + bs - 1) / bs : 0;  // block_view.py:49
+  const int nv = n64 > W + 1LL ? W + 1 : (int)n64;
+  uint32_t kept_bits = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = b0 + i;
+    kept_bits |= (b < W && (((keep_bits >> i) & 1u) || b == 0 || b == nv - 1) && b < nv) ? (1u << i) : 0u;
+  }
+  int total_kept;
+  int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int b = b0 + i;
+    if (b >= W) continue;
+    if ((kept_bits >> i) & 1u) s_out[before++] = entry[i];
+    else s_out[total_kept + (b - before)] = entry[i];  // dropped: after the kept ones, in order
+  }
+  __syncthreads();
+  int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
+  if (((uintptr_t)vrow & 15) == 0) {
+    for (int q = tid; 4 * q < W; q += kThreads) {
+      if (4 * q + 3 < W) {
+        *reinterpret_cast<int4 *>(vrow + 4 * q) =
+            make_int4(s_out[4 * q], s_out[4 * q + 1], s_out[4 * q + 2], s_out[4 * q + 3]);
+      } else {
+        for (int b = 4 * q; b < W; ++b) vrow[b] = s_out[b];
+      }
+    }
+  } else {
+    for (int b = tid; b < W; b += kThreads) vrow[b] = s_out[b];
+  }
+  if (tid == 0) {  // block_view.py:53-55
+    const int last = L - (int)(n64 - 1) * bs;
+    const int view_len = n64 > 0 ? (total_kept - 1) * bs + last : 0;
+    p.view_lens[row] = view_len;
+    if (p.view_counts != nullptr) {
+      // DecodeView._count for a live decoding row outside the audit (block_view.py:313-329)
+      const long long read = view_len > 0 ? ((long long)view_len + bs - 1) / bs : 0;
+      long long *c = p.view_counts + 5LL * row;
+      c[0] += read;
+      c[1] += n64;
+      c[3] += view_len == L ? read : 0;
+    }
+  }
+}
+
 }  // namespace rank
 }  // namespace ekv
 
@@ -631,7 +980,15 @@ extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride,
   p.view_counts = (long long *)counts;
   hipStream_t s = (hipStream_t)stream;
   const int per = (width + rank::kThreads - 1) / rank::kThreads;
-  if (per <= 4)
+  // the lean kernel counts blocks in 32 bits; larger batches (and the widest rows) take rank_kernel
+  const bool lean = (int64_t)rows * width < ((int64_t)1 << 31);
+  if (lean && per <= 4)
+    hipLaunchKernelGGL((rank::rank_view_kernel<4>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (lean && per <= 8)
+    hipLaunchKernelGGL((rank::rank_view_kernel<8>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (lean && per <= 16)
+    hipLaunchKernelGGL((rank::rank_view_kernel<16>), dim3(rows), dim3(rank::kThreads), 0, s, p);
+  else if (per <= 4)
     hipLaunchKernelGGL((rank::rank_kernel<4, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);
   else if (per <= 8)
     hipLaunchKernelGGL((rank::rank_kernel<8, true>), dim3(rows), dim3(rank::kThreads), 0, s, p);

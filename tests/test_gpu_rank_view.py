@@ -118,3 +118,36 @@ def test_counters_match_build_view(wide):
                            ("lens", view_lens, lens2), ("counts", counts, counts2)):
             assert torch.equal(g, w), (fraction, name)
     assert int(counts[:, 0].sum()) > 0
+
+
+@pytest.mark.parametrize("width", [6, 2049, 8192])
+def test_special_scores_fused(width):
+    # the key modes of the fused kernel: a NaN score ties every block of its row (index order), a
+    # +inf score puts the row's finite blocks first (tied) and the +inf blocks last, an all-zero or
+    # negative row ties by index, -0 and subnormals rank as values; checked against the two calls
+    # and the oracle's controller rule (observe/controller.py:398-451, observe/allocation.py:46-52)
+    from oracle import controller as oracle_controller
+
+    rng = np.random.default_rng(7 + width)
+    rows, bs, recent = 8, 16, 1
+    scores = rng.random((rows, width), dtype=np.float32)
+    n = np.full(rows, width, np.int32)
+    scores[0, width // 3] = np.nan
+    scores[1, [1, width // 2]] = np.inf
+    scores[2] = 0.0
+    scores[3] = -rng.random(width, dtype=np.float32)
+    scores[4, ::2] = -0.0
+    scores[5, ::3] = np.float32(1e-40)  # subnormal
+    scores[6, 1:] = np.float32(0.5)  # one long tie
+    scores[7, : width // 2] = -np.inf
+    n[7] = max(width - 3, 1)
+    table = rng.integers(0, 1 << 30, size=(rows, width)).astype(np.int32)
+    lens = (n.astype(np.int64) * bs).astype(np.int32)
+    dev = [torch.from_numpy(a).cuda() for a in (scores, n, table, lens)]
+    print(f"width {width}", flush=True)
+    keep, summary, view, view_lens = both(*dev, bs, fraction=0.5, recent_blocks=recent)
+    want_keep, budget = oracle_controller.keep_rows(scores, n, np.ones(rows, bool), 0.5, recent, 0)
+    assert summary[0] == budget
+    assert np.array_equal(keep, want_keep)
+    want_view, want_lens = obv.compact(table, lens, want_keep.astype(bool), bs)
+    assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens)
