@@ -40,10 +40,15 @@ extern "C" {
 #define EKV_F16 1
 #define EKV_BF16 2
 #define EKV_FP8_E4M3 3 /* OCP e4m3fn, dequantised as k_scale * value */
+#define EKV_F64 4      /* float64 shares (ekv_controller_keep) */
 
 /* aggregates of the share normalisation (observe/tile_shares.py:55) */
 #define EKV_AGG_MEAN 0
 #define EKV_AGG_MAX 1
+
+/* objectives of the controller's rule (Settings.objective, observe/controller.py:30) */
+#define EKV_OBJ_SUM 0
+#define EKV_OBJ_MAXMIN 1
 
 const char *ekv_last_error(void);
 int ekv_abi_version(void);
@@ -295,6 +300,32 @@ size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width);
 int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *blocks, const uint8_t *pinned,
                     int64_t pinned_stride, int32_t rows, int32_t width, int64_t budget, uint8_t *keep,
                     int64_t keep_stride, int64_t *summary, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The controller's keep rule under the `sum` or `maxmin` objective: Controller._allocate,
+ * observe/controller.py:398-451, with allocate(..., "sum" | "maxmin").  (The `uniform` objective is
+ * ekv_rank_uniform_ws with the same rows, pins and released blocks.)
+ *
+ * Row r takes part when lengths[r] > cap_above_blocks and evidence[r] != 0 (:402-408).  Its request
+ * is its n = min(lengths[r], width) blocks less the freed ones (released[r][b] != 0; NULL: none),
+ * in order, scored by shares[r][b] (float32 or float64, zero past the row's evidence), weighted by
+ * weights[r] (NULL: 1.0; `sum` only); block 0, blocks >= n - 1 - recent_blocks and blocks >=
+ * audited_blocks[r] (NULL: none) are pinned (:420-424).  The budget is max(pinned, ceil(fraction *
+ * blocks)) over every block of the taking-part rows, freed ones included (:435-437), and it is split
+ * across the requests as ekv_rank_sum / ekv_rank_maxmin split theirs, the requests numbered in row
+ * order.  keep[r][b] (uint8): the request's decision at a remaining block, 0 at a freed block, 1
+ * past the row and in every row that takes no part.  summary (int64[6], may be NULL): budget, blocks
+ * of the requests, pinned blocks, status, requests, free.  workspace:
+ * ekv_controller_keep_workspace(objective, rows, width) bytes the call may overwrite.  rows at most
+ * 65535 (`sum`) or 8192 (`maxmin`), width at most 12288.
+ */
+size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width);
+int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,
+                        const int32_t *lengths, const uint8_t *evidence, const int32_t *audited_blocks,
+                        const uint8_t *released, int64_t released_stride, const double *weights, int32_t rows,
+                        int32_t width, int32_t recent_blocks, int32_t cap_above_blocks, double fraction,
+                        uint8_t *keep, int64_t keep_stride, int64_t *summary, void *workspace,
+                        size_t workspace_bytes, void *stream);
 
 /*
  * compact_block_table (runtime/block_view.py:36-56).

@@ -76,6 +76,16 @@ struct Params {
   int64_t *summary;
   State *state;
   RowStat *row_stat;
+  // the controller's rule (ekv_controller_keep): budget < 0 takes max(pinned, ceil(fraction * blocks))
+  // over every block of the measured rows, from `ctl`, which also holds the request count
+  double fraction;
+  const struct CtlHeader *ctl;
+};
+
+// Written by ctl_plan_kernel: the measured rows' blocks (freed ones included) and their count.
+struct CtlHeader {
+  long long blocks;
+  long long requests;
 };
 
 __device__ __forceinline__ int row_blocks(const Params &p, int r) { return min(max(p.blocks[r], 0), p.width); }
@@ -197,8 +207,14 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
   s->must = v[0];
   s->sizes = v[1];
   s->open_total = v[2];
-  s->requests = p.rows;
-  const long long must = v[0], sizes = v[1], budget = p.budget;
+  const long long requests = p.ctl != nullptr ? p.ctl->requests : p.rows;
+  s->requests = requests;
+  const long long must = v[0], sizes = v[1];
+  long long budget = p.budget;
+  if (budget < 0) {  // controller.py:435-437
+    const long long want = (long long)ceil(p.fraction * (double)p.ctl->blocks);
+    budget = want > must ? want : must;
+  }
   s->budget = budget;
   s->error = (must > budget && budget < sizes) ? 1 : 0;
   const long long free_blocks = budget - must;
@@ -217,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
     p.summary[1] = sizes;
     p.summary[2] = must;
     p.summary[3] = s->error;
-    p.summary[4] = p.rows;
+    p.summary[4] = requests;
     p.summary[5] = free_blocks;
   }
 }
@@ -895,6 +911,138 @@ __global__ __launch_bounds__(kThreads) void mm_keep_kernel(const MaxminParams m)
   for (int i = threadIdx.x; i < counts; i += kThreads) krow[m.vals_out[row0 + i]] = 1;
 }
 
+// ---------------------------------------------------------------------------------------
+// The controller's rule for `sum` and `maxmin` (Controller._allocate, observe/controller.py:398-451):
+// a row takes part when it is longer than cap_above_blocks and has evidence; its request holds its
+// existing blocks in order (freed blocks leave it, :425-431), block 0, the recent_blocks newest and
+// the blocks from its audited length on being pinned (:420-424); the budget is
+// max(pinned, ceil(fraction * blocks)) over every block of the taking-part rows, freed or not
+// (:435-437); rows that take no part, and positions past a row, keep every block.  The requests
+// are numbered in row order over the taking-part rows only -- `maxmin` shifts request r's running
+// totals by 2r in its one search -- and the rows that take no part become empty requests after
+// them, which change nothing.
+// ---------------------------------------------------------------------------------------
+struct CtlParams {
+  const void *shares;
+  int32_t shares_f64;  // float64 shares (else float32)
+  int64_t shares_stride;
+  const int32_t *lengths;
+  const uint8_t *evidence;
+  const int32_t *audited;  // may be null
+  const uint8_t *released;  // may be null
+  int64_t released_stride;
+  const double *weights;  // may be null
+  int32_t rows, width, recent, cap;
+  CtlHeader *header;
+  int32_t *row_slot;  // request of each row, -1: takes no part
+  int32_t *slot_row;
+  // the requests as the allocation reads them: [rows][width] scores and pins, block counts, weights
+  double *req_scores;
+  uint8_t *req_pinned;
+  int32_t *req_blocks;
+  double *req_weights;
+  uint8_t *req_keep;
+};
+
+constexpr int kCtlPlanThreads = 1024;
+
+__device__ __forceinline__ int ctl_blocks(const CtlParams &c, int r) { return min(max(c.lengths[r], 0), c.width); }
+__device__ __forceinline__ bool ctl_takes_part(const CtlParams &c, int r) {
+  return c.lengths[r] > c.cap && c.evidence[r] != 0;  // controller.py:402-408
+}
+__device__ __forceinline__ bool ctl_exists(const CtlParams &c, int r, int b) {
+  return c.released == nullptr || c.released[(int64_t)r * c.released_stride + b] == 0;
+}
+
+// One workgroup: which rows take part, their requests' numbers, and their blocks.
+__global__ __launch_bounds__(kCtlPlanThreads) void ctl_plan_kernel(const CtlParams c) {
+  __shared__ int s_scan[kCtlPlanThreads / kWave];
+  __shared__ long long s_sum[kCtlPlanThreads / kWave];
+  long long blocks = 0;
+  int before = 0;
+  for (int r0 = 0; r0 < c.rows; r0 += kCtlPlanThreads) {
+    const int r = r0 + threadIdx.x;
+    const bool part = r < c.rows && ctl_takes_part(c, r);
+    int chunk;
+    const int slot = before + block_exclusive_scan<kCtlPlanThreads>(part ? 1 : 0, s_scan, chunk);
+    if (r < c.rows) c.row_slot[r] = part ? slot : -1;
+    if (part) {
+      c.slot_row[slot] = r;
+      blocks += ctl_blocks(c, r);
+    }
+    before += chunk;
+  }
+  blocks = block_sum<kCtlPlanThreads>(blocks, s_sum);
+  if (threadIdx.x == 0) {
+    c.header->blocks = blocks;
+    c.header->requests = before;
+  }
+}
+
+// One workgroup per request slot: the request's existing blocks in order, with their scores
+// (float64) and pins; the slots after the last request are empty.
+__global__ __launch_bounds__(kThreads) void ctl_compact_kernel(const CtlParams c) {
+  __shared__ int s_scan[kThreads / kWave];
+  const int j = blockIdx.x;
+  if (j >= c.header->requests) {
+    if (threadIdx.x == 0) {
+      c.req_blocks[j] = 0;
+      c.req_weights[j] = 1.0;
+    }
+    return;
+  }
+  const int r = c.slot_row[j];
+  const int n = ctl_blocks(c, r);
+  const int recent_at = max(0, n - 1 - c.recent);
+  const int audited_at = c.audited != nullptr ? min(max(c.audited[r], 0), n) : n;  // controller.py:424
+  double *srow = c.req_scores + (int64_t)j * c.width;
+  uint8_t *prow = c.req_pinned + (int64_t)j * c.width;
+  int base = 0;
+  for (int b0 = 0; b0 < n; b0 += kThreads) {
+    const int b = b0 + threadIdx.x;
+    const bool e = b < n && ctl_exists(c, r, b);
+    int chunk;
+    const int at = base + block_exclusive_scan<kThreads>(e ? 1 : 0, s_scan, chunk);
+    if (e) {
+      double s;
+      if (c.shares_f64) s = reinterpret_cast<const double *>(c.shares)[(int64_t)r * c.shares_stride + b];
+      else s = (double)reinterpret_cast<const float *>(c.shares)[(int64_t)r * c.shares_stride + b];
+      srow[at] = s;
+      prow[at] = (b == 0 || b >= recent_at || b >= audited_at) ? 1 : 0;
+    }
+    base += chunk;
+  }
+  if (threadIdx.x == 0) {
+    c.req_blocks[j] = base;
+    c.req_weights[j] = c.weights != nullptr ? c.weights[r] : 1.0;
+  }
+}
+
+// One workgroup per row: the request's keep back at the row's positions (a freed block 0, a
+// position past the row 1, a row that takes no part all 1).
+__global__ __launch_bounds__(kThreads) void ctl_scatter_kernel(const CtlParams c, uint8_t *keep, int64_t keep_stride) {
+  __shared__ int s_scan[kThreads / kWave];
+  const int r = blockIdx.x;
+  const int j = c.row_slot[r];
+  uint8_t *krow = keep + (int64_t)r * keep_stride;
+  const int n = j >= 0 ? ctl_blocks(c, r) : 0;
+  for (int b = n + threadIdx.x; b < c.width; b += kThreads) krow[b] = 1;
+  if (j < 0) return;
+  const uint8_t *qrow = c.req_keep + (int64_t)j * c.width;
+  int base = 0;
+  for (int b0 = 0; b0 < n; b0 += kThreads) {
+    const int b = b0 + threadIdx.x;
+    const bool e = b < n && ctl_exists(c, r, b);
+    int chunk;
+    const int at = base + block_exclusive_scan<kThreads>(e ? 1 : 0, s_scan, chunk);
+    if (b < n) krow[b] = e ? qrow[at] : 0;
+    base += chunk;
+  }
+}
+
+int launch_sum(Params p, hipStream_t s);
+int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s);
+
 }  // namespace alloc
 }  // namespace ekv
 
@@ -934,7 +1082,15 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   const uintptr_t base = ((uintptr_t)workspace + 255) & ~(uintptr_t)255;
   p.state = (alloc::State *)base;
   p.row_stat = (alloc::RowStat *)(base + sizeof(alloc::State));
-  hipStream_t s = (hipStream_t)stream;
+  return alloc::launch_sum(p, (hipStream_t)stream);
+}
+
+namespace ekv {
+namespace alloc {
+
+// The `sum` pipeline on prepared parameters (state and row statistics in place).
+int launch_sum(Params p, hipStream_t s) {
+  const int rows = p.rows;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
@@ -955,6 +1111,9 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
 }
+
+}  // namespace alloc
+}  // namespace ekv
 
 namespace {
 
@@ -1033,7 +1192,15 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   m.order = (int32_t *)(base + l.order);
   m.level_count = (int32_t *)(base + l.level_count);
   m.level_pos = (uint16_t *)(base + l.level_pos);
-  hipStream_t s = (hipStream_t)stream;
+  return alloc::launch_maxmin(m, rows, width, (hipStream_t)stream);
+}
+
+namespace ekv {
+namespace alloc {
+
+// The `maxmin` pipeline on prepared parameters (every workspace pointer in place).
+int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
+  Params &p = m.p;
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
@@ -1068,4 +1235,145 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
     hipLaunchKernelGGL(alloc::mm_bisect_kernel<8>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
   return check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
+}
+
+}  // namespace alloc
+}  // namespace ekv
+
+namespace {
+
+// Workspace of ekv_controller_keep: the plan, the requests in allocation form, then the objective's
+// own workspace.
+struct CtlLayout {
+  size_t header, row_slot, slot_row, req_blocks, req_weights, req_scores, req_pinned, req_keep, inner, total;
+};
+
+CtlLayout ctl_layout(int objective, int32_t rows, int32_t width) {
+  CtlLayout l{};
+  const size_t cells = (size_t)rows * (size_t)width;
+  size_t at = 0;
+  l.header = at;
+  at = align256(at + sizeof(alloc::CtlHeader));
+  l.row_slot = at;
+  at = align256(at + (size_t)rows * 4);
+  l.slot_row = at;
+  at = align256(at + (size_t)rows * 4);
+  l.req_blocks = at;
+  at = align256(at + (size_t)rows * 4);
+  l.req_weights = at;
+  at = align256(at + (size_t)rows * 8);
+  l.req_scores = at;
+  at = align256(at + cells * 8);
+  l.req_pinned = at;
+  at = align256(at + cells);
+  l.req_keep = at;
+  at = align256(at + cells);
+  l.inner = at;
+  at += objective == EKV_OBJ_SUM ? ekv_rank_sum_workspace(rows) : ekv_rank_maxmin_workspace(rows, width);
+  l.total = at + 256;  // + 256: the base may be realigned
+  return l;
+}
+
+}  // namespace
+
+extern "C" size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width) {
+  if ((objective != EKV_OBJ_SUM && objective != EKV_OBJ_MAXMIN) || rows <= 0 || width <= 0) return 256;
+  return ctl_layout(objective, rows, width).total;
+}
+
+extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,
+                                   const int32_t *lengths, const uint8_t *evidence, const int32_t *audited_blocks,
+                                   const uint8_t *released, int64_t released_stride, const double *weights,
+                                   int32_t rows, int32_t width, int32_t recent_blocks, int32_t cap_above_blocks,
+                                   double fraction, uint8_t *keep, int64_t keep_stride, int64_t *summary,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+  if (shares == nullptr || lengths == nullptr || evidence == nullptr || keep == nullptr || workspace == nullptr)
+    return fail(EKV_EINVAL, "ekv_controller_keep: null pointer");
+  if (objective != EKV_OBJ_SUM && objective != EKV_OBJ_MAXMIN)
+    return fail(EKV_EINVAL, "ekv_controller_keep: objective %d is neither sum (%d) nor maxmin (%d)", objective,
+                EKV_OBJ_SUM, EKV_OBJ_MAXMIN);
+  if (objective == EKV_OBJ_MAXMIN && weights != nullptr)
+    return fail(EKV_EINVAL, "ekv_controller_keep: the maxmin objective does not use request weights");
+  if (shares_dtype != EKV_F32 && shares_dtype != EKV_F64)
+    return fail(EKV_EUNSUPPORTED, "ekv_controller_keep: shares of dtype %d (float32 or float64)", shares_dtype);
+  const int max_rows = objective == EKV_OBJ_SUM ? alloc::kMaxRows : alloc::kMaxMaxminRows;
+  if (rows < 0 || rows > max_rows || width < 1 || width > alloc::kMaxWidth)
+    return fail(EKV_EINVAL, "ekv_controller_keep: rows %d (max %d), width %d (max %d)", rows, max_rows, width,
+                alloc::kMaxWidth);
+  if (recent_blocks < 0 || cap_above_blocks < 0)
+    return fail(EKV_EINVAL, "ekv_controller_keep: recent_blocks %d, cap_above_blocks %d", recent_blocks,
+                cap_above_blocks);
+  if (!(fraction > 0.0 && fraction <= 1.0))
+    return fail(EKV_EINVAL, "ekv_controller_keep: the budget fraction %g is not in (0, 1]", fraction);
+  if (rows == 0) return EKV_OK;
+  const CtlLayout l = ctl_layout(objective, rows, width);
+  if (workspace_bytes < l.total)
+    return fail(EKV_EINVAL, "ekv_controller_keep: a workspace of %zu bytes is below the %zu needed", workspace_bytes,
+                l.total);
+  const uintptr_t base = ((uintptr_t)workspace + 255) & ~(uintptr_t)255;
+  alloc::CtlParams c{};
+  c.shares = shares;
+  c.shares_f64 = shares_dtype == EKV_F64 ? 1 : 0;
+  c.shares_stride = shares_stride;
+  c.lengths = lengths;
+  c.evidence = evidence;
+  c.audited = audited_blocks;
+  c.released = released;
+  c.released_stride = released_stride;
+  c.weights = weights;
+  c.rows = rows;
+  c.width = width;
+  c.recent = recent_blocks;
+  c.cap = cap_above_blocks;
+  c.header = (alloc::CtlHeader *)(base + l.header);
+  c.row_slot = (int32_t *)(base + l.row_slot);
+  c.slot_row = (int32_t *)(base + l.slot_row);
+  c.req_blocks = (int32_t *)(base + l.req_blocks);
+  c.req_weights = (double *)(base + l.req_weights);
+  c.req_scores = (double *)(base + l.req_scores);
+  c.req_pinned = (uint8_t *)(base + l.req_pinned);
+  c.req_keep = (uint8_t *)(base + l.req_keep);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(alloc::ctl_plan_kernel, dim3(1), dim3(alloc::kCtlPlanThreads), 0, s, c);
+  hipLaunchKernelGGL(alloc::ctl_compact_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, c);
+  int rc = check_hip(hipGetLastError(), "ekv_controller_keep launch");
+  if (rc != EKV_OK) return rc;
+  // the objective over the requests (rows that take no part: empty requests after the others)
+  alloc::Params p{};
+  p.scores = c.req_scores;
+  p.scores_stride = width;
+  p.blocks = c.req_blocks;
+  p.weights = objective == EKV_OBJ_SUM ? c.req_weights : nullptr;
+  p.pinned = c.req_pinned;
+  p.pinned_stride = width;
+  p.rows = rows;
+  p.width = width;
+  p.budget = -1;  // the controller's: from the plan's header
+  p.fraction = fraction;
+  p.ctl = c.header;
+  p.keep = c.req_keep;
+  p.keep_stride = width;
+  p.summary = summary;
+  const uintptr_t inner = ((base + l.inner) + 255) & ~(uintptr_t)255;
+  if (objective == EKV_OBJ_SUM) {
+    p.state = (alloc::State *)inner;
+    p.row_stat = (alloc::RowStat *)(inner + sizeof(alloc::State));
+    rc = alloc::launch_sum(p, s);
+  } else {
+    const MaxminLayout ml = maxmin_layout(rows, width);
+    alloc::MaxminParams m{};
+    m.p = p;
+    m.p.state = (alloc::State *)(inner + ml.state);
+    m.p.row_stat = (alloc::RowStat *)(inner + ml.row_stat);
+    m.mrow = (alloc::MaxminRow *)(inner + ml.mrow);
+    m.vals_out = (int32_t *)(inner + ml.vals_out);
+    m.prefix = (double *)(inner + ml.prefix);
+    m.order = (int32_t *)(inner + ml.order);
+    m.level_count = (int32_t *)(inner + ml.level_count);
+    m.level_pos = (uint16_t *)(inner + ml.level_pos);
+    rc = alloc::launch_maxmin(m, rows, width, s);
+  }
+  if (rc != EKV_OK) return rc;
+  hipLaunchKernelGGL(alloc::ctl_scatter_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, c, keep, keep_stride);
+  return check_hip(hipGetLastError(), "ekv_controller_keep scatter launch");
 }

@@ -16,8 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("EKV_HIP_LIB") or os.path.join(HERE, "lib", "libekv_hip.so")
 
 OK, EINVAL, ELAUNCH, EUNSUPPORTED = 0, -1, -2, -3
-F32, F16, BF16, FP8_E4M3 = 0, 1, 2, 3
+F32, F16, BF16, FP8_E4M3, F64 = 0, 1, 2, 3, 4
 AGG_MEAN, AGG_MAX = 0, 1
+OBJ_SUM, OBJ_MAXMIN = 0, 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -83,6 +84,13 @@ _SIGNATURES: dict[str, list] = {
     "ekv_rank_sum": [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p, _sz, _p],
     "ekv_rank_maxmin_workspace": [_i32, _i32],
     "ekv_rank_maxmin": [_p, _i64, _p, _p, _i64, _i32, _i32, _i64, _p, _i64, _p, _p, _sz, _p],
+    "ekv_controller_keep_workspace": [_i32, _i32, _i32],
+    "ekv_controller_keep": [
+        _i32, _p, _i32, _i64,  # objective, shares, dtype, stride
+        _p, _p, _p, _p, _i64, _p,  # lengths, evidence, audited, released, stride, weights
+        _i32, _i32, _i32, _i32, _f64,  # rows, width, recent, cap, fraction
+        _p, _i64, _p, _p, _sz, _p,  # keep, stride, summary, workspace, bytes, stream
+    ],
     "ekv_compact_slots": [
         _p, _p, _i32, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _p, _p, _i32, _p,
     ],

@@ -45,7 +45,7 @@ def test_argument_errors_map_to_value_error():
 
 COMPUTE = ("ekv_audit_tile_lse", "ekv_tile_shares", "ekv_tile_shares_ws", "ekv_tile_shares_noalloc", "ekv_normalize_tile_lse",
            "ekv_rank_uniform", "ekv_rank_uniform_ws", "ekv_rank_uniform_view", "ekv_rank_sum", "ekv_rank_maxmin", "ekv_compact_view",
-           "ekv_build_view", "ekv_compact_slots")
+           "ekv_build_view", "ekv_compact_slots", "ekv_controller_keep")
 
 
 def test_every_entry_point_rejects_null_pointers_on_the_host():
@@ -88,3 +88,12 @@ def test_shape_limits_are_refused_on_the_host():
     # SGLang lists: slots of 3 bytes
     with pytest.raises(ValueError, match="slots"):
         ekv_hip.call("ekv_compact_slots", P, P, 3, P, 8, 0, 1, 1, 1, 8, 16, 16, P, P, P, 8, P, 0, 0, 0)
+    # the controller's rule: an unknown objective, weights under maxmin, a fraction outside (0, 1]
+    ctl = [ekv_hip.OBJ_SUM, P, ekv_hip.F32, 64, P, P, 0, 0, 0, 0, 4, 64, 1, 0, 0.5, P, 64, 0, P, 1 << 30, 0]
+    for at, value, match in ((0, 7, "objective"), (9, P, "weights"), (14, 1.5, "fraction"), (14, 0.0, "fraction")):
+        bad = list(ctl)
+        bad[at] = value
+        if at == 9:
+            bad[0] = ekv_hip.OBJ_MAXMIN
+        with pytest.raises(ValueError, match=match):
+            ekv_hip.call("ekv_controller_keep", *bad)

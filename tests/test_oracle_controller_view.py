@@ -107,3 +107,54 @@ def test_cycle_reader_algebra(known_answers):
     case = known_answers["cycles"]["shares"]
     assert abs(cycles.shares(case["cycles"])["A"] - case["A"]) < 1e-12
     assert cycles.shares({}) == {} and cycles.shares({"A": 0}) == {}
+
+
+def concentrated(n, width):
+    # tests/test_controller.py:94-99: one block carries nearly all the attention
+    s = np.zeros(width)
+    s[:n] = 0.02 / (n - 1)
+    s[3] = 0.98
+    s[:n] /= s[:n].sum()
+    return s
+
+
+def test_sum_objective_known_answers(known_answers):
+    # the reference's controller tests run under its default objective, `sum`
+    # (observe/controller.py:30; tests/test_controller.py:116-157)
+    for objective in ("sum", "maxmin"):
+        case = known_answers["controller"]["cap_trims_only_long_requests"]
+        width = case["width"]
+        shares = np.stack([diffuse(14, width), diffuse(6, width), np.zeros(width)])
+        keep, _ = oc.keep_rows(shares, np.array(case["lengths"]), np.array([1, 1, 0]), case["fraction"],
+                               case["recent_blocks"], case["cap_above_blocks"], objective=objective)
+        assert keep[0, :14].sum() == case["kept_long"] and keep[1, :6].sum() == case["short_reads_in_full"]
+        case = known_answers["controller"]["without_a_cap_both_are_trimmed"]
+        keep, _ = oc.keep_rows(shares, np.array(case["lengths"]), np.array([1, 1, 0]), case["fraction"],
+                               case["recent_blocks"], case["cap_above_blocks"], objective=objective)
+        assert keep[0, :14].sum() + keep[1, :6].sum() == case["kept_total"]
+    # tests/test_controller.py:116-132: the concentrated request gives blocks up to the diffuse one and
+    # keeps the block that carries its attention; first and newest blocks are kept
+    width = 16
+    shares = np.stack([concentrated(12, width), diffuse(12, width)])
+    keep, budget = oc.keep_rows(shares, np.array([12, 12]), np.array([1, 1]), 0.5, 1, 0, objective="sum")
+    kept = keep[:, :12].sum(axis=1)
+    assert kept.sum() <= int(np.ceil(0.5 * 24)) and kept[0] < kept[1]
+    assert keep[0, 3] and keep[:, 0].all() and keep[:, 11].all()
+
+
+def test_sum_ties_use_the_requests_remaining_blocks():
+    # Request(scores=scores[exists]) (observe/controller.py:425-431): a freed block leaves its request,
+    # so "the newer block" of the sum rule's tie is counted among the request's remaining blocks.
+    # Row 0 frees block 2: its block 4 is the request's 4th block (index 3); row 1's block 4 is index 4.
+    # Both carry gain 0.375, the one free block (budget max(4, ceil(0.4 * 12)) = 5 over 4 pins) goes
+    # to the newer one, row 1's -- by table position the two would tie and row 0 (earlier) would win.
+    width = 6
+    shares = np.array([[0.25, 0.125, 0.9, 0.125, 0.375, 0.125],
+                       [0.25, 0.125, 0.0625, 0.0625, 0.375, 0.125]])
+    released = np.zeros((2, width), dtype=bool)
+    released[0, 2] = True
+    keep, budget = oc.keep_rows(shares, np.array([6, 6]), np.array([1, 1]), 0.4, recent_blocks=0,
+                                released=released, objective="sum")
+    assert budget == 5
+    assert np.flatnonzero(keep[0]).tolist() == [0, 5]
+    assert np.flatnonzero(keep[1]).tolist() == [0, 4, 5]
