@@ -12,7 +12,7 @@
 
 namespace ekv {
 
-constexpr int kMaxLeaves = 256;  // pairwise leaves of a row of at most 12288 values
+constexpr int kMaxLeaves = 128;  // pairwise leaves of one run of at most kChunk values (65 at most)
 
 // np.maximum(s, 0.0): NaN stays NaN, -0.0 stays -0.0
 __device__ __forceinline__ double clamp0(double s) { return (s >= 0.0 || s != s) ? s : 0.0; }
@@ -61,42 +61,48 @@ template <class Get>
 __device__ double numpy_sum(Get get, int n, int *s_start, int *s_len, double *s_leaf) {
   const int lane = lane_id();
   __shared__ int s_nleaves;
-  if (lane == 0) {  // the leaves of every run, left to right: pieces of at most 128 values
-    int leaves = 0;
-    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk)
-      plan_leaves<kPairDepth>(c0, n > 0 ? min(n - c0, kChunk) : 0, leaves, s_start, s_len);
-    s_nleaves = leaves;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const int leaves = s_nleaves;
-  for (int j = lane; j < leaves; j += kWave) {  // a leaf: eight accumulators, then the rest in order
-    const int s = s_start[j], len = s_len[j];
-    double res;
-    if (len < 8) {
-      res = 0.0;
-      for (int i = 0; i < len; ++i) res += get(s + i);
-    } else {
-      double r[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) r[k] = get(s + k);
-      int i = 8;
-      for (; i < len - (len % 8); i += 8) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) r[k] += get(s + i + k);
-      }
-      res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-      for (; i < len; ++i) res += get(s + i);
-    }
-    s_leaf[j] = res;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   double total = 0.0;
-  if (lane == 0) {  // every run combined in its recursion's order, the runs added in turn
-    int next = 0;
-    for (int c0 = 0; c0 < max(n, 1); c0 += kChunk)
-      total += combine_leaves<kPairDepth>(n > 0 ? min(n - c0, kChunk) : 0, next, s_leaf);
+  // the runs one at a time: each run's leaves (at most 65, of at most 128 values each; fewer for
+  // a short run) planned by lane 0, summed by the wave, combined in the recursion's order by lane 0
+  // and added to the total in turn
+  for (int c0 = 0; c0 < max(n, 1); c0 += kChunk) {
+    const int run = n > 0 ? min(n - c0, kChunk) : 0;
+    if (lane == 0) {
+      int leaves = 0;
+      plan_leaves<kPairDepth>(c0, run, leaves, s_start, s_len);
+      s_nleaves = leaves;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int leaves = s_nleaves;
+    for (int j = lane; j < leaves; j += kWave) {  // a leaf: eight accumulators, then the rest in order
+      const int s = s_start[j], len = s_len[j];
+      double res;
+      if (len < 8) {
+        res = 0.0;
+        for (int i = 0; i < len; ++i) res += get(s + i);
+      } else {
+        double r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r[k] = get(s + k);
+        int i = 8;
+        for (; i < len - (len % 8); i += 8) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) r[k] += get(s + i + k);
+        }
+        res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < len; ++i) res += get(s + i);
+      }
+      s_leaf[j] = res;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (lane == 0) {
+      int next = 0;
+      total += combine_leaves<kPairDepth>(run, next, s_leaf);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the leaf arrays are free for the next run
   }
   return __shfl(total, 0, kWave);
 }

@@ -923,6 +923,254 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
   }
 }
 
+
+// ---------------------------------------------------------------------------------------
+// Rows wider than a row in registers (width > kMaxWidth): one 1024-thread workgroup per row
+// streams the row from memory in every pass instead -- the same budget, quota, key modes, radix
+// select and ties by index as rank_kernel, the keys recomputed from the scores and masks each
+// time they are needed.  The ties are ranked in index order, chunk by chunk, by a running scan.
+// ---------------------------------------------------------------------------------------
+constexpr int kWideThreads = 1024;
+constexpr int kMaxWideWidth = 1 << 18;  // 262144 blocks: a float64 row's set bits and their prefix fit LDS
+
+template <bool F64>
+__global__ __launch_bounds__(kWideThreads) void rank_wide_kernel(const Params p) {
+  constexpr int NT = kWideThreads, NW = NT / kWave;
+  using Key = typename std::conditional<F64, unsigned long long, uint32_t>::type;
+  constexpr Key kClosedKey = ~Key(0);
+  constexpr int kPasses = F64 ? 8 : 4;
+  __shared__ long long s_red[6][NW];
+  __shared__ int s_hist[2][256];
+  __shared__ int s_scan[NW];
+  __shared__ int s_digit, s_krem, s_whole;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const RowInfo me = row_info(p, row);
+  uint8_t *keep_row = p.keep + (int64_t)row * p.keep_stride;
+
+  long long t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
+  for (int r = tid; r < p.rows; r += NT) {
+    const RowInfo ri = row_info(p, r);
+    if (!ri.part) continue;
+    t5[0] += ri.n;
+    t5[1] += ri.pinned;
+    t5[2] += ri.exist;
+    t5[3] += ri.exist - ri.pinned;
+    t5[4] += 1;
+  }
+  block_sums_n<NT>(t5, reinterpret_cast<long long (*)[NW]>(s_red));
+  const long long total = t5[0], floor_pins = t5[1], sizes = t5[2], open_total = t5[3], nreq = t5[4];
+  long long budget = p.budget_in;
+  if (budget < 0) {  // controller.py:435-437
+    const long long want = (long long)ceil(p.fraction * (double)total);
+    budget = want > floor_pins ? want : floor_pins;
+  }
+  const bool error = floor_pins > budget && budget < sizes;  // allocation.py:64-65
+  const bool keep_all = budget >= sizes;                      // allocation.py:66-67
+  const long long free_blocks = budget - floor_pins;
+  if (row == 0 && tid == 0 && p.summary != nullptr) {
+    p.summary[0] = budget;
+    p.summary[1] = total;
+    p.summary[2] = floor_pins;
+    p.summary[3] = error ? 1 : 0;
+    p.summary[4] = nreq;
+    p.summary[5] = free_blocks;
+  }
+  if (!me.part || error) {  // rows without evidence read in full, controller.py:401
+    for (int b = tid; b < p.width; b += NT) keep_row[b] = 1;
+    return;
+  }
+  const int n = me.n;
+  auto open_at = [&](int b) -> bool { return b < n && exists(p, row, b) && !is_pinned(p, me, row, b); };
+  const double row_total = F64 ? p.totals[row] : 0.0;
+  const double uniform = 1.0 / (double)(me.exist > 0 ? me.exist : 1);
+
+  // ---- this row's quota (allocation.py:79-86) and its blocks' counts ----------------------------
+  const long long my_open = me.exist - me.pinned;
+  const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
+  const long long my_floor = (long long)my_exact;
+  const double my_frac = my_exact - (double)my_floor;
+  // floors, rows ahead in the leftover order, NaN / +inf / positive existing scores, open blocks
+  long long q[6] = {0, 0, 0, 0, 0, 0};
+  if (!keep_all) {
+    for (int r = tid; r < p.rows; r += NT) {
+      const RowInfo ri = row_info(p, r);
+      if (!ri.part) continue;
+      const long long open = ri.exist - ri.pinned;
+      const double exact = open_total > 0 ? (double)(free_blocks * open) / (double)open_total : 0.0;
+      const long long fl = (long long)exact;
+      const double frac = exact - (double)fl;
+      q[0] += fl;
+      q[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
+    }
+  }
+  for (int b = tid; b < n; b += NT) {
+    if (!exists(p, row, b)) continue;
+    if (!F64) {
+      const float s = p.scores[(int64_t)row * p.scores_stride + b];
+      q[2] += __builtin_isnan(s) ? 1 : 0;
+      q[3] += (__builtin_isinf(s) && s > 0.0f) ? 1 : 0;
+      q[4] += s > 0.0f ? 1 : 0;
+    }
+    q[5] += is_pinned(p, me, row, b) ? 0 : 1;
+  }
+  block_sums_n<NT>(q, s_red);
+  long long quota;
+  if (keep_all) {
+    quota = my_open;
+  } else {
+    const long long leftover = free_blocks - q[0];
+    quota = my_floor + (q[1] < leftover ? 1 : 0);
+  }
+  const long long open_count = q[5];
+  const int mode = q[2] ? 0 : (q[3] ? 2 : (q[4] ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
+
+  // a block's key (order-preserving, larger first), kClosedKey unless open
+  auto key_at = [&](int b) -> Key {
+    if (!open_at(b)) return kClosedKey;
+    if constexpr (F64) {
+      double v = row_total <= 0.0 ? uniform : clamp0(p.scores64[(int64_t)row * p.scores_stride + b]) / row_total;
+      if (v == 0.0) v = 0.0;
+      return v != v ? 0ull : __builtin_bit_cast(unsigned long long, v) + 1ull;
+    } else {
+      const float s = p.scores[(int64_t)row * p.scores_stride + b];
+      if (mode == 1) return s > 0.0f ? __builtin_bit_cast(uint32_t, s) : 0u;
+      if (mode == 2) return (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
+      return 0u;
+    }
+  };
+
+  bool keep_open = quota >= open_count, keep_none = quota <= 0;
+  Key prefix = 0, mask = 0;
+  int k_rem = (int)quota;
+  bool whole = false;
+  if (!keep_open && !keep_none) {
+    if (tid < 256) s_hist[0][tid] = 0;
+    __syncthreads();
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int shift = 8 * (kPasses - 1) - 8 * pass;
+      int *hist = s_hist[pass & 1];
+      for (int b = tid; b < n; b += NT) {
+        const Key k = key_at(b);
+        if (k != kClosedKey && (k & mask) == prefix) atomicAdd(&hist[(int)(k >> shift) & 255], 1);
+      }
+      if (tid < 256) s_hist[(pass & 1) ^ 1][tid] = 0;
+      __syncthreads();
+      if (wave == 0) {
+        int c[4], s4 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = hist[255 - 4 * lane - j];
+          s4 += c[j];
+        }
+        const int inc = wave_inclusive_scan(s4);
+        int acc = inc - s4;
+        if (acc < k_rem && inc >= k_rem) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (acc < k_rem && acc + c[j] >= k_rem) {
+              s_digit = 255 - 4 * lane - j;
+              s_krem = k_rem - acc;
+              s_whole = acc + c[j] == k_rem ? 1 : 0;
+            }
+            acc += c[j];
+          }
+        }
+      }
+      __syncthreads();
+      prefix |= (Key)s_digit << shift;
+      mask |= (Key)255 << shift;
+      k_rem = s_krem;
+      whole = s_whole != 0;
+      if (whole) break;
+    }
+  }
+  // the keep, chunk by chunk in index order; the equal keys before a block counted by a running scan
+  int eq_before = 0;
+  for (int b0 = 0; b0 < p.width; b0 += NT) {
+    const int b = b0 + tid;
+    const Key k = b < n ? key_at(b) : kClosedKey;
+    bool kept = false;
+    int eq_chunk = 0;
+    if (keep_open) {
+      kept = k != kClosedKey;
+    } else if (!keep_none) {
+      if (whole) {
+        kept = k != kClosedKey && (k & mask) >= prefix;
+      } else {
+        const bool eq = k != kClosedKey && k == prefix;
+        const int before = eq_before + block_exclusive_scan<NT>(eq ? 1 : 0, s_scan, eq_chunk);
+        kept = k != kClosedKey && (k > prefix || (eq && before < k_rem));
+      }
+    }
+    eq_before += eq_chunk;
+    if (b < p.width) {
+      uint8_t v;
+      if (b >= n) v = 1;
+      else if (!exists(p, row, b)) v = 0;
+      else if (is_pinned(p, me, row, b)) v = 1;
+      else v = kept ? 1 : 0;
+      keep_row[b] = v;
+    }
+  }
+}
+
+// Each float64 request's NumPy total over its existing blocks for rows wider than kMaxWidth with a
+// released mask: the row's existing blocks as bits in LDS with each word's prefix count, so that
+// NumPy's sum over the remaining blocks (taken by wave 0) finds the i-th one by a binary search.
+__global__ __launch_bounds__(kWideThreads) void total64_wide_kernel(const Params p, double *totals) {
+  constexpr int NT = kWideThreads, kWords = kMaxWideWidth / 32;
+  __shared__ uint32_t s_bits[kWords];
+  __shared__ int s_pref[kWords];
+  __shared__ int s_scan[NT / kWave];
+  __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
+  __shared__ double s_leaf[kMaxLeaves];
+  const int r = blockIdx.x;
+  const int n = min(max(p.blocks[r], 0), p.width);
+  const int words = (n + 31) / 32;
+  constexpr int kPer = kWords / NT;  // words per thread, a contiguous run (the scan below is in word order)
+  int cnt[kPer], mine = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int w = threadIdx.x * kPer + j;
+    uint32_t bits = 0;
+    if (w < words)
+      for (int i = 0; i < 32; ++i) {
+        const int b = 32 * w + i;
+        bits |= (b < n && exists(p, r, b)) ? (1u << i) : 0u;
+      }
+    s_bits[w] = bits;
+    cnt[j] = __popc(bits);
+    mine += cnt[j];
+  }
+  int total_bits;
+  int before = block_exclusive_scan<NT>(mine, s_scan, total_bits);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    s_pref[threadIdx.x * kPer + j] = before;
+    before += cnt[j];
+  }
+  __syncthreads();
+  if (threadIdx.x >= kWave) return;
+  const double *srow = p.scores64 + (int64_t)r * p.scores_stride;
+  static_assert(kWords % NT == 0, "whole runs of words per thread");
+  auto block_of = [&](int i) -> int {  // the i-th existing block
+    int lo = 0, hi = words - 1;
+    while (lo < hi) {  // the last word whose prefix count is at most i
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pref[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    uint32_t bits = s_bits[lo];
+    for (int k = i - s_pref[lo]; k > 0; --k) bits &= bits - 1;  // drop the lower set bits
+    return 32 * lo + __builtin_ctz(bits);
+  };
+  const double total = numpy_sum([&](int i) { return clamp0(srow[block_of(i)]); }, total_bits, s_start, s_len,
+                                 s_leaf);
+  if (lane_id() == 0) totals[r] = total;
+}
+
 }  // namespace rank
 }  // namespace ekv
 
@@ -949,8 +1197,8 @@ extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride,
   if (scores == nullptr || blocks == nullptr || keep == nullptr || table == nullptr || seq_lens == nullptr ||
       view_table == nullptr || view_lens == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_uniform_view: null pointer");
-  if (rows < 0 || width < 1 || width > rank::kMaxWidth)
-    return fail(EKV_EINVAL, "ekv_rank_uniform_view: rows %d, width %d (at most %d)", rows, width, rank::kMaxWidth);
+  if (rows < 0 || width < 1 || width > rank::kMaxWideWidth)
+    return fail(EKV_EINVAL, "ekv_rank_uniform_view: rows %d, width %d (at most %d)", rows, width, rank::kMaxWideWidth);
   if (recent_blocks < 0) return fail(EKV_EINVAL, "ekv_rank_uniform_view: recent_blocks %d < 0", recent_blocks);
   if (budget < 0 && !(fraction > 0.0 && fraction <= 1.0))
     return fail(EKV_EINVAL, "ekv_rank_uniform_view: the budget fraction %g is not in (0, 1]", fraction);
@@ -979,6 +1227,13 @@ extern "C" int ekv_rank_uniform_view(const float *scores, int64_t scores_stride,
   p.view_lens = view_lens;
   p.view_counts = (long long *)counts;
   hipStream_t s = (hipStream_t)stream;
+  if (width > rank::kMaxWidth) {  // a row too wide for registers: the streaming ranking, then the view
+    hipLaunchKernelGGL((rank::rank_wide_kernel<false>), dim3(rows), dim3(rank::kWideThreads), 0, s, p);
+    const int rc = check_hip(hipGetLastError(), "ekv_rank_uniform_view launch");
+    if (rc != EKV_OK) return rc;
+    return ekv_build_view(table, table_stride, seq_lens, keep, keep_stride, nullptr, 0, nullptr, nullptr, 1, rows,
+                          width, block_size, view_table, view_stride, view_lens, counts, stream);
+  }
   const int per = (width + rank::kThreads - 1) / rank::kThreads;
   // the lean kernel counts blocks in 32 bits; larger batches (and the widest rows) take rank_kernel
   const bool lean = (int64_t)rows * width < ((int64_t)1 << 31);
@@ -1007,8 +1262,8 @@ extern "C" int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, c
                                    int32_t *workspace, void *stream) {
   if (scores == nullptr || blocks == nullptr || keep == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_uniform: null pointer");
-  if (rows < 0 || width < 1 || width > rank::kMaxWidth)
-    return fail(EKV_EINVAL, "ekv_rank_uniform: rows %d, width %d (at most %d)", rows, width, rank::kMaxWidth);
+  if (rows < 0 || width < 1 || width > rank::kMaxWideWidth)
+    return fail(EKV_EINVAL, "ekv_rank_uniform: rows %d, width %d (at most %d)", rows, width, rank::kMaxWideWidth);
   if (recent_blocks < 0) return fail(EKV_EINVAL, "ekv_rank_uniform: recent_blocks %d < 0", recent_blocks);
   if (budget < 0 && !(fraction > 0.0 && fraction <= 1.0))
     return fail(EKV_EINVAL, "ekv_rank_uniform: the budget fraction %g is not in (0, 1]", fraction);
@@ -1040,6 +1295,11 @@ extern "C" int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, c
     if (rc != EKV_OK) return rc;
     p.counts = workspace;
   }
+  if (width > rank::kMaxWidth) {  // a row too wide for registers: the streaming ranking
+    hipLaunchKernelGGL((rank::rank_wide_kernel<false>), dim3(rows), dim3(rank::kWideThreads), 0, (hipStream_t)stream,
+                       p);
+    return check_hip(hipGetLastError(), "ekv_rank_uniform launch");
+  }
   const int per = (width + rank::kThreads - 1) / rank::kThreads;
   if (per <= 4)
     hipLaunchKernelGGL(rank::rank_kernel<4>, dim3(rows), dim3(rank::kThreads), 0, (hipStream_t)stream, p);
@@ -1070,8 +1330,8 @@ extern "C" int ekv_rank_uniform64(const double *scores, int64_t scores_stride, c
                                   void *workspace, size_t workspace_bytes, void *stream) {
   if (scores == nullptr || blocks == nullptr || keep == nullptr || workspace == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_uniform64: null pointer");
-  if (rows < 0 || width < 1 || width > rank::kMaxWidth)
-    return fail(EKV_EINVAL, "ekv_rank_uniform64: rows %d, width %d (at most %d)", rows, width, rank::kMaxWidth);
+  if (rows < 0 || width < 1 || width > rank::kMaxWideWidth)
+    return fail(EKV_EINVAL, "ekv_rank_uniform64: rows %d, width %d (at most %d)", rows, width, rank::kMaxWideWidth);
   if (recent_blocks < 0) return fail(EKV_EINVAL, "ekv_rank_uniform64: recent_blocks %d < 0", recent_blocks);
   if (budget < 0 && !(fraction > 0.0 && fraction <= 1.0))
     return fail(EKV_EINVAL, "ekv_rank_uniform64: the budget fraction %g is not in (0, 1]", fraction);
@@ -1100,7 +1360,10 @@ extern "C" int ekv_rank_uniform64(const double *scores, int64_t scores_stride, c
   double *totals = (double *)workspace;
   int32_t *counts = (int32_t *)((char *)workspace + uniform64_totals_bytes(rows));
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(rank::total64_kernel, dim3(rows), dim3(kWave), 0, s, p, totals);
+  if (width > rank::kMaxWidth && released != nullptr)  // the remaining blocks found through LDS bits
+    hipLaunchKernelGGL(rank::total64_wide_kernel, dim3(rows), dim3(rank::kWideThreads), 0, s, p, totals);
+  else
+    hipLaunchKernelGGL(rank::total64_kernel, dim3(rows), dim3(kWave), 0, s, p, totals);
   int rc = check_hip(hipGetLastError(), "ekv_rank_uniform64 totals launch");
   if (rc != EKV_OK) return rc;
   p.totals = totals;
@@ -1109,6 +1372,10 @@ extern "C" int ekv_rank_uniform64(const double *scores, int64_t scores_stride, c
     rc = check_hip(hipGetLastError(), "ekv_rank_uniform64 count launch");
     if (rc != EKV_OK) return rc;
     p.counts = counts;
+  }
+  if (width > rank::kMaxWidth) {  // a row too wide for registers: the streaming ranking
+    hipLaunchKernelGGL((rank::rank_wide_kernel<true>), dim3(rows), dim3(rank::kWideThreads), 0, s, p);
+    return check_hip(hipGetLastError(), "ekv_rank_uniform64 launch");
   }
   const int per = (width + rank::kThreads - 1) / rank::kThreads;
   if (per <= 4)

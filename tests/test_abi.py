@@ -64,13 +64,14 @@ def test_shape_limits_are_refused_on_the_host():
     import pytest
 
     P = 256  # a placeholder device address: the checks below refuse the call before using it
-    # ranking: a row wider than the register-resident maximum
+    # ranking: a row wider than the streaming kernel's LDS holds (262144 blocks)
+    wide = 300000
     with pytest.raises(ValueError, match="width"):
-        ekv_hip.call("ekv_rank_uniform", P, 20000, P, 0, 0, 0, 0, 0, 0, 0, 4, 20000, 0.5, -1, P, 20000, 0, 0)
+        ekv_hip.call("ekv_rank_uniform", P, wide, P, 0, 0, 0, 0, 0, 0, 0, 4, wide, 0.5, -1, P, wide, 0, 0)
     # ranking + view: the same width limit, and a block size below 1
     with pytest.raises(ValueError, match="width"):
-        ekv_hip.call("ekv_rank_uniform_view", P, 20000, P, 0, 0, 0, 4, 20000, 0.5, -1, P, 20000, 0, P, 20000, P, 16,
-                     P, 20000, P, 0, 0)
+        ekv_hip.call("ekv_rank_uniform_view", P, wide, P, 0, 0, 0, 4, wide, 0.5, -1, P, wide, 0, P, wide, P, 16,
+                     P, wide, P, 0, 0)
     with pytest.raises(ValueError, match="block size"):
         ekv_hip.call("ekv_rank_uniform_view", P, 64, P, 0, 0, 0, 4, 64, 0.5, -1, P, 64, 0, P, 64, P, 0, P, 64, P, 0, 0)
     # ranking: explicit masks without a workspace
