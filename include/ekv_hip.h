@@ -113,7 +113,8 @@ int ekv_audit_plan(const int32_t *table, int64_t table_stride, const int32_t *le
 /*
  * ekv_audit_tile_lse reading its work list from a plan built by ekv_audit_plan from the same
  * table, lengths, selection and query tokens: the same records and cycles, without the per-launch
- * scan of the rows.  Replaces tile_lse_kernel + RecordingPlane.launch, runtime/audit_kernel.py
+ * scan of the rows, and for any number of rows (ekv_audit_tile_lse keeps per-row offsets in LDS and
+ * takes at most 6000).  Replaces tile_lse_kernel + RecordingPlane.launch, runtime/audit_kernel.py
  * :34-109 and :224-265, as ekv_audit_tile_lse does.  Shapes without an MFMA form (fp32 keys,
  * 8-token blocks) run the self-contained kernel.
  */
@@ -206,6 +207,8 @@ int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row
  *    max(floor, ceil(fraction * total)) in IEEE double, total = sum of blocks[r].
  *  - free blocks are split by largest remainder in IEEE double, then each row keeps its quota
  *    of open blocks by (share desc, block index asc).  Shares are max(score, 0) as float32.
+ * width at most 262144: rows up to 12288 blocks wide are ranked in registers and LDS by one
+ * workgroup each, wider rows by a streaming workgroup per row over the scores in memory.
  * scores[r, b], pinned[r, b] and released[r, b] are read for every b < width (rows of `width`
  * readable entries; the values past blocks[r] are ignored).
  * keep[r, b] (uint8, row stride keep_stride) is written for every r < rows, b < width: 1 for
@@ -373,7 +376,8 @@ int ekv_build_view(const int32_t *table, int64_t table_stride, const int32_t *se
  * token while the policy is live, and blocks read while it is not.  `entries` is indptr[n_rows],
  * which the host knows.  With write_back, new_indptr is copied into indptr and the new list into
  * slots[0 .. new total) in place (entries past the new total keep their old values).  No host
- * synchronisation; n_rows <= 6000.
+ * synchronisation; up to 6000 rows the gather keeps the offsets in LDS, more rows take one more
+ * kernel that writes them to new_indptr first.
  */
 int ekv_compact_slots(int32_t *indptr, void *slots, int32_t slot_bytes, const uint8_t *keep,
                       int64_t keep_stride, const uint8_t *audit, int32_t active, int32_t n_real,

@@ -1332,16 +1332,16 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
                 int64_t lse_layer_stride, int64_t lse_row_stride, int32_t cells, uint64_t *cycles,
                 int32_t cycles_rows, float scale, int32_t layer, int32_t group_first, int32_t groups,
                 int32_t group_rows, int32_t rows, int32_t width, int32_t block_size, int32_t tile_blocks,
-                int32_t head_dim, int32_t chunk_tiles, Params &p, Launch &L) {
+                int32_t head_dim, int32_t chunk_tiles, bool planned, Params &p, Launch &L) {
   if (q == nullptr || keys == nullptr || table == nullptr || lens == nullptr || qrow == nullptr ||
       select == nullptr || flag == nullptr || lse == nullptr)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: null pointer argument");
   if (tile_blocks != kTileBlocks)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: tiles of %d blocks; the kernel records tiles of %d",
                 tile_blocks, kTileBlocks);
-  if (rows < 0 || rows > kMaxRows || width <= 0 || block_size <= 0 || layer < 0)
-    return fail(EKV_EINVAL, "ekv_audit_tile_lse: rows %d (max %d), width %d, block %d, layer %d out of range",
-                rows, kMaxRows, width, block_size, layer);
+  if (rows < 0 || width <= 0 || block_size <= 0 || layer < 0)
+    return fail(EKV_EINVAL, "ekv_audit_tile_lse: rows %d, width %d, block %d, layer %d out of range", rows, width,
+                block_size, layer);
   if (group_rows < 1 || group_rows > 16)
     return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d query rows per KV head; at most 16 are recorded", group_rows);
   if (groups < 1 || groups > 32767 || group_first < 0 || cells < groups * group_rows)
@@ -1392,6 +1392,12 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
   if (L.fn == nullptr)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, block size %d",
                 kv_dtype, head_dim, block_size);
+  // the self-contained kernels keep per-row tile offsets in LDS; a planned MFMA launch reads them
+  // from the plan and takes any number of rows
+  const bool row_lds = !(planned && use_mfma);
+  if (row_lds && rows > kMaxRows)
+    return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d rows; a launch without a step plan (or with fp32 keys or "
+                "8-token blocks) takes at most %d", rows, kMaxRows);
   // 16-byte loads of key rows and query slices
   const uint64_t kaddr = (uint64_t)keys | (uint64_t)(k_stride_block * kbytes) |
                          (uint64_t)(k_stride_pos * kbytes) | (uint64_t)(k_stride_head * kbytes);
@@ -1442,6 +1448,7 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
   const int64_t min_per_wave = p.chunk_tiles;
   const int waves = L.threads / kWave;
   int64_t blocks = (max_tiles + min_per_wave * waves - 1) / (min_per_wave * waves);
+  if (!row_lds) return EKV_OK;  // the planned launch's grid is one workgroup per compute unit
   const int resident = resident_blocks(L.fn, L.lds, L.threads);
   if (resident < 1)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: a workgroup of %d threads with %zu bytes of row data does "
@@ -1490,7 +1497,7 @@ extern "C" int ekv_audit_tile_lse(
                              k_stride_head, k_scale, table, table_stride, lens, qrow, select, flag, lse,
                              lse_plane_stride, lse_layer_stride, lse_row_stride, cells, cycles, cycles_rows, scale,
                              layer, group_first, groups, group_rows, rows, width, block_size, tile_blocks, head_dim,
-                             chunk_tiles, p, L);
+                             chunk_tiles, false, p, L);
   if (rc != EKV_OK || rows == 0) return rc;
   hipLaunchKernelGGL(L.fn, dim3((unsigned)L.blocks), dim3(L.threads), L.lds, (hipStream_t)stream, p);
   return check_hip(hipGetLastError(), "ekv_audit_tile_lse launch");
@@ -1556,7 +1563,7 @@ extern "C" int ekv_audit_tile_lse_planned(
   int rc = audit_setup(q, q_dtype, q_stride_token, q_stride_head, keys, kv_dtype, k_stride_block, k_stride_pos,
                        k_stride_head, k_scale, table, table_stride, lens, qrow, select, flag, lse, lse_plane_stride,
                        lse_layer_stride, lse_row_stride, cells, cycles, cycles_rows, scale, layer, group_first,
-                       groups, group_rows, rows, width, block_size, tile_blocks, head_dim, 0, p, L);
+                       groups, group_rows, rows, width, block_size, tile_blocks, head_dim, 0, true, p, L);
   if (rc != EKV_OK) return rc;
   rc = check_plan(plan, plan_bytes, plan_rows, plan_width, rows, width, "ekv_audit_tile_lse_planned");
   if (rc != EKV_OK || rows == 0) return rc;

@@ -15,7 +15,9 @@
 //    rows does not matter).
 //  * gather: every workgroup rebuilds the new offsets (an exclusive scan of the new lengths) and
 //    the old ones in LDS, finds each output position's row by binary search and copies the slot
-//    it comes from; workgroup 0 writes new_indptr.
+//    it comes from; workgroup 0 writes new_indptr.  Past kMaxRows rows (more than LDS holds) one
+//    workgroup writes new_indptr and the counters first, and the gather searches new_indptr and
+//    indptr in memory instead.
 //  * write back (optional): new_indptr into indptr and the new list into slots, in place.
 #include "ekv_common.hpp"
 
@@ -26,7 +28,8 @@ constexpr int kPlanThreads = 512;
 constexpr int kPlanWaves = kPlanThreads / kWave;
 constexpr int kGatherThreads = 256;
 constexpr int kPerThread = 4;  // output positions per gather thread
-constexpr int kMaxRows = 6000;  // the gather keeps two offsets per row in LDS
+constexpr int kMaxRows = 6000;  // the gather keeps two offsets per row in LDS up to this many rows
+constexpr int kOffsetThreads = 1024;  // offsets_kernel, for more rows
 
 struct Params {
   const int32_t *indptr;
@@ -82,11 +85,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const Params p) {
 // offsets: a row of `blocks` blocks whose length went from `length` to `new_length` kept
 // blocks + (new_length - length) / block_tokens of them.  One uncontended add per counter (the
 // rows' workgroups of plan_kernel would otherwise contend on the same five addresses).
+template <int NT>
 __device__ __forceinline__ void add_counts(const Params &p, const int *s_new, const int *s_old) {
-  __shared__ long long s_red[5][kGatherThreads / kWave];
+  __shared__ long long s_red[5][NT / kWave];
   const int bt = p.block_tokens;
   long long v[5] = {0, 0, 0, 0, 0};  // read, full, audit, untrimmed, expired
-  for (int r = threadIdx.x; r < p.n_real && r < p.n_rows; r += kGatherThreads) {
+  for (int r = threadIdx.x; r < p.n_real && r < p.n_rows; r += NT) {
     const int length = s_old[r + 1] - s_old[r];
     const int new_length = s_new[r + 1] - s_new[r];
     const int blocks = length > 0 ? (length + bt - 1) / bt : 0;
@@ -107,7 +111,7 @@ __device__ __forceinline__ void add_counts(const Params &p, const int *s_new, co
   __syncthreads();
   if (threadIdx.x < 5) {
     long long t = 0;
-    for (int w = 0; w < kGatherThreads / kWave; ++w) t += s_red[threadIdx.x][w];
+    for (int w = 0; w < NT / kWave; ++w) t += s_red[threadIdx.x][w];
     if (t != 0) atomicAdd((unsigned long long *)&p.counts[threadIdx.x], (unsigned long long)t);
   }
 }
@@ -135,16 +139,46 @@ __device__ __forceinline__ void copy_slot(char *dst, const char *src, int bytes)
   else *(uint32_t *)dst = *(const uint32_t *)src;
 }
 
+// More rows than LDS holds: the new offsets (new_indptr) and the counters, by one workgroup, before
+// the gather reads them from memory.
+__global__ __launch_bounds__(kOffsetThreads) void offsets_kernel(const Params p) {
+  __shared__ int s_scan[kOffsetThreads / kWave];
+  const int rows = p.n_rows;
+  const int per = (rows + kOffsetThreads - 1) / kOffsetThreads;
+  const int r0 = min((int)threadIdx.x * per, rows), r1 = min(r0 + per, rows);
+  int local = 0;
+  for (int r = r0; r < r1; ++r) local += p.lens[r];
+  int total;
+  int base = block_exclusive_scan<kOffsetThreads>(local, s_scan, total);
+  for (int r = r0; r < r1; ++r) {
+    p.new_indptr[r] = base;
+    base += p.lens[r];
+  }
+  if (threadIdx.x == 0) p.new_indptr[rows] = total;
+  if (p.counts == nullptr) return;
+  __syncthreads();  // the workgroup's writes of new_indptr are seen by its reads below
+  add_counts<kOffsetThreads>(p, p.new_indptr, p.indptr);
+}
+
+// OFFSETS_IN_MEMORY: the new offsets in new_indptr (offsets_kernel) and the old ones in indptr.
+template <bool OFFSETS_IN_MEMORY>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(const Params p) {
   extern __shared__ int s_mem[];  // [n_rows + 1] new offsets, [n_rows + 1] old offsets
   __shared__ int s_scan[kGatherThreads / kWave];
-  int *s_new = s_mem, *s_old = s_mem + p.n_rows + 1;
-  offsets_in_lds(p, s_new, s_old, s_scan);
+  const int *s_new, *s_old;
+  if constexpr (OFFSETS_IN_MEMORY) {
+    s_new = p.new_indptr;
+    s_old = p.indptr;
+  } else {
+    offsets_in_lds(p, s_mem, s_mem + p.n_rows + 1, s_scan);
+    s_new = s_mem;
+    s_old = s_mem + p.n_rows + 1;
+  }
   const int rows = p.n_rows;
   const int total = s_new[rows];
-  if (blockIdx.x == 0) {
+  if (!OFFSETS_IN_MEMORY && blockIdx.x == 0) {
     for (int r = threadIdx.x; r <= rows; r += kGatherThreads) p.new_indptr[r] = s_new[r];
-    if (p.counts != nullptr) add_counts(p, s_new, s_old);
+    if (p.counts != nullptr) add_counts<kGatherThreads>(p, s_new, s_old);
   }
   const int bt = p.block_tokens;
   const int sb = p.slot_bytes;
@@ -193,10 +227,10 @@ extern "C" int ekv_compact_slots(int32_t *indptr, void *slots_buf, int32_t slot_
     return fail(EKV_EINVAL, "ekv_compact_slots: null pointer");
   if (slot_bytes != 4 && slot_bytes != 8)
     return fail(EKV_EUNSUPPORTED, "ekv_compact_slots: slots of %d bytes (4 or 8)", slot_bytes);
-  if (n_rows < 0 || n_rows > slots::kMaxRows || width < 1 || block_tokens < 1 || entries < 0 ||
-      entries > INT32_MAX || table_stride < width)
-    return fail(EKV_EINVAL, "ekv_compact_slots: rows %d (max %d), width %d, block tokens %d, entries %lld",
-                n_rows, slots::kMaxRows, width, block_tokens, (long long)entries);
+  if (n_rows < 0 || n_rows >= INT32_MAX || width < 1 || block_tokens < 1 || entries < 0 || entries > INT32_MAX ||
+      table_stride < width)
+    return fail(EKV_EINVAL, "ekv_compact_slots: rows %d, width %d, block tokens %d, entries %lld", n_rows, width,
+                block_tokens, (long long)entries);
   if (n_real < 0) n_real = 0;
   slots::Params p{};
   p.indptr = indptr;
@@ -228,8 +262,13 @@ extern "C" int ekv_compact_slots(int32_t *indptr, void *slots_buf, int32_t slot_
   // the new list is never longer than the old one
   const int64_t per_block = (int64_t)slots::kGatherThreads * slots::kPerThread;
   const int64_t grid = entries > 0 ? (entries + per_block - 1) / per_block : 1;
-  const size_t lds = (size_t)2 * (n_rows + 1) * sizeof(int);
-  hipLaunchKernelGGL(slots::gather_kernel, dim3((unsigned)grid), dim3(slots::kGatherThreads), lds, s, p);
+  if (n_rows <= slots::kMaxRows) {
+    const size_t lds = (size_t)2 * (n_rows + 1) * sizeof(int);
+    hipLaunchKernelGGL(slots::gather_kernel<false>, dim3((unsigned)grid), dim3(slots::kGatherThreads), lds, s, p);
+  } else {  // more rows than LDS holds: the offsets go through memory
+    hipLaunchKernelGGL(slots::offsets_kernel, dim3(1), dim3(slots::kOffsetThreads), 0, s, p);
+    hipLaunchKernelGGL(slots::gather_kernel<true>, dim3((unsigned)grid), dim3(slots::kGatherThreads), 0, s, p);
+  }
   rc = check_hip(hipGetLastError(), "ekv_compact_slots gather launch");
   if (rc != EKV_OK || !write_back) return rc;
   hipLaunchKernelGGL(slots::write_back_kernel, dim3((unsigned)grid), dim3(slots::kGatherThreads), 0, s, p);

@@ -207,3 +207,44 @@ def test_plan_refuses_a_batch_larger_than_the_plane():
         ekv_hip.call("ekv_audit_plan", table.data_ptr(), table.stride(0), lens.data_ptr(), plane._token.data_ptr(),
                      plane._select.data_ptr(), plane._flag_dev, 4, 32, batch.block_size, 2, plane._plan,
                      plane._plan_bytes, 2, 8, 0)
+
+
+def test_planned_rows_past_the_lds_row_limit():
+    # 8192 rows, more than the 6000 whose tile offsets the self-contained kernel keeps in LDS: the
+    # planned launch takes them all, bit-identical to the self-contained kernel run on each half, and
+    # some rows agree with the oracle; the self-contained launch refuses the whole batch
+    rng = np.random.default_rng(8192)
+    rows, width, bs, kvh, g, d = 8192, 16, 16, 2, 4, 128
+    lens = rng.integers(1, width * bs + 1, size=rows).astype(np.int32)
+    pool = 2 * rows * width
+    table = rng.permutation(pool)[: rows * width].reshape(rows, width).astype(np.int32)
+    kv = torch.randn(pool, 2, bs, kvh, d, dtype=torch.bfloat16, device="cuda")
+    q = torch.randn(rows, kvh * g, d, dtype=torch.bfloat16, device="cuda")
+    scale = d ** -0.5
+    t_all, l_all = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
+    plane = RecordingPlane(1, rows, width, g, bs)
+    audit_on(plane)
+    plane.select(np.ones(rows, bool), np.arange(rows))
+    plane.plan(t_all, l_all)
+    plane.launch(0, t_all, l_all, q, kv[:, 0], scale, planned=True)
+    with pytest.raises(ValueError, match="rows"):
+        plane.launch(0, t_all, l_all, q, kv[:, 0], scale, planned=False)
+    torch.cuda.synchronize()
+    got = plane.read_planes()
+    half = rows // 2
+    for lo in (0, half):
+        part = RecordingPlane(1, half, width, g, bs)
+        audit_on(part)
+        part.select(np.ones(half, bool), np.arange(lo, lo + half))  # each row's query token is its own
+        part.launch(0, t_all[lo : lo + half].contiguous(), l_all[lo : lo + half].contiguous(), q, kv[:, 0], scale)
+        torch.cuda.synchronize()
+        want = part.read_planes()
+        assert np.array_equal(got[:, :, lo : lo + half], want, equal_nan=True), f"rows {lo}.."
+    sample = np.zeros(rows)
+    sample[::997] = 1
+    want = oa.new_planes(1, rows, width, g)
+    kvf, qf = kv.float().cpu().numpy(), q.float().cpu().numpy()
+    oa.tile_lse(want, qf, kvf[:, 0], table, lens, np.arange(rows), sample, 1, 0, scale, bs, g, [0])
+    live = ~np.isnan(want[0])
+    assert np.abs(got[0][live] - want[0][live]).max() < 1e-3
+    print(f"{int((~np.isnan(got[0])).sum())} cells; {int(sample.sum())} rows against the oracle", flush=True)

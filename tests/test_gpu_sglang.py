@@ -86,3 +86,20 @@ def test_large_batch():
     audited = rng.random(256) < 0.1
     counts = run(c, lens, keep, padding=8, audited=audited, seed=5)
     assert counts[0] < counts[1]
+
+
+def test_rows_past_the_lds_offsets():
+    # 8192 rows (more than the 6000 whose offsets the gather keeps in LDS): the offsets go through
+    # memory; 16 padding rows and audited rows, int64 and int32 slots
+    rng = np.random.default_rng(13)
+    width = 24
+    c = SlotCompactor(width, BLOCK, torch.device("cuda"))
+    rows = 8192
+    lens = rng.integers(1, width * BLOCK + 1, size=rows).tolist()
+    lens[5] = BLOCK  # one block
+    keep = rng.random((rows + 16, width)) < 0.4
+    audited = rng.random(rows) < 0.05
+    for dtype, seed in ((torch.int64, 21), (torch.int32, 22)):
+        print(f"{rows} rows, {dtype}", flush=True)
+        counts = run(c, lens, keep, padding=16, audited=audited, seed=seed, dtype=dtype)
+        assert counts[0] < counts[1]
