@@ -169,7 +169,7 @@ class Step:
         R, W = batch.rows, batch.width
         self.shares = torch.empty(R, W, dtype=torch.float32, device=dev)
         need = int(self.ekv.load().ekv_tile_shares_workspace(R, W, LAYERS))
-        self.shares_ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        self.shares_ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)  # zeroed once
         self.keep = torch.empty(R, W, dtype=torch.uint8, device=dev)
         self.summary = torch.zeros(6, dtype=torch.int64, device=dev)
         self.view = torch.zeros(R, W, dtype=torch.int32, device=dev)

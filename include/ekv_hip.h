@@ -153,10 +153,15 @@ int ekv_tile_shares(const float *lse, int64_t lse_plane_stride, int64_t lse_laye
 /*
  * ekv_tile_shares with a workspace, the same result (the same rules; float sums in another
  * fixed order): each row's layers are split over several workgroups, which write per-block
- * partial sums into the workspace, and a second kernel combines them, so a long row no longer
- * sets the time on one compute unit.  Replaces the same reference code as ekv_tile_shares.
- * workspace: ekv_tile_shares_workspace(nrows, width, layers) bytes of device memory the call
- * may overwrite (no initial contents needed; calls that share one workspace must not overlap).
+ * partial sums into the workspace, so a long row no longer sets the time on one compute unit.
+ * For 4 query rows per block, rows of at most 512 blocks and at most 65536 rows, the last of a
+ * row's workgroups to finish adds the partials and writes the row (it learns that it is last from
+ * a per-row arrival counter in the workspace); other shapes combine them in a second kernel.
+ * Replaces the same reference code as ekv_tile_shares.
+ * workspace: ekv_tile_shares_workspace(nrows, width, layers) bytes of device memory (256 KB of
+ * arrival counters, then the partials).  Fill it with zeros once before its first use; every call
+ * leaves the counters at zero again, for calls of any shape, as long as nothing else writes into
+ * the workspace.  Calls that share one workspace must not overlap.
  */
 size_t ekv_tile_shares_workspace(int32_t nrows, int32_t width, int32_t layers);
 int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
@@ -173,7 +178,8 @@ int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_l
  * No counterpart in the reference: this entry point is for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * A call whose ekv_tile_shares_workspace(nrows, width, layers) exceeds the scratch is refused
- * with EKV_EINVAL (e.g. 128 rows x 512 blocks x 32 layers need 8.4 MB and fit).  Every call on one
+ * with EKV_EINVAL (e.g. 128 rows x 512 blocks x 32 layers need 8.7 MB and fit).  The scratch
+ * starts zeroed, as a workspace must.  Every call on one
  * device uses that device's one scratch: calls that overlap on one device (two streams, two
  * threads, two graphs replayed at once) race and must be ordered by the caller.
  */

@@ -51,6 +51,9 @@ constexpr int kSplitThreads = 256;  // a (row, layer group) per workgroup
 constexpr int kBatch = 8;  // quads (or cells) of each plane in flight per lane
 constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
+constexpr int kWaveLayers = 8;   // the wave form: one layer per wave, 8 waves per workgroup
+constexpr int kMaxArrivalRows = 65536;  // rows whose arrival counters the workspace holds
+constexpr size_t kArrivalBytes = (size_t)kMaxArrivalRows * sizeof(int32_t);
 
 struct Params {
   const float *m;  // plane 0 (or u when from_u)
@@ -65,6 +68,7 @@ struct Params {
   int32_t groups;      // layer groups per row (the split form), 1 otherwise
   float *part;         // split form: [rows][groups][width] partial sums (or maxes)
   int32_t *part_count; // split form: [rows][groups] contributing (layer, query row) pairs
+  int32_t *arrivals;   // wave form: [rows] workgroups of the row done so far (0 between calls)
 };
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -506,6 +510,236 @@ __global__ __launch_bounds__(kSplitThreads) void shares_reg_kernel(const Params 
   }
 }
 
+// Four values per lane reduced over the wave: afterwards lane 16 r holds value r's reduction (and
+// so does every lane of 16-lane row r).  Values 0 and 2, then 1 and 3, trade wave halves
+// (v_permlane32_swap), the two results trade 16-lane rows (v_permlane16_swap), and each row
+// finishes with rotations by 8, 4, 2 and 1 lanes (DPP row_ror), so no value goes through LDS.  The
+// lanes of a row may hold differently rounded sums; callers read lane 16 r.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce4(const float (&v)[4]) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  auto swap = [](float x, float y, auto rows16) {
+    uint32_t xi = __builtin_bit_cast(uint32_t, x), yi = __builtin_bit_cast(uint32_t, y);
+    asm volatile("" : "+v"(xi), "+v"(yi));
+    uint32_t r0, r1;
+    if constexpr (decltype(rows16)::value) {
+      const auto r = __builtin_amdgcn_permlane16_swap(xi, yi, false, false);
+      r0 = r[0];
+      r1 = r[1];
+    } else {
+      const auto r = __builtin_amdgcn_permlane32_swap(xi, yi, false, false);
+      r0 = r[0];
+      r1 = r[1];
+    }
+    asm volatile("" : "+v"(r0), "+v"(r1));
+    return MAX ? fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1))
+               : __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  };
+  // lanes 0-31: value 0 (resp. 1), lanes 32-63: value 2 (resp. 3)
+  const float x = swap(v[0], v[2], std::false_type{});
+  const float y = swap(v[1], v[3], std::false_type{});
+  // row r: value r, over lanes l, l + 16, l + 32, l + 48
+  float z = swap(x, y, std::true_type{});
+  auto ror = [](float a, auto ctrl) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a),
+                                                                 decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  z = op(z, ror(z, std::integral_constant<int, 0x128>{}));
+  z = op(z, ror(z, std::integral_constant<int, 0x124>{}));
+  z = op(z, ror(z, std::integral_constant<int, 0x122>{}));
+  z = op(z, ror(z, std::integral_constant<int, 0x121>{}));
+  return z;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// The wave form for quads of 4 cells and rows of at most 64 S blocks: one pass over memory, and a
+// (layer, query row)'s softmax never leaves its wave.  Wave w of a workgroup takes layer
+// 8 g + w of layer group g of the row; lane i keeps blocks i + 64 s (s < S) of that layer in
+// registers, so the peak and total of each query row are wave reductions (wave_reduce4) and the
+// slots past the row's blocks are skipped by the whole wave.  The layers' per-block shares meet in
+// LDS and are added in layer order.  A row of several groups writes each group's partial to the
+// workspace; the last of the row's workgroups to finish (counted in arrivals[row], which it
+// resets) adds them in group order and writes the row, so no second kernel runs.
+template <int S>
+__global__ __launch_bounds__(kWaveLayers *kWave) __attribute__((amdgpu_waves_per_eu(4)))
+void shares_wave_kernel(const Params p) {
+  constexpr int NW = kWaveLayers, NT = NW * kWave, kSlots = S * kWave;
+  __shared__ float s_part[NW][kSlots];
+  __shared__ int s_count[NW];
+  __shared__ float s_red[NW];
+  __shared__ int s_last;
+  const int out_row = blockIdx.x / p.groups;
+  const int group = blockIdx.x - out_row * p.groups;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = lane_id();
+  const int nl = min(NW, p.layers - group * NW);  // the group's layers
+  const bool mine = wave < nl;                     // this wave has a layer
+  const int src_row = p.row_ids != nullptr ? p.row_ids[out_row] : out_row;
+  const int n_row = p.row_blocks != nullptr ? max(p.row_blocks[out_row], 0) : p.width;
+  const int n = min(n_row, p.width);
+  const RowWeight weight(p, n_row);  // planes of m and l (never u values: those take no workspace)
+  const int64_t base = (int64_t)(group * NW + (mine ? wave : 0)) * p.layer_stride + (int64_t)src_row * p.row_stride;
+
+  // the lane's records; a slot the whole wave has past the row is neither loaded nor used
+  float mv[S][4], wv[S][4];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (mine && s * kWave < n) {
+      const int b = s * kWave + lane;
+      const int64_t at = base + 4 * (int64_t)(b < n ? b : 0);
+      const f32x4_t mq = *reinterpret_cast<const f32x4_t *>(p.m + at);
+      const f32x4_t lq = *reinterpret_cast<const f32x4_t *>(p.l + at);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        mv[s][c] = mq[c];
+        wv[s][c] = lq[c];
+      }
+    }
+  }
+  // weights (0: the record carries none, its m then -inf) and the lane's peak per query row
+  float red[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (mine && s * kWave < n) {
+      const int b = s * kWave + lane;
+      const bool live = b < n;
+      const float tail = b >= weight.tail_start ? weight.tail_mult : 1.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float m = mv[s][c], l = wv[s][c];
+        const bool carries = live && finite(m) && l > 0.0f && l < INFINITY;
+        wv[s][c] = carries ? l * tail : 0.0f;
+        mv[s][c] = carries ? m : -INFINITY;
+        red[c] = mv[s][c] > red[c] ? mv[s][c] : red[c];  // no NaN here: a plain compare
+      }
+    }
+  }
+  float peak[4];
+  int contributors = 0;
+  {
+    float z = wave_reduce4<true>(red);
+    const bool found = z != -INFINITY;
+    z = found ? z : 0.0f;  // a query row with no weight: its terms are w * exp(-inf) = 0
+    const uint64_t rows_found = __ballot(found);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      peak[c] = lane_value(z, 16 * c);
+      contributors += mine ? (int)((rows_found >> (16 * c)) & 1) : 0;
+    }
+  }
+  // each record's term w exp(m - M) replaces its weight; the lane's totals per query row
+#pragma unroll
+  for (int c = 0; c < 4; ++c) red[c] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (mine && s * kWave < n) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float term = wv[s][c] * __expf(mv[s][c] - peak[c]);
+        wv[s][c] = term;
+        red[c] += term;
+      }
+    }
+  }
+  float inv_total[4];
+  {
+    const float z = wave_reduce4<false>(red);
+    const float inv = z > 0.0f ? 1.0f / z : 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) inv_total[c] = lane_value(inv, 16 * c);
+  }
+  // the layer's share of each block, summed (or maxed) over its query rows
+  const bool use_max = p.aggregate == EKV_AGG_MAX;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (mine && s * kWave < n) {
+      float sh;
+      if (use_max) {
+        sh = fmaxf(fmaxf(wv[s][0] * inv_total[0], wv[s][1] * inv_total[1]),
+                   fmaxf(wv[s][2] * inv_total[2], wv[s][3] * inv_total[3]));
+      } else {
+        sh = wv[s][0] * inv_total[0];
+        sh = fmaf(wv[s][1], inv_total[1], sh);
+        sh = fmaf(wv[s][2], inv_total[2], sh);
+        sh = fmaf(wv[s][3], inv_total[3], sh);
+      }
+      s_part[wave][s * kWave + lane] = sh;
+    }
+  }
+  if (lane == 0) s_count[wave] = contributors;
+  __syncthreads();
+
+  // the group's partial of block b = threadIdx.x, over its layers in order
+  const int b = threadIdx.x;
+  float v = 0.0f;
+  if (b < n) {
+    for (int w = 0; w < nl; ++w) v = use_max ? fmaxf(v, s_part[w][b]) : v + s_part[w][b];
+  }
+  int count = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) count += s_count[w];
+
+  if (p.groups > 1) {
+    // The partials and counts cross workgroups (and XCDs) through device-coherent stores and
+    // loads, which pass the per-XCD L2 caches; a fence would instead write back and invalidate
+    // the whole L2 of the XCD.  A workgroup's stores have completed (vmcnt 0) before its arrival
+    // is counted, and the last workgroup loads the others' only after it has seen every arrival.
+    float *part = p.part + (int64_t)out_row * p.groups * p.width;
+    if (b < n) __hip_atomic_store(&part[(int64_t)group * p.width + b], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&p.part_count[(int64_t)out_row * p.groups + group], count, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&p.arrivals[out_row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               p.groups - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(&p.arrivals[out_row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every group's partial, in group order (this group's from registers)
+    float acc = 0.0f;
+    const int own = count;
+    count = 0;
+    for (int g0 = 0; g0 < p.groups; g0 += kBatch) {
+      float x[kBatch];
+      int c[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int g = g0 + k;
+        const bool other = g < p.groups && g != group;
+        x[k] = other && b < n ? __hip_atomic_load(&part[(int64_t)g * p.width + b], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : (g == group ? v : 0.0f);
+        c[k] = other ? __hip_atomic_load(&p.part_count[(int64_t)out_row * p.groups + g], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT)
+                     : (g == group ? own : 0);
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        acc = use_max ? fmaxf(acc, x[k]) : acc + x[k];
+        count += c[k];
+      }
+    }
+    v = acc;
+  }
+  // the whole-row rules: NaN without evidence, the mean over contributing pairs, or the max
+  // renormalised over the row
+  float *out = p.shares + (int64_t)out_row * p.shares_stride;
+  if (count == 0) {
+    if (b < p.width) out[b] = NAN;
+    return;
+  }
+  if (use_max) {
+    const float total = block_sum<NT>(v, s_red);
+    if (b < p.width) out[b] = total > 0.0f ? v / total : 0.0f;
+  } else if (b < p.width) {
+    out[b] = v / (float)count;
+  }
+}
+
 // The split form's second kernel: one workgroup per row combines the row's K partials in group
 // order, then applies the whole-row rules (NaN without evidence, the mean over contributing
 // pairs, or the max renormalised over the row).
@@ -556,10 +790,13 @@ int split_groups(int nrows, int layers) {
   return std::max(1, std::min(want, layers));
 }
 
-// (sized for one group per layer, the most either split form takes)
+// The workspace: the wave form's arrival counters for up to kMaxArrivalRows rows (zero before the
+// first call, and every call leaves them zero), then the partials and their counts, sized for one
+// group per layer, the most any split form takes.  The counters sit at the same place whatever the
+// call's shape, and no call writes partials over them.
 size_t split_workspace(int nrows, int width, int layers) {
   const size_t parts = (size_t)nrows * layers * width * sizeof(float);
-  return ((parts + 255) / 256) * 256 + (size_t)nrows * layers * sizeof(int32_t);
+  return kArrivalBytes + ((parts + 255) / 256) * 256 + (size_t)nrows * layers * sizeof(int32_t);
 }
 
 // the register form's layers per group for J blocks per thread (at most 12 quads of each plane)
@@ -593,8 +830,9 @@ int launch(Params p, int nrows, void *workspace, size_t workspace_bytes, void *s
   const int group_layers = (p.layers + p.groups - 1) / p.groups;  // the largest group
   if (split) {
     const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
-    p.part = (float *)workspace;
-    p.part_count = (int32_t *)((char *)workspace + ((parts + 255) / 256) * 256);
+    p.arrivals = (int32_t *)workspace;
+    p.part = (float *)((char *)workspace + kArrivalBytes);
+    p.part_count = (int32_t *)((char *)p.part + ((parts + 255) / 256) * 256);
   }
   const size_t lds = (size_t)2 * group_layers * cp * sizeof(float);
   const bool aligned = ((uintptr_t)p.m % 16) == 0 && (p.from_u || ((uintptr_t)p.l % 16) == 0) &&
@@ -606,13 +844,26 @@ int launch(Params p, int nrows, void *workspace, size_t workspace_bytes, void *s
   while (lpl > 1 && lpl * group_layers > NT) lpl >>= 1;
   p.lanes_per_layer = std::max(lpl, std::max(cp / 4, 1));
   hipStream_t s = (hipStream_t)stream;
+  if (split && vec && !p.from_u && p.cells == 4 && p.width <= kWaveLayers * kWave && nrows <= kMaxArrivalRows) {
+    // the wave form: one layer per wave, the row's last workgroup combines
+    p.groups = (p.layers + kWaveLayers - 1) / kWaveLayers;
+    const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
+    p.part_count = (int32_t *)((char *)p.part + ((parts + 255) / 256) * 256);
+    const unsigned grid = (unsigned)nrows * (unsigned)p.groups;
+    const dim3 block(kWaveLayers * kWave);
+    if (p.width <= kWave) hipLaunchKernelGGL(shares_wave_kernel<1>, dim3(grid), block, 0, s, p);
+    else if (p.width <= 2 * kWave) hipLaunchKernelGGL(shares_wave_kernel<2>, dim3(grid), block, 0, s, p);
+    else if (p.width <= 4 * kWave) hipLaunchKernelGGL(shares_wave_kernel<4>, dim3(grid), block, 0, s, p);
+    else hipLaunchKernelGGL(shares_wave_kernel<8>, dim3(grid), block, 0, s, p);
+    return check_hip(hipGetLastError(), "tile shares launch");
+  }
   if (split && vec && p.cells == 4 && p.width <= 4 * kSplitThreads) {
     // the register form: one pass, J blocks per thread, reg_layers(J) layers per group
     const int J = (p.width + kSplitThreads - 1) / kSplitThreads;
     const int NLg = reg_layers(J);
     p.groups = (p.layers + NLg - 1) / NLg;
     const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
-    p.part_count = (int32_t *)((char *)workspace + ((parts + 255) / 256) * 256);
+    p.part_count = (int32_t *)((char *)p.part + ((parts + 255) / 256) * 256);
     const unsigned grid = (unsigned)nrows * (unsigned)p.groups;
     switch (J) {
       case 1: hipLaunchKernelGGL((shares_reg_kernel<1, reg_layers(1)>), dim3(grid), dim3(kSplitThreads), 0, s, p); break;

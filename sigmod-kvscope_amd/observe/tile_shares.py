@@ -175,7 +175,8 @@ def tile_shares(
 
     ``row_ids`` / ``row_blocks`` are int32 device tensors (None: every row / full width).  The rows'
     layers are split over several workgroups through a device workspace (``workspace``, a uint8
-    device tensor of at least ``shares_workspace_bytes`` bytes, or one allocated here)."""
+    device tensor of at least ``shares_workspace_bytes`` bytes, zero-filled before its first use and
+    not written by anything else between calls; or one allocated here)."""
     code = _aggregate_code(aggregate)
     n = rows if row_ids is None else int(row_ids.shape[0])
     if out is None:
@@ -188,7 +189,7 @@ def tile_shares(
     layer_stride = rows * width * group_rows
     need = shares_workspace_bytes(n, width, layers)
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=out.device)
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=out.device)
     if workspace.dtype != torch.uint8 or not workspace.is_cuda or workspace.numel() < need:
         raise ValueError(f"workspace must be a uint8 device tensor of at least {need} bytes")
     ekv_hip.call(
@@ -225,21 +226,35 @@ class DeviceTileShareSource:
         local = pid == os.getpid()
         self.base = int(entry["tile_lse_dev"]) if local else cuda.ipc_open(str(entry["tile_lse_ipc"]))  # type: ignore[attr-defined]
         self.table = int(entry["layer_table_dev"]) if local else cuda.ipc_open(str(entry["layer_table_ipc"]))  # type: ignore[attr-defined]
+        # buffers for the most rows a read can ask for, allocated once: every read reuses them
+        self._ids = torch.empty(self.rows, dtype=torch.int32, device="cuda")
+        self._lengths = torch.empty(self.rows, dtype=torch.int32, device="cuda")
+        self._out = torch.empty(self.rows, self.width, dtype=torch.float32, device="cuda")
+        self._staging = torch.empty(2, self.rows, dtype=torch.int32, pin_memory=True)
+        need = shares_workspace_bytes(self.rows, self.width, self.max_layers)
+        self._workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda")
 
     def read(self, live_rows: int, row_blocks: np.ndarray) -> np.ndarray:
         raw = self.cuda.d2h(self.table, self.max_layers * 8)  # type: ignore[attr-defined]
         layers = int(np.count_nonzero(np.frombuffer(raw, dtype=np.uint64)))
         if layers == 0:
             raise RuntimeError("the layer table is empty: the serving process has not filled it")
+        if not 0 <= live_rows <= self.rows:
+            raise ValueError(f"{live_rows} live rows, the plane holds {self.rows}")
         shares = np.full((live_rows, self.width), np.nan)
         wanted = np.flatnonzero(np.asarray(row_blocks[:live_rows]) > 0)
         if wanted.size == 0:
             return shares
-        ids = torch.from_numpy(wanted.astype(np.int32)).cuda()
-        lengths = torch.from_numpy(np.asarray(row_blocks)[wanted].astype(np.int32)).cuda()
-        got = tile_shares(
+        k = int(wanted.size)
+        staged = self._staging.numpy()
+        staged[0, :k] = wanted
+        staged[1, :k] = np.asarray(row_blocks)[wanted]
+        ids, lengths, out = self._ids[:k], self._lengths[:k], self._out[:k]
+        ids.copy_(self._staging[0, :k], non_blocking=True)
+        lengths.copy_(self._staging[1, :k], non_blocking=True)
+        tile_shares(
             self.base, self.max_layers, layers, self.rows, self.width, self.group_rows, ids, lengths,
-            self.tile_blocks, self.aggregate,
+            self.tile_blocks, self.aggregate, out=out, workspace=self._workspace,
         )
-        shares[wanted] = got.cpu().numpy()
+        shares[wanted] = out.cpu().numpy()  # waits for the copies and the kernels
         return shares

@@ -173,3 +173,36 @@ def test_split_form_rejects_a_short_workspace():
     short = torch.empty(need - 1, dtype=torch.uint8, device="cuda")
     with pytest.raises(ValueError):
         tile_shares.tile_shares(dev.data_ptr(), 2, 2, 4, 64, 4, None, None, 2, workspace=short)
+
+
+def test_one_workspace_across_shapes_keeps_its_arrival_counters_zero():
+    # the wave form (4 query rows, rows of at most 512 blocks) counts each row's finished
+    # workgroups in the workspace's first 256 KB and the last one resets the count: one workspace
+    # used for calls of several shapes in a row gives what a fresh workspace gives, and its
+    # counters are zero after every call, including after calls of the other split kernels
+    rng = np.random.default_rng(77)
+    shapes = [(32, 40, 512, 4, "mean"), (9, 100, 64, 4, "max"), (17, 7, 300, 4, "mean"), (5, 11, 300, 5, "mean"),
+              (32, 40, 512, 4, "max"), (3, 9, 700, 4, "mean"), (1, 5, 100, 4, "mean"), (40, 3, 129, 4, "max")]
+    size = max(tile_shares.shares_workspace_bytes(rows, width, layers) for layers, rows, width, _, _ in shapes)
+    workspace = torch.zeros(size, dtype=torch.uint8, device="cuda")
+    for layers, rows, width, cells, aggregate in shapes:
+        m = rng.normal(0, 3, (layers, rows, width, cells)).astype(np.float32)
+        l = rng.uniform(0.5, 30, (layers, rows, width, cells)).astype(np.float32)
+        m[rng.random(m.shape) < 0.03] = -np.inf
+        m[:, rows // 2] = np.nan  # a row without evidence
+        planes = np.stack([m, l])
+        dev = planes_on_device(planes)
+        row_blocks = rng.integers(0, width + 3, size=rows)
+        row_blocks[0] = width
+        blocks = torch.from_numpy(row_blocks.astype(np.int32)).cuda()
+        what = f"{layers} layers x {rows} rows x {width} blocks x {cells} cells, {aggregate}"
+        print(what, flush=True)
+        reused = tile_shares.tile_shares(dev.data_ptr(), layers, layers, rows, width, cells, None, blocks, 2,
+                                         aggregate, workspace=workspace)
+        fresh = tile_shares.tile_shares(dev.data_ptr(), layers, layers, rows, width, cells, None, blocks, 2,
+                                        aggregate)
+        torch.cuda.synchronize()
+        assert torch.equal(torch.nan_to_num(reused, nan=-1.0), torch.nan_to_num(fresh, nan=-1.0)), what
+        assert int(torch.count_nonzero(workspace[: 256 * 1024])) == 0, what
+        want = ots.normalize(ots.read_rows(planes, layers, np.arange(rows), 2), row_blocks, 2, aggregate)
+        assert_close(reused.cpu().numpy().astype(np.float64), want, what=what)

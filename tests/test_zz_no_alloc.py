@@ -36,7 +36,7 @@ def call_both(planes, layers, row_ids, row_blocks, tile, aggregate):
     with_ws = torch.full((n, width), 7.0, dtype=torch.float32, device="cuda")
     no_alloc = torch.full((n, width), -7.0, dtype=torch.float32, device="cuda")
     need = int(ekv_hip.load().ekv_tile_shares_workspace(n, width, layers))
-    workspace = torch.empty(need, dtype=torch.uint8, device="cuda")
+    workspace = torch.zeros(need, dtype=torch.uint8, device="cuda")  # zeroed before its first use
     stream = ekv_hip.stream_handle()
     ekv_hip.call("ekv_tile_shares_ws", *common, with_ws.data_ptr(), width, workspace.data_ptr(), need, stream)
     ekv_hip.call("ekv_tile_shares_noalloc", *common, no_alloc.data_ptr(), width, stream)
