@@ -28,6 +28,7 @@
 // clamp(s) / total (1 / n when total <= 0; NaN last), 64 bits wide, selected 8 bits a pass.
 #pragma clang fp contract(off)
 
+#include <limits.h>
 #include <math.h>
 
 #include <type_traits>
@@ -597,6 +598,11 @@ __device__ __forceinline__ void load_scores_run(const Params &p, int row, int n,
     for (int g = 0; g < PER / 4; ++g) {
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
       if (b0 + 4 * g < n) v = *reinterpret_cast<const uint4 *>(srow + b0 + 4 * g);
+      if (b0 + 4 * g + 4 > n) {  // the group the row ends in: the blocks past it read as 0
+        v.y = b0 + 4 * g + 1 < n ? v.y : 0u;
+        v.z = b0 + 4 * g + 2 < n ? v.z : 0u;
+        v.w = b0 + 4 * g + 3 < n ? v.w : 0u;
+      }
       key[4 * g] = v.x;
       key[4 * g + 1] = v.y;
       key[4 * g + 2] = v.z;
@@ -630,185 +636,113 @@ __device__ __forceinline__ void block_sums_n(T (&v)[N], T (*scratch)[NT / kWave]
   __syncthreads();
 }
 
-template <int PER>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void rank_view_kernel(
-    const Params p) {
-  // the row's keys during the select, then the view row being assembled
-  __shared__ uint32_t s_row[PER * kThreads];
-  int32_t *s_out = reinterpret_cast<int32_t *>(s_row);
-  __shared__ int s_red[5][kWaves];
-  __shared__ int s_hist[2][256];
-  __shared__ int s_scan[kWaves];
-  __shared__ int s_digit, s_krem, s_whole;
+// bits [0, k) of a word (k clipped to [0, 32]), and bits [lo, hi)
+__device__ __forceinline__ uint32_t bits_below(int k) { return k <= 0 ? 0u : (k >= 32 ? ~0u : (1u << k) - 1u); }
+__device__ __forceinline__ uint32_t bit_range(int lo, int hi) { return bits_below(hi) & ~bits_below(lo); }
 
-  const int row = blockIdx.x;
+// max of an int over a wave (signed or as unsigned), every lane receiving it: DPP within each
+// 16-lane row, then the four rows' lanes 0
+template <bool SIGNED>
+__device__ __forceinline__ int wave_max_int(int v) {
+  auto mx = [](int a, int b) { return SIGNED ? max(a, b) : (int)max((uint32_t)a, (uint32_t)b); };
+  v = mx(v, dpp_move<0xB1>(v));
+  v = mx(v, dpp_move<0x4E>(v));
+  v = mx(v, dpp_move<0x124>(v));
+  v = mx(v, dpp_move<0x128>(v));
+  return mx(mx(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+            mx(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// The budget of the controller's rule over every row taking part (controller.py:435-437,
+// allocation.py:64-67), from the rows' block counts.
+struct Budget {
+  long long total, floor_pins, sizes, open_total, nreq, budget, free_blocks;
+  bool error, keep_all;
+};
+
+// The quota of one row: largest remainder in IEEE double (allocation.py:79-86).
+struct Quota {
+  long long open, floor;
+  double frac;
+};
+
+__device__ __forceinline__ Quota quota_of(const Budget &bg, const RowInfo &me) {
+  Quota q;
+  q.open = me.exist - me.pinned;
+  const double exact = bg.open_total > 0 ? (double)(bg.free_blocks * q.open) / (double)bg.open_total : 0.0;
+  q.floor = (long long)exact;
+  q.frac = exact - (double)q.floor;
+  return q;
+}
+
+// The key mode of a row's shares (allocation.py:46-52) from two maxima over its live scores (0 past
+// the row): of the bits without the sign, above +inf's 0x7f800000 only for a NaN, and of the bits as
+// a signed int, which is +inf's at most without a NaN and above 0 for a positive score.
+// 0: all tie, 1: by value, 2: +inf last.
+__device__ __forceinline__ int key_mode(uint32_t mag, int sgn) {
+  return mag > 0x7f800000u ? 0 : (sgn == 0x7f800000 ? 2 : (sgn > 0 ? 1 : 0));
+}
+
+// One row's keep (the quota's best open blocks) and its view, from the raw score bits and the
+// table run the thread holds: the radix select over the keys in LDS, the keep bytes, then
+// compact_block_table (runtime/block_view.py:36-56) on that keep, the row assembled in the same LDS.
+template <int PER>
+__device__ __forceinline__ void keep_and_view(const Params &p, int row, const RowInfo &me, int L,
+                                              const uint32_t (&key)[PER], const int32_t (&entry)[PER],
+                                              bool decide, long long quota, int mode, uint32_t *s_row,
+                                              int *s_hist, int *s_scan, int *s_sel) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
   const int W = p.width;
   const int b0 = tid * PER;
-
-  // ---- the row's counts and token length, every row's counts for the budget, then the row's
-  // live scores ---------------------------------------------------------------------------------
-  const RowInfo me = row_info(p, row);
-  const int L = p.seq_lens[row];
-  constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
-  int open_reg[kRegRows];
-  int t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
-#pragma unroll
-  for (int i = 0; i < kRegRows; ++i) {
-    const int r = tid + i * kThreads;
-    open_reg[i] = -1;  // not taking part
-    if (r < p.rows) {
-      const RowInfo ri = row_info(p, r);
-      if (ri.part) {
-        t5[0] += ri.n;
-        t5[1] += ri.pinned;
-        t5[2] += ri.exist;
-        t5[3] += ri.exist - ri.pinned;
-        t5[4] += 1;
-        open_reg[i] = ri.exist - ri.pinned;
-      }
-    }
-  }
-  const int n = __builtin_amdgcn_readfirstlane(me.n);
-  uint32_t key[PER];  // the raw score bits
-  load_scores_run<PER>(p, row, n, key);
-  for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
-    const RowInfo ri = row_info(p, r);
-    if (!ri.part) continue;
-    t5[0] += ri.n;
-    t5[1] += ri.pinned;
-    t5[2] += ri.exist;
-    t5[3] += ri.exist - ri.pinned;
-    t5[4] += 1;
-  }
-  block_sums_n<kThreads>(t5, s_red);
-  const long long total = t5[0], floor_pins = t5[1], sizes = t5[2], open_total = t5[3], nreq = t5[4];
-  long long budget = p.budget_in;
-  if (budget < 0) {  // controller.py:435-437
-    const long long want = (long long)ceil(p.fraction * (double)total);
-    budget = want > floor_pins ? want : floor_pins;
-  }
-  const bool error = floor_pins > budget && budget < sizes;  // allocation.py:64-65
-  const bool keep_all = budget >= sizes;                      // allocation.py:66-67
-  const long long free_blocks = budget - floor_pins;
-  if (row == 0 && tid == 0 && p.summary != nullptr) {
-    p.summary[0] = budget;
-    p.summary[1] = total;
-    p.summary[2] = floor_pins;
-    p.summary[3] = error ? 1 : 0;
-    p.summary[4] = nreq;
-    p.summary[5] = free_blocks;
-  }
-
-  // open blocks: existing (every block below n) and not pinned (block 0, blocks >= pin_at)
-  uint32_t open_bits = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int b = b0 + i;
-    open_bits |= (b < n && b != 0 && b < me.pin_at) ? (1u << i) : 0u;
-  }
+  // open blocks: existing (every block below n) and not pinned (block 0, blocks >= pin_at <= n);
+  // the thread's run is contiguous, so they are one range of its bits
+  const uint32_t open_bits = bit_range(max(1, b0) - b0, min(me.pin_at - b0, PER));
   uint32_t keep_bits = ~0u;  // rows without evidence read in full, controller.py:401
-  int32_t entry[PER];        // the table run
-  if (!me.part || error) {
-    load_run<PER>(p, row, entry);
-  } else {
-    // the key mode's counts from the scores in registers; the scores then wait in LDS (slot i of
-    // thread t at i * kThreads + t: lane-consecutive, free of bank conflicts), and the table run
-    // is requested once they are there, to arrive during the select
-    int nan_c = 0, inf_c = 0, pos_c = 0;  // key mode of the row's shares: allocation.py:46-52
+  if (decide) {
+    // keys, larger first: an open block's is at least 1 (by value: the score's bits + 1 for a
+    // positive score, else 1; inf last: 1 for +inf, else 2; tie: 1), a closed block's is 0, the
+    // smallest, which the select never reaches (the quota is below the open count).  Slot i of
+    // thread t sits at i * kThreads + t: lane-consecutive, free of bank conflicts.
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const float s = __builtin_bit_cast(float, key[i]);
-      const bool live = b0 + i < n;
-      nan_c += (live && __builtin_isnan(s)) ? 1 : 0;
-      inf_c += (live && __builtin_isinf(s) && s > 0.0f) ? 1 : 0;
-      pos_c += (live && s > 0.0f) ? 1 : 0;
-      s_row[i * kThreads + tid] = key[i];
+      uint32_t k;
+      if (mode == 1) k = (uint32_t)max((int)key[i], 0) + 1u;
+      else if (mode == 2) k = key[i] == 0x7f800000u ? 1u : 2u;
+      else k = 1u;
+      s_row[i * kThreads + tid] = ((open_bits >> i) & 1u) ? k : 0u;
     }
-    // ---- this row's quota: largest remainder in IEEE double, allocation.py:79-86 -------------
-    const long long my_open = me.exist - me.pinned;
-    const double my_exact = open_total > 0 ? (double)(free_blocks * my_open) / (double)open_total : 0.0;
-    const long long my_floor = (long long)my_exact;
-    const double my_frac = my_exact - (double)my_floor;
-    // [0] floors, [1] rows ahead in the leftover order, [2] [3] counts of the row's blocks in
-    // 16-bit fields: NaN, +inf and positive scores, and open blocks (int sums: the floors add up
-    // to at most the budget)
-    int q4[4] = {0, 0, nan_c + (inf_c << 16), pos_c + ((int)__popc(open_bits) << 16)};
-    if (!keep_all) {
-      auto visit = [&](int r, int open) {
-        const double exact = open_total > 0 ? (double)(free_blocks * open) / (double)open_total : 0.0;
-        const int fl = (int)exact;
-        const double frac = exact - (double)fl;
-        q4[0] += fl;
-        q4[1] += (frac > my_frac || (frac == my_frac && r < row)) ? 1 : 0;
-      };
-#pragma unroll
-      for (int i = 0; i < kRegRows; ++i)
-        if (open_reg[i] >= 0) visit(tid + i * kThreads, open_reg[i]);
-      for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
-        const RowInfo ri = row_info(p, r);
-        if (ri.part) visit(r, ri.exist - ri.pinned);
-      }
-    }
-    block_sums_n<kThreads>(q4, s_red);
-    load_run<PER>(p, row, entry);  // after the barriers: with the scores still in flight it would not fit
-    long long quota;
-    if (keep_all) {
-      quota = my_open;
-    } else {
-      const long long leftover = free_blocks - q4[0];
-      quota = my_floor + (q4[1] < leftover ? 1 : 0);
-    }
-    const int has_nan = q4[2] & 0xffff, has_inf = (q4[2] >> 16) & 0xffff, has_pos = q4[3] & 0xffff;
-    const int open_count = (q4[3] >> 16) & 0xffff;
-    const int mode = has_nan ? 0 : (has_inf ? 2 : (has_pos ? 1 : 0));  // 0 tie, 1 by value, 2 inf last
-
-    // keys of the open blocks (order-preserving, larger first), ~0 elsewhere; each thread
-    // rewrites its own slots
-    constexpr uint32_t kClosedKey = ~0u;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint32_t bits = s_row[i * kThreads + tid];
-      const float s = __builtin_bit_cast(float, bits);
-      uint32_t k = kClosedKey;
-      if ((open_bits >> i) & 1u) {
-        if (mode == 1) k = s > 0.0f ? bits : 0u;
-        else if (mode == 2) k = (__builtin_isinf(s) && s > 0.0f) ? 0u : 1u;
-        else k = 0u;
-      }
-      s_row[i * kThreads + tid] = k;
-    }
+    const int open_count = (int)(me.exist - me.pinned);
     uint32_t open_keep = 0;
     if (quota >= open_count) {
       open_keep = ~0u;
     } else if (quota > 0) {
-      // radix select of the quota-th largest key, 8 bits at a time from the top; the histogram is
-      // double-buffered, and the select stops once the quota ends at the end of a digit's bucket
+      // radix select of the quota-th largest key, 8 bits at a time from the top; wave 0 scans the
+      // counts and clears them for the next pass, and the select stops once the quota ends at the
+      // end of a digit's bucket.  Closed blocks (key 0) only ever count in the lowest buckets.
       uint32_t prefix = 0, mask = 0;
       int k_rem = (int)quota;
       bool whole = false;
-      if (tid < 256) s_hist[0][tid] = 0;
-      __syncthreads();
+      const int copy = lane & 3;
 #pragma unroll 1
       for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
-        int *hist = s_hist[pass & 1];
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const uint32_t k = s_row[i * kThreads + tid];
-          if (k != kClosedKey && (k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1);
+          if ((k & mask) == prefix) atomicAdd(&s_hist[((k >> shift) & 255) * 4 + copy], 1);
         }
-        if (tid < 256) s_hist[(pass & 1) ^ 1][tid] = 0;
         __syncthreads();
         if (wave == 0) {
           // lane l holds digits 255 - 4l .. 252 - 4l; a scan over the lanes counts the keys above
           int c[4], s4 = 0;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            c[j] = hist[255 - 4 * lane - j];
+            const int4 h4 = *reinterpret_cast<const int4 *>(&s_hist[4 * (255 - 4 * lane - j)]);
+            c[j] = h4.x + h4.y + h4.z + h4.w;
             s4 += c[j];
+            asm volatile("" ::: "memory");  // one bin's copies in registers at a time
           }
           const int inc = wave_inclusive_scan(s4);
           int acc = inc - s4;
@@ -816,36 +750,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               if (acc < k_rem && acc + c[j] >= k_rem) {
-                s_digit = 255 - 4 * lane - j;
-                s_krem = k_rem - acc;
-                s_whole = acc + c[j] == k_rem ? 1 : 0;
+                s_sel[0] = 255 - 4 * lane - j;
+                s_sel[1] = k_rem - acc;
+                s_sel[2] = acc + c[j] == k_rem ? 1 : 0;
               }
               acc += c[j];
             }
           }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)  // cleared for the next pass
+            *reinterpret_cast<int4 *>(&s_hist[4 * (255 - 4 * lane - j)]) = make_int4(0, 0, 0, 0);
         }
         __syncthreads();
-        prefix |= (uint32_t)s_digit << shift;
+        prefix |= (uint32_t)s_sel[0] << shift;
         mask |= 255u << shift;
-        k_rem = s_krem;
-        whole = __builtin_amdgcn_readfirstlane(s_whole) != 0;
+        k_rem = s_sel[1];
+        whole = __builtin_amdgcn_readfirstlane(s_sel[2]) != 0;
         if (whole) break;
       }
       if (whole) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const uint32_t k = s_row[i * kThreads + tid];
-          open_keep |= (k != kClosedKey && (k & mask) >= prefix) ? (1u << i) : 0u;
+          open_keep |= (k != 0u && (k & mask) >= prefix) ? (1u << i) : 0u;
         }
       } else {
-        // every key above the threshold and the first k_rem equal keys by block index: the equal
-        // keys before a thread's run are one scan of the threads' counts
+        // every key above the threshold (at least 1: closed keys are below it) and the first k_rem
+        // equal keys by block index: the equal keys before a thread's run are one scan of the
+        // threads' counts
         uint32_t eq_bits = 0, above_bits = 0;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const uint32_t k = s_row[i * kThreads + tid];
           eq_bits |= k == prefix ? (1u << i) : 0u;
-          above_bits |= (k != kClosedKey && k > prefix) ? (1u << i) : 0u;
+          above_bits |= k > prefix ? (1u << i) : 0u;
         }
         int eq_total;
         int before = block_exclusive_scan<kThreads>(__popc(eq_bits), s_scan, eq_total);
@@ -876,15 +814,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
   __syncthreads();  // every key is read before the view row overwrites them
 
   // ---- compact_block_table (runtime/block_view.py:36-56) of the row on that keep ------------
+  int32_t *s_out = reinterpret_cast<int32_t *>(s_row);
   const int bs = p.block_size;
   const long long n64 = L > 0 ? ((long long)L + bs - 1) / bs : 0;  // block_view.py:49
   const int nv = n64 > W + 1LL ? W + 1 : (int)n64;
-  uint32_t kept_bits = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int b = b0 + i;
-    kept_bits |= (b < W && (((keep_bits >> i) & 1u) || b == 0 || b == nv - 1) && b < nv) ? (1u << i) : 0u;
-  }
+  // keep' = (keep | b == 0 | b == nv - 1) & b < min(nv, W), as bits of the thread's run
+  const int last_at = nv - 1 - b0;
+  const uint32_t kept_bits = (keep_bits | (b0 == 0 ? 1u : 0u) | (last_at >= 0 && last_at < PER ? 1u << last_at : 0u)) &
+                             bits_below(min(min(nv, W) - b0, PER));
   int total_kept;
   int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
 #pragma unroll
@@ -923,6 +860,159 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
   }
 }
 
+// The quota sums of the view build in one pass over the workgroup: v[0 .. NS) summed, then pairs of
+// (largest as unsigned, largest as signed).
+template <int N, int NS>
+__device__ __forceinline__ void quota_reduce(int (&v)[N], int (*scratch)[kWaves]) {
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    if (j < NS) v[j] = wave_sum_int(v[j]);
+    else if ((j - NS) % 2 == 0) v[j] = wave_max_int<false>(v[j]);
+    else v[j] = wave_max_int<true>(v[j]);
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) scratch[j][wave] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    int r = j < NS ? 0 : ((j - NS) % 2 == 0 ? 0 : INT_MIN);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int x = scratch[j][w];
+      if (j < NS) r += x;
+      else if ((j - NS) % 2 == 0) r = (int)max((uint32_t)r, (uint32_t)x);
+      else r = max(r, x);
+    }
+    v[j] = r;
+  }
+  __syncthreads();
+}
+
+// The uniform ranking and the view in one kernel, one row per workgroup (four per compute unit, 64
+// registers a thread).  Every workgroup computes the budget from all rows' counts and its row's quota
+// from all rows' open counts (the rows' floors and their order by remainder), then decides and
+// compacts its row, the keys in LDS.  The decisions are those of rank_kernel<PER, true>.  (Two rows
+// per workgroup, both rows' scores and table runs requested at entry so that the second row's data
+// streams in while the first is decided, took 40.5 us against 33.6 us at 1024 rows x 8192 blocks:
+// at two workgroups per compute unit the select's barriers and LDS atomics stall the CU.)
+template <int PER>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void rank_view_kernel(
+    const Params p) {
+  // the row's keys during the select, then the view row being assembled
+  __shared__ uint32_t s_row[PER * kThreads];
+  __shared__ int s_red[5][kWaves];
+  // the select's digit counts: four copies of each bin side by side (bin * 4 + lane % 4), so that
+  // the lanes of one instruction that share a digit add to four words, not one
+  __shared__ __align__(16) int s_hist[256 * 4];
+  __shared__ int s_scan[kWaves];
+  __shared__ int s_sel[3];  // the select's digit, remaining count and whether the bucket ends it
+
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  if (tid < 256) *reinterpret_cast<int4 *>(&s_hist[4 * tid]) = make_int4(0, 0, 0, 0);  // seen after the first barrier
+
+  // ---- the row's counts and token length, every row's counts for the budget, then the row's
+  // live scores ---------------------------------------------------------------------------------
+  const RowInfo me = row_info(p, row);
+  const int L = p.seq_lens[row];
+  constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
+  int open_reg[kRegRows];
+  int t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
+#pragma unroll
+  for (int i = 0; i < kRegRows; ++i) {
+    const int r = tid + i * kThreads;
+    open_reg[i] = -1;  // not taking part
+    if (r < p.rows) {
+      const RowInfo ri = row_info(p, r);
+      if (ri.part) {
+        t5[0] += ri.n;
+        t5[1] += ri.pinned;
+        t5[2] += ri.exist;
+        t5[3] += ri.exist - ri.pinned;
+        t5[4] += 1;
+        open_reg[i] = ri.exist - ri.pinned;
+      }
+    }
+  }
+  uint32_t key[PER];  // the raw score bits
+  load_scores_run<PER>(p, row, __builtin_amdgcn_readfirstlane(me.n), key);
+  for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
+    const RowInfo ri = row_info(p, r);
+    if (!ri.part) continue;
+    t5[0] += ri.n;
+    t5[1] += ri.pinned;
+    t5[2] += ri.exist;
+    t5[3] += ri.exist - ri.pinned;
+    t5[4] += 1;
+  }
+  block_sums_n<kThreads>(t5, s_red);
+  Budget bg;
+  bg.total = t5[0];
+  bg.floor_pins = t5[1];
+  bg.sizes = t5[2];
+  bg.open_total = t5[3];
+  bg.nreq = t5[4];
+  bg.budget = p.budget_in;
+  if (bg.budget < 0) {  // controller.py:435-437
+    const long long want = (long long)ceil(p.fraction * (double)bg.total);
+    bg.budget = want > bg.floor_pins ? want : bg.floor_pins;
+  }
+  bg.error = bg.floor_pins > bg.budget && bg.budget < bg.sizes;  // allocation.py:64-65
+  bg.keep_all = bg.budget >= bg.sizes;                            // allocation.py:66-67
+  bg.free_blocks = bg.budget - bg.floor_pins;
+  if (blockIdx.x == 0 && tid == 0 && p.summary != nullptr) {
+    p.summary[0] = bg.budget;
+    p.summary[1] = bg.total;
+    p.summary[2] = bg.floor_pins;
+    p.summary[3] = bg.error ? 1 : 0;
+    p.summary[4] = bg.nreq;
+    p.summary[5] = bg.free_blocks;
+  }
+
+  // ---- the row's quota and key mode ----------------------------------------------------------
+  const bool decide = me.part && !bg.error;
+  const Quota q = quota_of(bg, me);
+  // [0] floors of every row, [1] rows ahead of this one in the leftover order (int sums: the floors
+  // add up to at most the budget), [2] [3] the two maxima of the key mode
+  int qs[4] = {0, 0, 0, 0};
+  if (decide && !bg.keep_all) {
+    auto visit = [&](int r, int open) {
+      const double exact = bg.open_total > 0 ? (double)(bg.free_blocks * open) / (double)bg.open_total : 0.0;
+      const int fl = (int)exact;
+      const double frac = exact - (double)fl;
+      qs[0] += fl;
+      qs[1] += (frac > q.frac || (frac == q.frac && r < row)) ? 1 : 0;
+    };
+#pragma unroll
+    for (int i = 0; i < kRegRows; ++i)
+      if (open_reg[i] >= 0) visit(tid + i * kThreads, open_reg[i]);
+    for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
+      const RowInfo ri = row_info(p, r);
+      if (ri.part) visit(r, ri.exist - ri.pinned);
+    }
+  }
+  {
+    uint32_t mag = 0;
+    int sgn = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      mag = max(mag, key[i] & 0x7fffffffu);
+      sgn = max(sgn, (int)key[i]);
+    }
+    qs[2] = (int)mag;
+    qs[3] = sgn;
+  }
+  quota_reduce<4, 2>(qs, s_red);
+  int32_t entry[PER];  // the table run
+  load_run<PER>(p, row, entry);  // after the barriers: with the scores in flight it would not fit
+  const long long leftover = bg.free_blocks - qs[0];
+  const long long quota = bg.keep_all ? q.open : q.floor + (qs[1] < leftover ? 1 : 0);
+  keep_and_view<PER>(p, row, me, L, key, entry, decide, quota, key_mode((uint32_t)qs[2], qs[3]), s_row, s_hist,
+                     s_scan, s_sel);
+}
 
 // ---------------------------------------------------------------------------------------
 // Rows wider than a row in registers (width > kMaxWidth): one 1024-thread workgroup per row

@@ -151,3 +151,35 @@ def test_special_scores_fused(width):
     assert np.array_equal(keep, want_keep)
     want_view, want_lens = obv.compact(table, lens, want_keep.astype(bool), bs)
     assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens)
+
+
+@pytest.mark.parametrize("rows,width", [(1025, 300), (1500, 1000), (1031, 8192)])
+def test_more_rows_than_workgroups_fit_at_once(rows, width):
+    # batches past four rows per compute unit (the workgroups run in more than one round), with
+    # special scores (NaN: all tie, +inf last, all zero, all negative), rows that do not take part,
+    # explicit pin starts and an exact budget, against the two calls and the oracle's compaction
+    rng = np.random.default_rng(rows + width)
+    bs = 16
+    blocks = rng.integers(0, width + 1, size=rows).astype(np.int32)
+    blocks[:3] = [0, width, 1]
+    blocks[-1] = width
+    lens = (blocks.astype(np.int64) * bs - rng.integers(0, bs, size=rows)).clip(0).astype(np.int32)
+    lens[3] = 0
+    lens[4] = (width + 3) * bs
+    scores = rng.random((rows, width), dtype=np.float32)
+    scores[5, width // 3] = np.nan  # all tie
+    scores[6, : width // 2] = np.inf  # +inf last
+    scores[7] = 0.0
+    scores[8] = -scores[8]
+    scores[rows // 2 + 1, : width // 2] = 0.25  # ties go to the lower block
+    table = rng.integers(0, 1 << 30, size=(rows, width)).astype(np.int32)
+    measured = (rng.random(rows) < 0.9).astype(np.uint8)
+    pin_from = rng.integers(0, width + 1, size=rows).astype(np.int32)
+    dev = {k: torch.from_numpy(v).cuda() for k, v in
+           dict(scores=scores, blocks=blocks, table=table, lens=lens, measured=measured, pin_from=pin_from).items()}
+    print(f"{rows} rows x {width} blocks", flush=True)
+    for kw in (dict(fraction=0.5), dict(fraction=0.3, recent_blocks=2, measured=dev["measured"]),
+               dict(budget=int(blocks.sum()) // 3, pin_from=dev["pin_from"])):
+        keep, summary, view, view_lens = both(dev["scores"], dev["blocks"], dev["table"], dev["lens"], bs, **kw)
+        want_view, want_lens = obv.compact(table, lens, keep.astype(bool), bs)
+        assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens), kw
