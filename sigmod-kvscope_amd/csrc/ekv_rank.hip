@@ -102,6 +102,18 @@ __device__ __forceinline__ RowInfo row_info(const Params &p, int r) {
   return ri;
 }
 
+// row_info from a row's loaded values, without explicit masks: its block count, whether it is
+// measured, and its pin start (INT_MAX: none)
+__device__ __forceinline__ RowInfo row_info_of(const Params &p, int blocks, bool measured, int pin_from) {
+  RowInfo ri;
+  ri.n = min(max(blocks, 0), p.width);
+  ri.part = measured && ri.n > 0;
+  ri.pin_at = min(max(0, ri.n - 1 - p.recent), min(max(pin_from, 0), ri.n));  // controller.py:422-424
+  ri.exist = ri.n;
+  ri.pinned = ri.n == 0 ? 0 : (ri.n - ri.pin_at) + (ri.pin_at > 0 ? 1 : 0);
+  return ri;
+}
+
 __device__ __forceinline__ bool is_pinned(const Params &p, const RowInfo &ri, int r, int b) {
   if (p.pinned != nullptr) return p.pinned[(int64_t)r * p.pinned_stride + b] != 0;
   return b == 0 || b >= ri.pin_at;
@@ -596,21 +608,19 @@ __device__ __forceinline__ void load_scores_run(const Params &p, int row, int n,
   if (b0 + PER <= p.width && ((uintptr_t)(srow + b0) & 15) == 0) {
 #pragma unroll
     for (int g = 0; g < PER / 4; ++g) {
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (b0 + 4 * g < n) v = *reinterpret_cast<const uint4 *>(srow + b0 + 4 * g);
-      if (b0 + 4 * g + 4 > n) {  // the group the row ends in: the blocks past it read as 0
-        v.y = b0 + 4 * g + 1 < n ? v.y : 0u;
-        v.z = b0 + 4 * g + 2 < n ? v.z : 0u;
-        v.w = b0 + 4 * g + 3 < n ? v.w : 0u;
-      }
+      // a group past the row reads the row's first group instead (in range, no branch to wait in)
+      const uint4 v = *reinterpret_cast<const uint4 *>(srow + (b0 + 4 * g < n ? b0 + 4 * g : 0));
       key[4 * g] = v.x;
       key[4 * g + 1] = v.y;
       key[4 * g + 2] = v.z;
       key[4 * g + 3] = v.w;
     }
   } else {
+    // the run's own entries, clipped to the row's last (block 0 for an empty row)
+    const float *run = srow + min(b0, max(n - 1, 0));
+    const int last = max(n - 1 - b0, 0);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) key[i] = b0 + i < n ? __builtin_bit_cast(uint32_t, srow[b0 + i]) : 0u;
+    for (int i = 0; i < PER; ++i) key[i] = __builtin_bit_cast(uint32_t, run[min(i, last)]);
   }
 }
 
@@ -807,9 +817,11 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
       *reinterpret_cast<uint32_t *>(keep_row + b0 + 4 * g) = k4;
     }
   } else {
+    uint8_t *run = keep_row + b0;
+    const int in_row = W - b0;
 #pragma unroll
     for (int i = 0; i < PER; ++i)
-      if (b0 + i < W) keep_row[b0 + i] = (keep_bits >> i) & 1u;
+      if (i < in_row) run[i] = (keep_bits >> i) & 1u;
   }
   __syncthreads();  // every key is read before the view row overwrites them
 
@@ -918,27 +930,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
   // live scores ---------------------------------------------------------------------------------
   const RowInfo me = row_info(p, row);
   const int L = p.seq_lens[row];
+  // the counts of rows tid and tid + kThreads, then the row's scores: every load in flight at once
+  // (a load behind a null test of its array would be waited for before the next is issued)
   constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
+  // Every load is unconditional (an absent array is read through the block counts, in range, and
+  // ignored), so none waits inside a branch.
+  const uint8_t *measured = p.measured != nullptr ? p.measured : reinterpret_cast<const uint8_t *>(p.blocks);
+  const int32_t *pin_from = p.pin_from != nullptr ? p.pin_from : p.blocks;
+  int nb[kRegRows], pf[kRegRows], ms[kRegRows];
+#pragma unroll
+  for (int i = 0; i < kRegRows; ++i) {
+    const int r = min(tid + i * kThreads, p.rows - 1);
+    nb[i] = p.blocks[r];
+    ms[i] = measured[r];
+    pf[i] = pin_from[r];
+  }
+  uint32_t key[PER];  // the raw score bits (past the row: whatever the row holds there)
+  load_scores_run<PER>(p, row, __builtin_amdgcn_readfirstlane(me.n), key);
   int open_reg[kRegRows];
   int t5[5] = {0, 0, 0, 0, 0};  // total, floor_pins, sizes, open_total, requests
 #pragma unroll
   for (int i = 0; i < kRegRows; ++i) {
-    const int r = tid + i * kThreads;
+    const bool in = tid + i * kThreads < p.rows;
+    const RowInfo ri = row_info_of(p, in ? nb[i] : 0, p.measured == nullptr || ms[i] != 0,
+                                   p.pin_from != nullptr ? pf[i] : INT_MAX);
     open_reg[i] = -1;  // not taking part
-    if (r < p.rows) {
-      const RowInfo ri = row_info(p, r);
-      if (ri.part) {
-        t5[0] += ri.n;
-        t5[1] += ri.pinned;
-        t5[2] += ri.exist;
-        t5[3] += ri.exist - ri.pinned;
-        t5[4] += 1;
-        open_reg[i] = ri.exist - ri.pinned;
-      }
+    if (ri.part) {
+      t5[0] += ri.n;
+      t5[1] += ri.pinned;
+      t5[2] += ri.exist;
+      t5[3] += ri.exist - ri.pinned;
+      t5[4] += 1;
+      open_reg[i] = ri.exist - ri.pinned;
     }
   }
-  uint32_t key[PER];  // the raw score bits
-  load_scores_run<PER>(p, row, __builtin_amdgcn_readfirstlane(me.n), key);
   for (int r = tid + kRegRows * kThreads; r < p.rows; r += kThreads) {
     const RowInfo ri = row_info(p, r);
     if (!ri.part) continue;
@@ -997,10 +1022,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
   {
     uint32_t mag = 0;
     int sgn = 0;
+    const int live = me.n - tid * PER;  // the thread's live slots
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      mag = max(mag, key[i] & 0x7fffffffu);
-      sgn = max(sgn, (int)key[i]);
+      const uint32_t k = i < live ? key[i] : 0u;
+      mag = max(mag, k & 0x7fffffffu);
+      sgn = max(sgn, (int)k);
     }
     qs[2] = (int)mag;
     qs[3] = sgn;
