@@ -290,6 +290,7 @@ int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_
  * may be NULL): budget, blocks of all rows, pinned blocks, status (1: the budget is below the
  * pinned blocks -- the reference raises ValueError -- and every block is kept), requests, free.
  * workspace: ekv_rank_sum_workspace(rows) bytes of device memory the call may overwrite.
+ * rows at most 65535, width at most 262144 (every pass streams the rows from memory).
  */
 size_t ekv_rank_sum_workspace(int32_t rows);
 int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blocks, const double *weights,
@@ -326,7 +327,7 @@ int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *
  * past the row and in every row that takes no part.  summary (int64[6], may be NULL): budget, blocks
  * of the requests, pinned blocks, status, requests, free.  workspace:
  * ekv_controller_keep_workspace(objective, rows, width) bytes the call may overwrite.  rows at most
- * 65535 (`sum`) or 8192 (`maxmin`), width at most 12288.
+ * 65535 (`sum`) or 8192 (`maxmin`), width at most 262144 (`sum`) or 12288 (`maxmin`).
  */
 size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width);
 int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,

@@ -42,7 +42,8 @@ namespace ekv {
 namespace alloc {
 
 constexpr int kThreads = 256;
-constexpr int kMaxWidth = 12288;
+constexpr int kMaxWidth = 12288;          // maxmin: a request sorted in one workgroup's LDS
+constexpr int kMaxSumWidth = 1 << 18;     // sum: the per-row loops stream the row; the tie key's block field
 constexpr int kMaxRows = 65535;  // the tie key holds the request in 16 bits
 
 enum Mode : int { kSelect = 0, kKeepAll = 1, kKeepOpen = 2, kPinnedOnly = 3 };
@@ -245,6 +246,8 @@ __device__ __forceinline__ unsigned long long key_at(const Params &p, const RowS
 __device__ __forceinline__ unsigned long long tie_key(int r, int b) {
   return ((unsigned long long)b << 16) | (unsigned long long)(0xFFFF - r);  // newer block, then earlier request
 }
+// the tie key's width: 16 bits of request below the block's bits (14 up to 16384 blocks, else 18)
+inline int tie_bits(int width) { return width <= (1 << 14) ? 30 : 34; }
 
 // one radix pass: the histogram of the `bits`-wide digit at `shift` over the open blocks whose key
 // matches the prefix so far (tie passes: the blocks at the gain threshold, over the tie key).
@@ -1058,9 +1061,9 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
                             void *workspace, size_t workspace_bytes, void *stream) {
   if (scores == nullptr || blocks == nullptr || keep == nullptr || workspace == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_sum: null pointer");
-  if (rows < 0 || rows > alloc::kMaxRows || width < 1 || width > alloc::kMaxWidth)
+  if (rows < 0 || rows > alloc::kMaxRows || width < 1 || width > alloc::kMaxSumWidth)
     return fail(EKV_EINVAL, "ekv_rank_sum: rows %d (max %d), width %d (max %d)", rows, alloc::kMaxRows, width,
-                alloc::kMaxWidth);
+                alloc::kMaxSumWidth);
   if (budget < 0) return fail(EKV_EINVAL, "ekv_rank_sum: the budget cannot be negative");
   if (workspace_bytes < ekv_rank_sum_workspace(rows))
     return fail(EKV_EINVAL, "ekv_rank_sum: a workspace of %zu bytes is below the %zu needed", workspace_bytes,
@@ -1101,9 +1104,9 @@ int launch_sum(Params p, hipStream_t s) {
     hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
     hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, shift == 0);
   }
-  // among the blocks at the threshold: newer block, earlier request (the 30-bit tie key)
-  static_assert(alloc::kMaxWidth <= (1 << 14), "the tie key's block field is 14 bits");
-  for (int top = 30; top > 0; top -= alloc::kDigitBits) {
+  // among the blocks at the threshold: newer block, earlier request (the tie key)
+  static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
+  for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
     hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
     hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, 0);
@@ -1297,9 +1300,10 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
   if (shares_dtype != EKV_F32 && shares_dtype != EKV_F64)
     return fail(EKV_EUNSUPPORTED, "ekv_controller_keep: shares of dtype %d (float32 or float64)", shares_dtype);
   const int max_rows = objective == EKV_OBJ_SUM ? alloc::kMaxRows : alloc::kMaxMaxminRows;
-  if (rows < 0 || rows > max_rows || width < 1 || width > alloc::kMaxWidth)
+  const int max_width = objective == EKV_OBJ_SUM ? alloc::kMaxSumWidth : alloc::kMaxWidth;
+  if (rows < 0 || rows > max_rows || width < 1 || width > max_width)
     return fail(EKV_EINVAL, "ekv_controller_keep: rows %d (max %d), width %d (max %d)", rows, max_rows, width,
-                alloc::kMaxWidth);
+                max_width);
   if (recent_blocks < 0 || cap_above_blocks < 0)
     return fail(EKV_EINVAL, "ekv_controller_keep: recent_blocks %d, cap_above_blocks %d", recent_blocks,
                 cap_above_blocks);

@@ -61,6 +61,24 @@ def test_sum_rows_past_one_reduction_run():
         assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, weights, budget)), frac
 
 
+def test_sum_rows_wider_than_a_register_row():
+    # rows past 12288 blocks and past the 14-bit block field of the narrower tie key (16384): the tie
+    # passes cover 18 bits of block; integer scores force ties at the threshold across requests, and
+    # NumPy's totals add several 8192-value runs
+    rng = np.random.default_rng(16)
+    for sizes in ((16384, 12289, 300), (16385, 32768, 5000), (40000, 17, 20000)):
+        scores = [rng.integers(0, 5, size=n).astype(float) * rng.choice([1e-3, 1.0]) for n in sizes]
+        scores[0][::7] = 2.0  # many equal gains
+        pinned = [oa.default_pins(len(x)) for x in scores]
+        weights = [1.0, 2.0, 1.0][: len(sizes)]
+        total = sum(sizes)
+        for frac in (0.2, 0.5):
+            budget = int(frac * total)
+            reqs = [allocation.Request(scores=x, weight=w) for x, w in zip(scores, weights)]
+            print(f"sizes {sizes} budget {budget}", flush=True)
+            assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, weights, budget))
+
+
 def test_sum_view_build_configuration():
     # 1024 rows of U[1, 8192] blocks with Dirichlet(0.1) float32 shares: budgets 0.2 / 0.5 / 0.8
     c = workloads.config4()

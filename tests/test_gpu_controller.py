@@ -111,3 +111,18 @@ def test_view_build_configuration_at_cap_256(objective):
     keep, summary = run(c["shares"], c["blocks"].astype(np.int64), np.ones(rows, bool), 0.5, 4, 256,
                         objective=objective)
     assert summary[4] == int((c["blocks"] > 256).sum())
+
+
+def test_sum_rows_wider_than_a_register_row():
+    # the default objective on rows past 16384 blocks (the wider tie key): released blocks, audit
+    # lengths, a row under the cap and one without evidence, weights
+    rng = np.random.default_rng(21)
+    rows, width = 5, 20000
+    shares = rng.integers(0, 4, size=(rows, width)).astype(np.float64)  # equal gains: ties at the cut
+    lengths = np.array([20000, 16385, 300, 19999, 12000])
+    evidence = np.array([1, 1, 1, 0, 1])
+    audited = np.array([19000, 16385, 300, 0, 11000])
+    released = (rng.random((rows, width)) < 0.05).astype(np.uint8)
+    weights = np.array([1.0, 2.0, 0.5, 1.0, 1.5])
+    for fraction in (0.3, 0.6):
+        run(shares, lengths, evidence, fraction, 4, 256, audited=audited, released=released, weights=weights)
