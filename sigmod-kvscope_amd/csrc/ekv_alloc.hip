@@ -662,7 +662,6 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
   static_assert(RPT >= 1 && RPT * kBisectThreads <= kMaxMaxminRows, "requests per thread");
   __shared__ long long s_red[kBisectThreads / kWave];
   __shared__ double s_best[kBisectThreads / kWave];
-  __shared__ int s_best_row[kBisectThreads / kWave];
   const Params &p = m.p;
   const State *s = p.state;
   if (s->mode != kSelect || s->error) return;
@@ -845,51 +844,102 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
     retained[j] = base[j] + (counts[j] ? m.prefix[(int64_t)r * p.width + counts[j] - 1] : 0.0);
   }
   long long leftover = free_blocks - block_sum<kBisectThreads>(used, s_red);
-  while (leftover > 0) {
-    double best = INFINITY;
-    int best_row = INT_MAX;
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-      const int r = tid + j * kBisectThreads;
-      if (r >= p.rows || counts[j] >= open[j]) continue;
-      if (retained[j] < best || (retained[j] == best && r < best_row)) {
-        best = retained[j];
-        best_row = r;
+  // The leftover as the reference's heap hands it out (allocation.py:157-166): the request with the
+  // lowest (retained, index) takes its next block, and its retained share grows by that block's
+  // share.  A request's level never falls, so the pops are a merge of the requests' level sequences
+  // by (level, index).  One pass serves every request tied at the lowest level L, in index order:
+  // a request whose next share leaves L unchanged when added (zero, or below L's last bit) stays at
+  // L and so takes every block it has left (its later shares, sorted descending, are no larger),
+  // any other takes one block and rises above L.  The pass ends the leftover where it runs out.
+  if constexpr (RPT <= 4) {
+    __shared__ int s_scan[kBisectThreads / kWave];
+    while (leftover > 0) {
+      double low_level = INFINITY;
+  #pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) {
+        const int r = tid + j * kBisectThreads;
+        if (r < p.rows && counts[j] < open[j]) low_level = fmin(low_level, retained[j]);
       }
-    }
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const double ob = __shfl_xor(best, msk, kWave);
-      const int orow = __shfl_xor(best_row, msk, kWave);
-      if (ob < best || (ob == best && orow < best_row)) {
-        best = ob;
-        best_row = orow;
+      for (int msk = 32; msk >= 1; msk >>= 1) low_level = fmin(low_level, __shfl_xor(low_level, msk, kWave));
+      if (lane == 0) s_best[wave] = low_level;
+      __syncthreads();
+      low_level = s_best[0];
+      for (int w = 1; w < kBisectThreads / kWave; ++w) low_level = fmin(low_level, s_best[w]);
+      __syncthreads();
+      if (low_level == INFINITY) break;  // every request keeps all its blocks
+      long long served = 0;  // blocks the tied requests before the current rows take
+  #pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) {
+        const int r = tid + j * kBisectThreads;
+        const bool tied = r < p.rows && counts[j] < open[j] && retained[j] == low_level;
+        double next_share = 0.0;
+        int take = 0;
+        if (tied) {
+          const RowStat st = p.row_stat[r];
+          next_share = share_of(p, st, r, m.vals_out[(int64_t)r * p.width + counts[j]]);
+          take = low_level + next_share == low_level ? open[j] - counts[j] : 1;
+        }
+        int pass_total;
+        const long long before = served + block_exclusive_scan<kBisectThreads>(take, s_scan, pass_total);
+        const long long got = tied ? max(0LL, min((long long)take, leftover - before)) : 0LL;
+        if (got > 0) {
+          counts[j] += (int)got;
+          if (take == 1) retained[j] = low_level + next_share;  // the level popped plus the kept block's share
+        }
+        served += pass_total;
       }
+      leftover -= min(served, leftover);
     }
-    if (lane == 0) {
-      s_best[wave] = best;
-      s_best_row[wave] = best_row;
-    }
-    __syncthreads();
-    best = s_best[0];
-    best_row = s_best_row[0];
-    for (int w = 1; w < kBisectThreads / kWave; ++w) {
-      if (s_best[w] < best || (s_best[w] == best && s_best_row[w] < best_row)) {
-        best = s_best[w];
-        best_row = s_best_row[w];
+  } else {
+    // with eight requests a thread, one block a pass (the per-row scans of the batched form would
+    // not fit the registers)
+    __shared__ int s_best_row[kBisectThreads / kWave];
+    while (leftover > 0) {
+      double best = INFINITY;
+      int best_row = INT_MAX;
+  #pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) {
+        const int r = tid + j * kBisectThreads;
+        if (r >= p.rows || counts[j] >= open[j]) continue;
+        if (retained[j] < best || (retained[j] == best && r < best_row)) {
+          best = retained[j];
+          best_row = r;
+        }
       }
+      for (int msk = 32; msk >= 1; msk >>= 1) {
+        const double ob = __shfl_xor(best, msk, kWave);
+        const int orow = __shfl_xor(best_row, msk, kWave);
+        if (ob < best || (ob == best && orow < best_row)) {
+          best = ob;
+          best_row = orow;
+        }
+      }
+      if (lane == 0) {
+        s_best[wave] = best;
+        s_best_row[wave] = best_row;
+      }
+      __syncthreads();
+      best = s_best[0];
+      best_row = s_best_row[0];
+      for (int w = 1; w < kBisectThreads / kWave; ++w) {
+        if (s_best[w] < best || (s_best[w] == best && s_best_row[w] < best_row)) {
+          best = s_best[w];
+          best_row = s_best_row[w];
+        }
+      }
+      __syncthreads();
+      if (best_row == INT_MAX) break;  // every request keeps all its blocks
+  #pragma unroll
+      for (int j = 0; j < kRowsPerThread; ++j) {
+        if (tid + j * kBisectThreads != best_row) continue;
+        const int64_t row0 = (int64_t)best_row * p.width;
+        const RowStat st = p.row_stat[best_row];
+        const double sh = share_of(p, st, best_row, m.vals_out[row0 + counts[j]]);
+        counts[j] += 1;
+        retained[j] = best + sh;  // the level popped plus the kept block's share
+      }
+      --leftover;
     }
-    __syncthreads();
-    if (best_row == INT_MAX) break;  // every request keeps all its blocks
-#pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j) {
-      if (tid + j * kBisectThreads != best_row) continue;
-      const int64_t row0 = (int64_t)best_row * p.width;
-      const RowStat st = p.row_stat[best_row];
-      const double sh = share_of(p, st, best_row, m.vals_out[row0 + counts[j]]);
-      counts[j] += 1;
-      retained[j] = best + sh;  // the level popped plus the kept block's share
-    }
-    --leftover;
   }
 #pragma unroll
   for (int j = 0; j < kRowsPerThread; ++j) {

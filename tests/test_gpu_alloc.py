@@ -134,6 +134,37 @@ def test_maxmin_identical_requests_and_edges():
         allocation.allocate([allocation.Request(scores=np.ones(5))] * 2, 3, "maxmin")
 
 
+@pytest.mark.parametrize("rows", [12, 1500, 3000])
+def test_maxmin_leftover_over_plateaus_and_ties(rows):
+    # a large leftover: requests whose remaining shares are zero (a plateau the level bisection stops
+    # below) take every block they have left at one level; equal shares, shares too small to move the
+    # level and distinct ones mixed across requests; 1500 and 3000 requests put 2 and 4 on a thread
+    rng = np.random.default_rng(rows)
+    scores = []
+    for r in range(rows):
+        n = int(rng.integers(3, 60))
+        kind = r % 4
+        if kind == 0:
+            x = np.zeros(n)
+            x[0] = 1.0  # one block carries everything: the rest are a zero plateau
+        elif kind == 1:
+            x = np.ones(n)  # equal shares
+        elif kind == 2:
+            x = np.full(n, 1e-30)
+            x[0] = 1.0  # shares below the level's last bit once the first block is kept
+        else:
+            x = rng.random(n)
+        scores.append(x)
+    pinned = [oa.default_pins(len(x)) for x in scores]
+    total = sum(len(x) for x in scores)
+    must = sum(int(q.sum()) for q in pinned)
+    for frac in (0.3, 0.6, 0.95):
+        budget = max(must, int(frac * total))
+        reqs = [allocation.Request(scores=x) for x in scores]
+        print(f"{rows} requests, budget {budget} of {total}", flush=True)
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
+
+
 def test_maxmin_float64_scores_zero_rows_and_long_rows():
     rng = np.random.default_rng(6)
     scores = [rng.random(n) * (1 + 1e-9 * rng.random(n)) for n in (8191, 8193, 12288, 50)]
