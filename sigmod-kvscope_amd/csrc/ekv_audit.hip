@@ -912,6 +912,67 @@ __global__ __launch_bounds__(kFillThreads) void plan_fill_kernel(const PlanArgs 
   }
 }
 
+// The plan in one launch, for batches of at most kPlanRowsLds rows: every workgroup scans all rows'
+// live tiles itself (a few hundred rows: one block scan) into LDS, so its rows' first tiles and the
+// grid's split need no kernel before it, and the workgroup of tile t comes from arithmetic on the
+// split (b = floor(((t + 1) G - 1) / T) is the last b with floor(T b / G) <= t).  The workgroups
+// take rows blockIdx.x, blockIdx.x + gridDim.x, ...; the owner of a workgroup's first tile writes
+// its (count, first row), and workgroup 0 writes the empty workgroups' zero counts.
+constexpr int kPlanThreads = 256;
+constexpr int kPlanRowsLds = 4096;
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(const PlanArgs a) {
+  __shared__ int s_scan[kPlanThreads / kWave];
+  __shared__ int s_off[kPlanRowsLds + 1];
+  const bool on = *(volatile const uint32_t *)a.flag != 0u;
+  const int per = (a.rows + kPlanThreads - 1) / kPlanThreads;
+  const int r0 = min((int)threadIdx.x * per, a.rows);
+  const int r1 = min(r0 + per, a.rows);
+  int local = 0;
+  if (on)
+    for (int r = r0; r < r1; ++r) local += plan_row_tiles(a, r);
+  int total = 0;
+  int base = block_exclusive_scan<kPlanThreads>(local, s_scan, total);
+  for (int r = r0; r < r1; ++r) {
+    s_off[r] = base;
+    if (on) base += plan_row_tiles(a, r);
+  }
+  if (threadIdx.x == 0) s_off[a.rows] = total;
+  const int64_t T = total, G = a.grid;
+  auto first = [&](int64_t b) { return (int)(T * b / G); };
+  if (blockIdx.x == 0) {
+    for (int b = threadIdx.x; b < kMaxGrid; b += kPlanThreads)
+      if (b >= a.grid || first(b + 1) == first(b)) a.wg[b] = make_int2(0, 0);
+  }
+  __syncthreads();
+  if (T == 0) return;
+  const int tile_tokens = kTileBlocks * a.block_size;
+  for (int row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const int off = s_off[row];
+    const int tiles = s_off[row + 1] - off;
+    if (tiles <= 0) continue;
+    const int len = min(max(a.lens[row], 0), a.width * a.block_size);
+    const int nb = (len + a.block_size - 1) / a.block_size;
+    const int qtok = a.qrow[row];
+    const int32_t *trow = a.table + (int64_t)row * a.table_stride;
+    for (int k = threadIdx.x; k < tiles; k += kPlanThreads) {
+      const int t = off + k;
+      const int b = (int)(((int64_t)(t + 1) * G - 1) / T);
+      const int fb = first(b);
+      TileDesc d;
+      d.row = row;
+      d.k = k;
+      d.valid = min(len - k * tile_tokens, tile_tokens);
+      d.qtok = qtok;
+      d.id0 = trow[kTileBlocks * k];
+      d.id1 = kTileBlocks * k + 1 < nb ? trow[kTileBlocks * k + 1] : d.id0;  // past the row: stands in
+      d.pad0 = d.pad1 = 0;
+      a.desc[(int64_t)b * a.cap + (t - fb)] = d;
+      if (t == fb) a.wg[b] = make_int2(first(b + 1) - fb, row);
+    }
+  }
+}
+
 struct PlanView {
   const int2 *wg;
   const TileDesc *desc;
@@ -1540,6 +1601,11 @@ extern "C" int ekv_audit_plan(const int32_t *table, int64_t table_stride, const 
   a.first = (int32_t *)(base + Lp.first);
   a.row_off = (int32_t *)(base + Lp.row_off);
   a.desc = (TileDesc *)(base + Lp.desc);
+  if (rows <= kPlanRowsLds) {  // one launch
+    const int blocks = std::max(1, std::min(rows, 1024));
+    hipLaunchKernelGGL(plan_kernel, dim3(blocks), dim3(kPlanThreads), 0, (hipStream_t)stream, a);
+    return check_hip(hipGetLastError(), "ekv_audit_plan launch");
+  }
   hipLaunchKernelGGL(plan_split_kernel, dim3(1), dim3(kSplitThreads), 0, (hipStream_t)stream, a);
   int rc2 = check_hip(hipGetLastError(), "ekv_audit_plan split launch");
   if (rc2 != EKV_OK || rows == 0) return rc2;
