@@ -34,6 +34,7 @@
 #include <algorithm>
 
 #include <rocprim/block/block_radix_sort.hpp>
+#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "ekv_common.hpp"
 #include "ekv_pairwise.hpp"
@@ -43,6 +44,7 @@ namespace alloc {
 
 constexpr int kThreads = 256;
 constexpr int kMaxWidth = 12288;          // maxmin: a request sorted in one workgroup's LDS
+constexpr int kMaxMaxminWidth = 65535;    // maxmin past it: positions kept in 16 bits
 constexpr int kMaxSumWidth = 1 << 18;     // sum: the per-row loops stream the row; the tie key's block field
 constexpr int kMaxRows = 65535;  // the tie key holds the request in 16 bits
 
@@ -407,6 +409,12 @@ struct MaxminParams {
   int32_t *order;     // the requests, longest first: the sorting workgroups' order
   int32_t *level_count;  // per level j / kLevels, the requests' counts summed
   uint16_t *level_pos;   // per request and level j / kLevels, its position there
+  // requests wider than a sort in LDS (width > kMaxWidth): the device-wide segmented sort's inputs
+  unsigned long long *keys_in;  // [rows][width]
+  int32_t *vals_in;             // [rows][width]
+  int32_t *seg_begin, *seg_end; // [rows]
+  void *sort_temp;              // the segmented sort's temporary storage (host-side fields)
+  size_t sort_temp_bytes;
 };
 
 // the bisection's first kLevelBits steps can only reach the levels j / 2^kLevelBits (0 < j < 2^kLevelBits,
@@ -414,27 +422,36 @@ struct MaxminParams {
 constexpr int kLevelBits = 10;
 constexpr int kLevels = 1 << kLevelBits;
 
-// per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts
+// per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts.  The
+// pinned blocks are listed in order first: in LDS, or for rows wider than it holds (WIDE) in the
+// request's row of vals_out, which the sort overwrites afterwards.
+template <bool WIDE>
 __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
   __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
   __shared__ double s_leaf[kMaxLeaves];
-  __shared__ unsigned short s_pin[kMaxWidth];  // the pinned blocks, in order
+  __shared__ unsigned short s_pin[WIDE ? 1 : kMaxWidth];  // the pinned blocks, in order
   const Params &p = m.p;
   const int r = blockIdx.x;
   const int lane = lane_id();
   const RowStat st = p.row_stat[r];
+  int32_t *g_pin = m.vals_out + (int64_t)r * p.width;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int npin = 0;
   for (int b0 = 0; b0 < st.n; b0 += kWave) {
     const int b = b0 + lane;
     const bool pin = b < st.n && pinned_at(p, r, b, st.n);
     const uint64_t mask = __ballot(pin);
-    if (pin) s_pin[npin + __popcll(mask & below)] = (unsigned short)b;
+    if (pin) {
+      if constexpr (WIDE) g_pin[npin + __popcll(mask & below)] = b;
+      else s_pin[npin + __popcll(mask & below)] = (unsigned short)b;
+    }
     npin += __popcll(mask);
   }
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  const double base = numpy_sum([&](int k) { return share_of(p, st, r, s_pin[k]); }, npin, s_start, s_len, s_leaf);
+  if constexpr (WIDE) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");  // the list's stores, then its loads
+  else __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const double base = numpy_sum([&](int k) { return share_of(p, st, r, WIDE ? g_pin[k] : (int)s_pin[k]); }, npin,
+                                s_start, s_len, s_leaf);
   if (lane == 0) {
     MaxminRow mr;
     mr.base = base;
@@ -503,7 +520,8 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   for (int j = tid; j < kLevels; j += kSortThreads) m.level_count[j] = 0;  // summed into by mm_levels_kernel
   if (tid < kOrderClasses) s_count[tid] = 0;
   __syncthreads();
-  for (int r = tid; r < rows; r += kSortThreads) atomicAdd(&s_count[m.p.row_stat[r].n / kOrderStep], 1);
+  auto cls = [&](int r) { return min(m.p.row_stat[r].n / kOrderStep, kOrderClasses - 1); };
+  for (int r = tid; r < rows; r += kSortThreads) atomicAdd(&s_count[cls(r)], 1);
   __syncthreads();
   if (tid == 0) {
     int at = 0;
@@ -513,7 +531,7 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
     }
   }
   __syncthreads();
-  for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[m.p.row_stat[r].n / kOrderStep], 1)] = r;
+  for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[cls(r)], 1)] = r;
 }
 
 template <int MAX_ITEMS>
@@ -542,6 +560,38 @@ __global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParam
     sort_request<kMid>(m, st, r, reinterpret_cast<typename RequestSort<kMid>::storage_type &>(raw));
   else
     sort_request<MAX_ITEMS>(m, st, r, raw);
+}
+
+// Requests wider than a sort in LDS go through a device-wide segmented radix sort (rocPRIM's, stable,
+// descending) instead: this kernel writes every request's keys and block indices (the keys of
+// sort_request) and its segment, one workgroup per request ...
+__global__ __launch_bounds__(kThreads) void mm_wide_keys_kernel(const MaxminParams m) {
+  const Params &p = m.p;
+  const int r = blockIdx.x;
+  const RowStat st = p.row_stat[r];
+  const int64_t row0 = (int64_t)r * p.width;
+  for (int pos = threadIdx.x; pos < st.n; pos += kThreads) {
+    const bool pinned = pinned_at(p, r, pos, st.n);
+    m.keys_in[row0 + pos] = pinned ? 0ull : gain_key(share_value(st, p.scores[(int64_t)r * p.scores_stride + pos]));
+    m.vals_in[row0 + pos] = pos;
+  }
+  if (threadIdx.x == 0) {
+    m.seg_begin[r] = (int32_t)row0;
+    m.seg_end[r] = (int32_t)(row0 + st.n);
+  }
+}
+
+// ... and this one turns the sorted keys, written over `prefix`, into the open shares in sorted order.
+__global__ __launch_bounds__(kThreads) void mm_wide_unpack_kernel(const MaxminParams m) {
+  const Params &p = m.p;
+  const int r = blockIdx.x;
+  const int open = p.row_stat[r].open;
+  double *row = m.prefix + (int64_t)r * p.width;
+  const unsigned long long *keys = reinterpret_cast<const unsigned long long *>(row);
+  for (int pos = threadIdx.x; pos < open; pos += kThreads) {
+    const unsigned long long k = keys[pos];
+    row[pos] = key_value(k);
+  }
 }
 
 // per request, one wave: the running totals of its sorted open shares (np.cumsum), in place. One
@@ -613,10 +663,10 @@ __global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) 
 // the positions give the brackets that those steps leave.
 constexpr int kLevelThreads = 256;
 
-template <int CAP>
+template <int CAP>  // CAP 0: the totals are searched in memory (requests wider than LDS holds)
 __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminParams m) {
   constexpr int kMine = (kLevels + kLevelThreads - 1) / kLevelThreads;  // levels per thread
-  __shared__ double s_tot[CAP];  // the request's running totals
+  __shared__ double s_lds[CAP > 0 ? CAP : 1];  // the request's running totals
   // a workgroup takes requests blockIdx.x, + gridDim.x, ... and adds its counts once per level
   int mine[kMine];
 #pragma unroll
@@ -626,7 +676,10 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
   const MaxminRow mr = m.mrow[r];
   const int open = mr.open;
   const double *pre = m.prefix + (int64_t)r * m.p.width;
-  for (int i = threadIdx.x; i < open; i += kLevelThreads) s_tot[i] = pre[i];
+  if constexpr (CAP > 0) {
+    for (int i = threadIdx.x; i < open; i += kLevelThreads) s_lds[i] = pre[i];
+  }
+  const double *s_tot = CAP > 0 ? s_lds : pre;
   __syncthreads();
   const double shift = 2.0 * (double)r;
   uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
@@ -1172,7 +1225,19 @@ namespace {
 
 struct MaxminLayout {
   size_t state, row_stat, mrow, order, level_count, level_pos, vals_out, prefix, total;
+  size_t keys_in, vals_in, seg_begin, seg_end, sort_temp, sort_temp_bytes;  // rows wider than kMaxWidth
 };
+
+// Temporary storage of the segmented sort of rows x width keys (0 if the query fails).
+size_t wide_sort_bytes(int32_t rows, int32_t width) {
+  size_t bytes = 0;
+  unsigned long long *keys = nullptr;
+  int32_t *vals = nullptr, *offsets = nullptr;
+  const hipError_t e = rocprim::segmented_radix_sort_pairs_desc(
+      nullptr, bytes, keys, keys, vals, vals, (unsigned int)((size_t)rows * (size_t)width), (unsigned int)rows, offsets,
+      offsets, 0, 64, (hipStream_t)0);
+  return e == hipSuccess ? bytes : 0;
+}
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1196,8 +1261,41 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + cells * 4);
   l.prefix = at;
   at = align256(at + cells * 8);
+  if (width > alloc::kMaxWidth) {
+    l.keys_in = at;
+    at = align256(at + cells * 8);
+    l.vals_in = at;
+    at = align256(at + cells * 4);
+    l.seg_begin = at;
+    at = align256(at + (size_t)rows * 4);
+    l.seg_end = at;
+    at = align256(at + (size_t)rows * 4);
+    l.sort_temp_bytes = wide_sort_bytes(rows, width);
+    l.sort_temp = at;
+    at = align256(at + l.sort_temp_bytes);
+  }
   l.total = at + 256;  // + 256: the base may be realigned
   return l;
+}
+
+// The maxmin buffers of a workspace laid out by maxmin_layout from `base`.
+void set_maxmin_buffers(const MaxminLayout &l, uintptr_t base, alloc::MaxminParams &m) {
+  m.p.state = (alloc::State *)(base + l.state);
+  m.p.row_stat = (alloc::RowStat *)(base + l.row_stat);
+  m.mrow = (alloc::MaxminRow *)(base + l.mrow);
+  m.vals_out = (int32_t *)(base + l.vals_out);
+  m.prefix = (double *)(base + l.prefix);
+  m.order = (int32_t *)(base + l.order);
+  m.level_count = (int32_t *)(base + l.level_count);
+  m.level_pos = (uint16_t *)(base + l.level_pos);
+  if (l.sort_temp_bytes > 0) {
+    m.keys_in = (unsigned long long *)(base + l.keys_in);
+    m.vals_in = (int32_t *)(base + l.vals_in);
+    m.seg_begin = (int32_t *)(base + l.seg_begin);
+    m.seg_end = (int32_t *)(base + l.seg_end);
+    m.sort_temp = (void *)(base + l.sort_temp);
+    m.sort_temp_bytes = l.sort_temp_bytes;
+  }
 }
 
 }  // namespace
@@ -1213,12 +1311,14 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
                                void *workspace, size_t workspace_bytes, void *stream) {
   if (scores == nullptr || blocks == nullptr || keep == nullptr || workspace == nullptr)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: null pointer");
-  if (rows < 0 || rows > alloc::kMaxMaxminRows || width < 1 || width > alloc::kMaxWidth)
+  if (rows < 0 || rows > alloc::kMaxMaxminRows || width < 1 || width > alloc::kMaxMaxminWidth)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: rows %d (max %d), width %d (max %d)", rows, alloc::kMaxMaxminRows,
-                width, alloc::kMaxWidth);
+                width, alloc::kMaxMaxminWidth);
   if (budget < 0) return fail(EKV_EINVAL, "ekv_rank_maxmin: the budget cannot be negative");
   if (rows == 0) return EKV_OK;
   const MaxminLayout l = maxmin_layout(rows, width);
+  if (width > alloc::kMaxWidth && l.sort_temp_bytes == 0)
+    return fail(EKV_ELAUNCH, "ekv_rank_maxmin: the segmented sort's storage query failed");
   if (workspace_bytes < l.total)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: a workspace of %zu bytes is below the %zu needed", workspace_bytes,
                 l.total);
@@ -1237,14 +1337,7 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   p.keep = keep;
   p.keep_stride = keep_stride;
   p.summary = summary;
-  p.state = (alloc::State *)(base + l.state);
-  p.row_stat = (alloc::RowStat *)(base + l.row_stat);
-  m.mrow = (alloc::MaxminRow *)(base + l.mrow);
-  m.vals_out = (int32_t *)(base + l.vals_out);
-  m.prefix = (double *)(base + l.prefix);
-  m.order = (int32_t *)(base + l.order);
-  m.level_count = (int32_t *)(base + l.level_count);
-  m.level_pos = (uint16_t *)(base + l.level_pos);
+  set_maxmin_buffers(l, base, m);
   return alloc::launch_maxmin(m, rows, width, (hipStream_t)stream);
 }
 
@@ -1257,11 +1350,24 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
-  hipLaunchKernelGGL(alloc::mm_base_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  const bool wide = width > alloc::kMaxWidth;
+  if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);
+  else hipLaunchKernelGGL(alloc::mm_base_kernel<false>, dim3(rows), dim3(kWave), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_order_kernel, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
-  if (width <= 4 * alloc::kSortThreads)
+  if (wide) {
+    // a device-wide segmented sort over the requests' keys, the sorted keys over `prefix`
+    hipLaunchKernelGGL(alloc::mm_wide_keys_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
+    size_t temp_bytes = m.sort_temp_bytes;
+    rc = check_hip(rocprim::segmented_radix_sort_pairs_desc(
+                       m.sort_temp, temp_bytes, m.keys_in, reinterpret_cast<unsigned long long *>(m.prefix),
+                       m.vals_in, m.vals_out, (unsigned int)((size_t)rows * (size_t)width), (unsigned int)rows,
+                       m.seg_begin, m.seg_end, 0, 64, s),
+                   "ekv_rank_maxmin segmented sort");
+    if (rc != EKV_OK) return rc;
+    hipLaunchKernelGGL(alloc::mm_wide_unpack_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
+  } else if (width <= 4 * alloc::kSortThreads)
     hipLaunchKernelGGL(alloc::mm_sort_kernel<4>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   else if (width <= 8 * alloc::kSortThreads)
     hipLaunchKernelGGL(alloc::mm_sort_kernel<8>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
@@ -1271,7 +1377,9 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3(rows), dim3(kWave), 0, s, m);
   const dim3 level_grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 2));
-  if (width <= 4096)
+  if (wide)
+    hipLaunchKernelGGL(alloc::mm_levels_kernel<0>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
+  else if (width <= 4096)
     hipLaunchKernelGGL(alloc::mm_levels_kernel<4096>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
   else if (width <= 8192)
     hipLaunchKernelGGL(alloc::mm_levels_kernel<8192>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
@@ -1350,7 +1458,7 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
   if (shares_dtype != EKV_F32 && shares_dtype != EKV_F64)
     return fail(EKV_EUNSUPPORTED, "ekv_controller_keep: shares of dtype %d (float32 or float64)", shares_dtype);
   const int max_rows = objective == EKV_OBJ_SUM ? alloc::kMaxRows : alloc::kMaxMaxminRows;
-  const int max_width = objective == EKV_OBJ_SUM ? alloc::kMaxSumWidth : alloc::kMaxWidth;
+  const int max_width = objective == EKV_OBJ_SUM ? alloc::kMaxSumWidth : alloc::kMaxMaxminWidth;
   if (rows < 0 || rows > max_rows || width < 1 || width > max_width)
     return fail(EKV_EINVAL, "ekv_controller_keep: rows %d (max %d), width %d (max %d)", rows, max_rows, width,
                 max_width);
@@ -1415,16 +1523,11 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
     rc = alloc::launch_sum(p, s);
   } else {
     const MaxminLayout ml = maxmin_layout(rows, width);
+    if (width > alloc::kMaxWidth && ml.sort_temp_bytes == 0)
+      return fail(EKV_ELAUNCH, "ekv_controller_keep: the segmented sort's storage query failed");
     alloc::MaxminParams m{};
     m.p = p;
-    m.p.state = (alloc::State *)(inner + ml.state);
-    m.p.row_stat = (alloc::RowStat *)(inner + ml.row_stat);
-    m.mrow = (alloc::MaxminRow *)(inner + ml.mrow);
-    m.vals_out = (int32_t *)(inner + ml.vals_out);
-    m.prefix = (double *)(inner + ml.prefix);
-    m.order = (int32_t *)(inner + ml.order);
-    m.level_count = (int32_t *)(inner + ml.level_count);
-    m.level_pos = (uint16_t *)(inner + ml.level_pos);
+    set_maxmin_buffers(ml, inner, m);
     rc = alloc::launch_maxmin(m, rows, width, s);
   }
   if (rc != EKV_OK) return rc;

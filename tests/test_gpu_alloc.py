@@ -165,6 +165,25 @@ def test_maxmin_leftover_over_plateaus_and_ties(rows):
         assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
 
 
+@pytest.mark.parametrize("sizes", [(12289, 300, 5000), (20000, 16384, 17, 9000), (65535, 40000, 12288)])
+def test_maxmin_rows_wider_than_a_sort_in_lds(sizes):
+    # requests past 12288 blocks go through the device-wide segmented sort and search their running
+    # totals in memory; ties (integer scores), explicit pins and a zero tail
+    rng = np.random.default_rng(sum(sizes))
+    scores = [rng.integers(0, 6, size=n).astype(float) * rng.choice([1e-3, 1.0]) for n in sizes]
+    scores[0][-(len(scores[0]) // 5):] = 0.0
+    pinned = [oa.default_pins(len(x)) for x in scores]
+    pinned[1] = pinned[1].copy()
+    pinned[1][:: 97] = True
+    total = sum(sizes)
+    must = sum(int(q.sum()) for q in pinned)
+    for frac in (0.2, 0.55, 0.9):
+        budget = max(must, int(frac * total))
+        reqs = [allocation.Request(scores=x, pinned=q) for x, q in zip(scores, pinned)]
+        print(f"sizes {sizes}, budget {budget}", flush=True)
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
+
+
 def test_maxmin_float64_scores_zero_rows_and_long_rows():
     rng = np.random.default_rng(6)
     scores = [rng.random(n) * (1 + 1e-9 * rng.random(n)) for n in (8191, 8193, 12288, 50)]
