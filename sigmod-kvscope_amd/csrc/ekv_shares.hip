@@ -23,11 +23,14 @@
 // thread sums (or maxes) its block's shares over its layers and query rows in a fixed order, and
 // the group partials are combined in LDS in a fixed order.
 //
-// Two forms.  Without a workspace one 1024-thread workgroup takes a whole row, so the longest row
+// Three forms.  Without a workspace one 1024-thread workgroup takes a whole row, so the longest row
 // sets the time (its records are read twice by one CU).  With a workspace (ekv_tile_shares_ws)
-// the layers are split into K groups, (row, group) workgroups of 256 threads write per-block
-// partial sums (or maxes) and their contributor counts, and a second kernel combines each row's K
-// partials in group order.  Both are deterministic (no atomics) and the same on every call.
+// the layers are split into K groups whose workgroups write per-block partial sums (or maxes) and
+// their contributor counts: for 4 query rows and rows of at most 512 blocks (shares_wave_kernel)
+// the last of a row's workgroups to finish adds them and writes the row, otherwise a second kernel
+// (combine_kernel) adds each row's K partials in group order.  Every form adds in a fixed order,
+// so the results are the same on every call (the wave form's arrival counter only picks which
+// workgroup adds the partials).
 #include <limits.h>
 #include <math.h>
 
