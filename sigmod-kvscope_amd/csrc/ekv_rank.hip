@@ -712,25 +712,29 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
   uint32_t keep_bits = ~0u;  // rows without evidence read in full, controller.py:401
   if (decide) {
     // keys, larger first: an open block's is at least 1 (by value: the score's bits + 1 for a
-    // positive score, else 1; inf last: 1 for +inf, else 2; tie: 1), a closed block's is 0, the
-    // smallest, which the select never reaches (the quota is below the open count).  Slot i of
-    // thread t sits at i * kThreads + t: lane-consecutive, free of bank conflicts.
+    // positive score, else 1; inf last: 1 for +inf, else 2; tie: 1), a closed block's is 0 and is
+    // never counted.  Slot i of thread t sits at i * kThreads + t: lane-consecutive, free of bank
+    // conflicts.  A thread whose run holds no open block (past a short row) neither writes nor
+    // reads its slots.
+    const bool any_open = open_bits != 0u;
+    if (any_open) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      uint32_t k;
-      if (mode == 1) k = (uint32_t)max((int)key[i], 0) + 1u;
-      else if (mode == 2) k = key[i] == 0x7f800000u ? 1u : 2u;
-      else k = 1u;
-      s_row[i * kThreads + tid] = ((open_bits >> i) & 1u) ? k : 0u;
+      for (int i = 0; i < PER; ++i) {
+        uint32_t k;
+        if (mode == 1) k = (uint32_t)max((int)key[i], 0) + 1u;
+        else if (mode == 2) k = key[i] == 0x7f800000u ? 1u : 2u;
+        else k = 1u;
+        s_row[i * kThreads + tid] = ((open_bits >> i) & 1u) ? k : 0u;
+      }
     }
     const int open_count = (int)(me.exist - me.pinned);
     uint32_t open_keep = 0;
     if (quota >= open_count) {
       open_keep = ~0u;
     } else if (quota > 0) {
-      // radix select of the quota-th largest key, 8 bits at a time from the top; wave 0 scans the
-      // counts and clears them for the next pass, and the select stops once the quota ends at the
-      // end of a digit's bucket.  Closed blocks (key 0) only ever count in the lowest buckets.
+      // radix select of the quota-th largest key over the open blocks, 8 bits at a time from the
+      // top; wave 0 scans the counts and clears them for the next pass, and the select stops once
+      // the quota ends at the end of a digit's bucket
       uint32_t prefix = 0, mask = 0;
       int k_rem = (int)quota;
       bool whole = false;
@@ -738,10 +742,12 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
 #pragma unroll 1
       for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
+        if (any_open) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const uint32_t k = s_row[i * kThreads + tid];
-          if ((k & mask) == prefix) atomicAdd(&s_hist[((k >> shift) & 255) * 4 + copy], 1);
+          for (int i = 0; i < PER; ++i) {
+            const uint32_t k = s_row[i * kThreads + tid];
+            if (k != 0u && (k & mask) == prefix) atomicAdd(&s_hist[((k >> shift) & 255) * 4 + copy], 1);
+          }
         }
         __syncthreads();
         if (wave == 0) {
@@ -779,21 +785,25 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
         if (whole) break;
       }
       if (whole) {
+        if (any_open) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const uint32_t k = s_row[i * kThreads + tid];
-          open_keep |= (k != 0u && (k & mask) >= prefix) ? (1u << i) : 0u;
+          for (int i = 0; i < PER; ++i) {
+            const uint32_t k = s_row[i * kThreads + tid];
+            open_keep |= (k != 0u && (k & mask) >= prefix) ? (1u << i) : 0u;
+          }
         }
       } else {
         // every key above the threshold (at least 1: closed keys are below it) and the first k_rem
         // equal keys by block index: the equal keys before a thread's run are one scan of the
         // threads' counts
         uint32_t eq_bits = 0, above_bits = 0;
+        if (any_open) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const uint32_t k = s_row[i * kThreads + tid];
-          eq_bits |= k == prefix ? (1u << i) : 0u;
-          above_bits |= k > prefix ? (1u << i) : 0u;
+          for (int i = 0; i < PER; ++i) {
+            const uint32_t k = s_row[i * kThreads + tid];
+            eq_bits |= k == prefix ? (1u << i) : 0u;
+            above_bits |= k > prefix ? (1u << i) : 0u;
+          }
         }
         int eq_total;
         int before = block_exclusive_scan<kThreads>(__popc(eq_bits), s_scan, eq_total);
