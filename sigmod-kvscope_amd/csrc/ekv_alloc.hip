@@ -58,6 +58,10 @@ struct State {
   unsigned long long prefix, mask, threshold;  // threshold: the gain key at the cut
   long long k_rem, free_blocks, must, sizes, open_total, requests, budget;
   int mode, error;
+  // the select ended early: the free blocks end exactly at the end of a digit's bucket, so every
+  // key with that prefix is kept and the later passes have nothing to rank (done_tie: in a pass
+  // over the tie key, among the blocks at the gain threshold)
+  int done, done_tie;
 };
 
 struct RowStat {
@@ -259,7 +263,7 @@ template <bool TIE>
 __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits) {
   __shared__ unsigned int s_hist[kBins];
   const State *s = p.state;
-  if (s->mode != kSelect || s->error) return;
+  if (s->mode != kSelect || s->error || s->done) return;
   for (int i = threadIdx.x; i < kBins; i += kThreads) s_hist[i] = 0u;
   __syncthreads();
   const unsigned int digit_mask = (1u << bits) - 1u;
@@ -315,9 +319,11 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
 __global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shift, int bits, int last_gain_pass) {
   constexpr int kPer = kBins / kThreads;
   __shared__ long long s_scan[kThreads / kWave];
+  __shared__ int s_whole;
   State *s = p.state;
-  if (s->mode != kSelect || s->error) return;
+  if (s->mode != kSelect || s->error || s->done) return;
   const int t = threadIdx.x;
+  if (t == 0) s_whole = 0;
   long long h[kPer], mine = 0;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -346,6 +352,7 @@ __global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shif
       if (before < k_rem && before + h[i] >= k_rem) {
         s->prefix |= (unsigned long long)(kBins - 1 - (kPer * t + i)) << shift;
         s->k_rem = k_rem - before;
+        if (before + h[i] == k_rem) s_whole = 1;  // the bucket ends the free blocks
       }
       before += h[i];
     }
@@ -355,7 +362,10 @@ __global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shif
   __syncthreads();
   if (t == 0) {
     s->mask |= ((1ull << bits) - 1ull) << shift;
-    if (last_gain_pass) {  // the gain threshold is complete: the tie passes start
+    if (s_whole) {
+      s->done = 1;
+      s->done_tie = last_gain_pass < 0 ? 1 : 0;
+    } else if (last_gain_pass > 0) {  // the gain threshold is complete: the tie passes start
       s->threshold = s->prefix;
       s->prefix = 0ull;
       s->mask = 0ull;
@@ -369,7 +379,8 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
   const RowStat st = p.row_stat[r];
   const int mode = s->mode;
   const bool error = s->error != 0;
-  const unsigned long long threshold = s->threshold, tie = s->prefix;
+  const unsigned long long threshold = s->threshold, prefix = s->prefix, mask = s->mask;
+  const bool done_gain = s->done && !s->done_tie;
   const double weight = weight_of(p, r);
   uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
   for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < p.width; b0 += kThreads * kRun) {
@@ -385,7 +396,8 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
       else if (mode == kPinnedOnly) k = 0;
       else {
         const unsigned long long key = gain_key(weight * share_value(st, run.score[u]));
-        k = (key > threshold || (key == threshold && tie_key(r, b) >= tie)) ? 1 : 0;
+        if (done_gain) k = (key & mask) >= prefix ? 1 : 0;  // every key from the last bucket on
+        else k = (key > threshold || (key == threshold && (tie_key(r, b) & mask) >= prefix)) ? 1 : 0;
       }
       krow[b] = k;
     }
@@ -1205,14 +1217,14 @@ int launch_sum(Params p, hipStream_t s) {
   for (int top = 64; top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
     hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, shift == 0);
+    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, shift == 0 ? 1 : 0);
   }
   // among the blocks at the threshold: newer block, earlier request (the tie key)
   static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
   for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
     hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, 0);
+    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
   }
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
