@@ -159,9 +159,10 @@ int ekv_tile_shares(const float *lse, int64_t lse_plane_stride, int64_t lse_laye
  * a per-row arrival counter in the workspace); other shapes combine them in a second kernel.
  * Replaces the same reference code as ekv_tile_shares.
  * workspace: ekv_tile_shares_workspace(nrows, width, layers) bytes of device memory (256 KB of
- * arrival counters, then the partials).  Fill it with zeros once before its first use; every call
- * leaves the counters at zero again, for calls of any shape, as long as nothing else writes into
- * the workspace.  Calls that share one workspace must not overlap.
+ * arrival counters, then the partials and their counts, which the last workgroup of a row reads
+ * as they land: a slot reads zero until its value has arrived).  Fill it with zeros once before its
+ * first use; every call leaves all of it at zero again, for calls of any shape, as long as nothing
+ * else writes into the workspace.  Calls that share one workspace must not overlap.
  */
 size_t ekv_tile_shares_workspace(int32_t nrows, int32_t width, int32_t layers);
 int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,

@@ -558,6 +558,36 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// The wave form's workspace slots hold a value plus one, so that a slot reads 0 until its value
+// has landed: a partial's bits plus one (a NaN with every bit set is stored as the quiet NaN), a
+// count plus one.  The workgroup that adds a row's partials waits on each slot it reads until it is
+// non-zero, then sets it back to 0; combine_kernel clears the slots it reads too, so that between
+// calls every slot of the workspace is 0.
+constexpr int kSpinLimit = 1 << 20;  // reloads of a slot before the value is taken as lost
+
+__device__ __forceinline__ uint32_t slot_of(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u == 0xFFFFFFFFu ? 0x7FC00000u : u) + 1u;
+}
+
+__device__ __forceinline__ uint32_t load_slot(const uint32_t *at) {
+  return __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_slot(uint32_t *at, uint32_t v) {
+  __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// the slot's value once it has landed (0 when it was first read), or 0 after kSpinLimit reloads
+__device__ __forceinline__ uint32_t landed(const uint32_t *at, uint32_t first) {
+  uint32_t v = first;
+  for (int k = 0; v == 0u && k < kSpinLimit; ++k) {
+    __builtin_amdgcn_s_sleep(1);
+    v = load_slot(at);
+  }
+  return v;
+}
+
 // The wave form for quads of 4 cells and rows of at most 64 S blocks: one pass over memory, and a
 // (layer, query row)'s softmax never leaves its wave.  Wave w of a workgroup takes layer
 // 8 g + w of layer group g of the row; lane i keeps blocks i + 64 s (s < S) of that layer in
@@ -687,46 +717,79 @@ void shares_wave_kernel(const Params p) {
   if (p.groups > 1) {
     // The partials and counts cross workgroups (and XCDs) through device-coherent stores and
     // loads, which pass the per-XCD L2 caches; a fence would instead write back and invalidate
-    // the whole L2 of the XCD.  A workgroup's stores have completed (vmcnt 0) before its arrival
-    // is counted, and the last workgroup loads the others' only after it has seen every arrival.
-    float *part = p.part + (int64_t)out_row * p.groups * p.width;
-    if (b < n) __hip_atomic_store(&part[(int64_t)group * p.width + b], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&p.part_count[(int64_t)out_row * p.groups + group], count, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0)
+    // the whole L2 of the XCD.  A workgroup counts its arrival without waiting for its stores to
+    // complete: the last workgroup of the row, which adds the partials, waits on each slot until
+    // its value has landed (slots read 0 until then) and sets it back to 0.
+    uint32_t *part = reinterpret_cast<uint32_t *>(p.part) + (int64_t)out_row * p.groups * p.width;
+    uint32_t *counts = reinterpret_cast<uint32_t *>(p.part_count) + (int64_t)out_row * p.groups;
+    if (b < n) store_slot(&part[(int64_t)group * p.width + b], slot_of(v));
+    if (threadIdx.x == 0) {
+      store_slot(&counts[group], (uint32_t)count + 1u);
       s_last = __hip_atomic_fetch_add(&p.arrivals[out_row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                p.groups - 1;
+    }
     __syncthreads();
     if (!s_last) return;
-    if (threadIdx.x == 0) __hip_atomic_store(&p.arrivals[out_row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // every group's partial, in group order (this group's from registers)
+    // this group's own slots, written before it knew it was last, are cleared as well
+    if (b < n) store_slot(&part[(int64_t)group * p.width + b], 0u);
+    // the contributor counts, by one thread (a slot is cleared only after its last read)
+    if (threadIdx.x == 0) {
+      store_slot(&counts[group], 0u);
+      __hip_atomic_store(&p.arrivals[out_row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int total = count;
+      bool lost = false;
+      for (int g0 = 0; g0 < p.groups; g0 += kBatch) {
+        uint32_t c[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int g = g0 + k;
+          c[k] = g < p.groups && g != group ? load_slot(&counts[g]) : 1u;
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const int g = g0 + k;
+          if (g < p.groups && g != group) {
+            c[k] = landed(&counts[g], c[k]);
+            lost |= c[k] == 0u;
+            total += (int)c[k] - 1;
+            store_slot(&counts[g], 0u);
+          }
+        }
+      }
+      s_count[0] = lost ? -1 : total;
+    }
+    // every group's partial of block b, in group order (this group's from registers)
     float acc = 0.0f;
-    const int own = count;
-    count = 0;
+    bool lost = false;
     for (int g0 = 0; g0 < p.groups; g0 += kBatch) {
-      float x[kBatch];
-      int c[kBatch];
+      uint32_t x[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int g = g0 + k;
-        const bool other = g < p.groups && g != group;
-        x[k] = other && b < n ? __hip_atomic_load(&part[(int64_t)g * p.width + b], __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : (g == group ? v : 0.0f);
-        c[k] = other ? __hip_atomic_load(&p.part_count[(int64_t)out_row * p.groups + g], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT)
-                     : (g == group ? own : 0);
+        x[k] = g < p.groups && g != group && b < n ? load_slot(&part[(int64_t)g * p.width + b]) : 1u;
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
-        acc = use_max ? fmaxf(acc, x[k]) : acc + x[k];
-        count += c[k];
+        const int g = g0 + k;
+        float xv = 0.0f;
+        if (g == group) {
+          xv = v;
+        } else if (g < p.groups && b < n) {
+          x[k] = landed(&part[(int64_t)g * p.width + b], x[k]);
+          lost |= x[k] == 0u;
+          xv = __builtin_bit_cast(float, x[k] - 1u);
+          store_slot(&part[(int64_t)g * p.width + b], 0u);
+        }
+        acc = use_max ? fmaxf(acc, xv) : acc + xv;
       }
     }
-    v = acc;
+    __syncthreads();
+    count = s_count[0];
+    v = lost ? NAN : acc;
+    if (count < 0) {  // a count never landed: the row is left without evidence
+      if (b < p.width) p.shares[(int64_t)out_row * p.shares_stride + b] = NAN;
+      return;
+    }
   }
   // the whole-row rules: NaN without evidence, the mean over contributing pairs, or the max
   // renormalised over the row
@@ -751,7 +814,7 @@ __global__ __launch_bounds__(kSplitThreads) void combine_kernel(const Params p) 
   __shared__ float s_red[NT / kWave];
   const int row = blockIdx.x;
   const int K = p.groups;
-  const float *part = p.part + (int64_t)row * K * p.width;
+  float *part = p.part + (int64_t)row * K * p.width;
   float *out = p.shares + (int64_t)row * p.shares_stride;
   int contributors = 0;
   for (int g0 = 0; g0 < K; g0 += kBatch) {  // kBatch counts in flight
@@ -761,8 +824,13 @@ __global__ __launch_bounds__(kSplitThreads) void combine_kernel(const Params p) 
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) contributors += c[k];
   }
+  __syncthreads();  // every thread has read the counts: they are cleared for the next call
+  for (int g = threadIdx.x; g < K; g += NT) p.part_count[(int64_t)row * K + g] = 0;
   if (contributors == 0) {  // no evidence about the row, tile_shares.py:103
-    for (int b = threadIdx.x; b < p.width; b += NT) out[b] = NAN;
+    for (int b = threadIdx.x; b < p.width; b += NT) {
+      out[b] = NAN;
+      for (int g = 0; g < K; ++g) part[(int64_t)g * p.width + b] = 0.0f;
+    }
     return;
   }
   const bool use_max = p.aggregate == EKV_AGG_MAX;
@@ -775,6 +843,9 @@ __global__ __launch_bounds__(kSplitThreads) void combine_kernel(const Params p) 
       for (int k = 0; k < kBatch; ++k) x[k] = g0 + k < K ? part[(int64_t)(g0 + k) * p.width + b] : 0.0f;
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) v = use_max ? fmaxf(v, x[k]) : v + x[k];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (g0 + k < K) part[(int64_t)(g0 + k) * p.width + b] = 0.0f;  // cleared for the next call
     }
     local_total += v;
     out[b] = use_max ? v : v / (float)contributors;
