@@ -546,8 +546,11 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[cls(r)], 1)] = r;
 }
 
+// At most 64 VGPRs (8 waves per SIMD), so that two 16-wave sorting workgroups share a CU where their
+// LDS allows it (sorts of up to 8192 keys take 64 KB): at 82 VGPRs one held the CU alone.
 template <int MAX_ITEMS>
-__global__ __launch_bounds__(kSortThreads) void mm_sort_kernel(const MaxminParams m) {
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void mm_sort_kernel(const MaxminParams m) {
   using Largest = typename RequestSort<MAX_ITEMS>::storage_type;
   constexpr int kMid = MAX_ITEMS < 8 ? MAX_ITEMS : 8;
   static_assert(sizeof(typename RequestSort<1>::storage_type) <= sizeof(Largest) &&
