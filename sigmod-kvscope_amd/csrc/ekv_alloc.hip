@@ -62,6 +62,7 @@ struct State {
   // key with that prefix is kept and the later passes have nothing to rank (done_tie: in a pass
   // over the tie key, among the blocks at the gain threshold)
   int done, done_tie;
+  int arrivals, pad;  // a pass's workgroups that have flushed their histogram (0 between passes)
 };
 
 struct RowStat {
@@ -158,11 +159,6 @@ constexpr int kRun = 8;  // blocks per thread per step of the per-row loops
 
 __device__ __forceinline__ double weight_of(const Params &p, int r) { return p.weights != nullptr ? p.weights[r] : 1.0; }
 
-__global__ __launch_bounds__(kThreads) void clear_kernel(State *s) {
-  unsigned long long *w = (unsigned long long *)s;
-  for (int i = threadIdx.x; i < (int)(sizeof(State) / 8); i += kThreads) w[i] = 0ull;
-}
-
 // one wave per request: its total, its pinned and open blocks
 __global__ __launch_bounds__(kWave) void prepare_kernel(const Params p) {
   __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
@@ -187,9 +183,14 @@ __global__ __launch_bounds__(kWave) void prepare_kernel(const Params p) {
 }
 
 // the requests' pinned, existing and open blocks, summed over the rows' statistics by one
-// workgroup, then the budget's mode (allocation.py:57-76) and the select's start
+// workgroup, then the budget's mode (allocation.py:57-76) and the select's start; the state
+// (histogram, flags, counters) is cleared first
 __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
   __shared__ long long s_red[3][kThreads / kWave];
+  {
+    unsigned long long *w = (unsigned long long *)p.state;
+    for (int i = threadIdx.x; i < (int)(sizeof(State) / 8); i += kThreads) w[i] = 0ull;
+  }
   long long v[3] = {0, 0, 0};  // must, sizes, open_total
   for (int r = threadIdx.x; r < p.rows; r += kThreads) {
     const RowStat st = p.row_stat[r];
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
     v[k] = wave_sum_i64(v[k]);
     if (lane_id() == 0) s_red[k][wave] = v[k];
   }
-  __syncthreads();
+  __syncthreads();  // also orders the clearing stores before thread 0's
   if (threadIdx.x != 0) return;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -255,14 +256,78 @@ __device__ __forceinline__ unsigned long long tie_key(int r, int b) {
 // the tie key's width: 16 bits of request below the block's bits (14 up to 16384 blocks, else 18)
 inline int tie_bits(int width) { return width <= (1 << 14) ? 30 : 34; }
 
-// one radix pass: the histogram of the `bits`-wide digit at `shift` over the open blocks whose key
+// The digit where the k_rem-th largest key lies, and the next pass's prefix, from the pass's
+// histogram: thread t holds the kBins / kThreads digits below kBins - (kBins / kThreads) t, in
+// descending order.  The histogram is read with device-coherent loads (the pass's workgroups added
+// into it with device-scope atomics from every XCD) and cleared for the next pass.
+__device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_pass) {
+  constexpr int kPer = kBins / kThreads;
+  __shared__ long long s_scan[kThreads / kWave];
+  __shared__ int s_whole;
+  State *s = p.state;
+  const int t = threadIdx.x;
+  if (t == 0) s_whole = 0;
+  long long h[kPer], mine = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    h[i] = (long long)__hip_atomic_load(&s->hist[kBins - 1 - (kPer * t + i)], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    mine += h[i];
+  }
+  // inclusive scan over the threads: the keys at digits >= this thread's lowest
+  const int lane = lane_id(), wave = t / kWave;
+  long long inc = mine;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const long long up = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += up;
+  }
+  if (lane == kWave - 1) s_scan[wave] = inc;
+  __syncthreads();
+  long long base = 0;
+  for (int w = 0; w < wave; ++w) base += s_scan[w];
+  inc += base;
+  long long before = inc - mine;
+  const long long k_rem = s->k_rem;
+  __syncthreads();
+  if (before < k_rem && inc >= k_rem) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      if (before < k_rem && before + h[i] >= k_rem) {
+        s->prefix |= (unsigned long long)(kBins - 1 - (kPer * t + i)) << shift;
+        s->k_rem = k_rem - before;
+        if (before + h[i] == k_rem) s_whole = 1;  // the bucket ends the free blocks
+      }
+      before += h[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) s->hist[kBins - 1 - (kPer * t + i)] = 0ull;
+  __syncthreads();
+  if (t == 0) {
+    s->mask |= ((1ull << bits) - 1ull) << shift;
+    if (s_whole) {
+      s->done = 1;
+      s->done_tie = last_gain_pass < 0 ? 1 : 0;
+    } else if (last_gain_pass > 0) {  // the gain threshold is complete: the tie passes start
+      s->threshold = s->prefix;
+      s->prefix = 0ull;
+      s->mask = 0ull;
+    }
+  }
+}
+
+// One radix pass: the histogram of the `bits`-wide digit at `shift` over the open blocks whose key
 // matches the prefix so far (tie passes: the blocks at the gain threshold, over the tie key).
-// Workgroup w takes rows w, w + grid, ..., so each workgroup flushes its LDS histogram to the global
-// one once.
+// Workgroup w takes rows w, w + grid, ..., so each workgroup adds its LDS histogram into the global
+// one once, with device-scope atomics; once they have completed it counts its arrival, and the
+// pass's last workgroup picks the digit (pick_digit), so no second kernel runs per pass.
+// last_gain_pass: 1 on the last gain pass, 0 on the others, -1 on tie passes.
 template <bool TIE>
-__global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits) {
+__global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits, int last_gain_pass) {
   __shared__ unsigned int s_hist[kBins];
-  const State *s = p.state;
+  __shared__ int s_last;
+  State *s = p.state;
   if (s->mode != kSelect || s->error || s->done) return;
   for (int i = threadIdx.x; i < kBins; i += kThreads) s_hist[i] = 0u;
   __syncthreads();
@@ -310,67 +375,16 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   __syncthreads();
   for (int i = threadIdx.x; i < kBins; i += kThreads) {
     const unsigned int c = s_hist[i];
-    if (c) atomicAdd(&p.state->hist[i], (unsigned long long)c);
+    if (c) __hip_atomic_fetch_add(&s->hist[i], (unsigned long long)c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// the digit where the k_rem-th largest key lies; the next pass's prefix.  Thread t holds the
-// kBins / kThreads digits below kBins - (kBins / kThreads) t, in descending order.
-__global__ __launch_bounds__(kThreads) void pick_kernel(const Params p, int shift, int bits, int last_gain_pass) {
-  constexpr int kPer = kBins / kThreads;
-  __shared__ long long s_scan[kThreads / kWave];
-  __shared__ int s_whole;
-  State *s = p.state;
-  if (s->mode != kSelect || s->error || s->done) return;
-  const int t = threadIdx.x;
-  if (t == 0) s_whole = 0;
-  long long h[kPer], mine = 0;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    h[i] = (long long)s->hist[kBins - 1 - (kPer * t + i)];
-    mine += h[i];
-  }
-  // inclusive scan over the threads: the keys at digits >= this thread's lowest
-  const int lane = lane_id(), wave = t / kWave;
-  long long inc = mine;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const long long up = __shfl_up(inc, d, kWave);
-    if (lane >= d) inc += up;
-  }
-  if (lane == kWave - 1) s_scan[wave] = inc;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's adds have completed
   __syncthreads();
-  long long base = 0;
-  for (int w = 0; w < wave; ++w) base += s_scan[w];
-  inc += base;
-  long long before = inc - mine;
-  const long long k_rem = s->k_rem;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(&s->arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
   __syncthreads();
-  if (before < k_rem && inc >= k_rem) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      if (before < k_rem && before + h[i] >= k_rem) {
-        s->prefix |= (unsigned long long)(kBins - 1 - (kPer * t + i)) << shift;
-        s->k_rem = k_rem - before;
-        if (before + h[i] == k_rem) s_whole = 1;  // the bucket ends the free blocks
-      }
-      before += h[i];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) s->hist[kBins - 1 - (kPer * t + i)] = 0ull;
-  __syncthreads();
-  if (t == 0) {
-    s->mask |= ((1ull << bits) - 1ull) << shift;
-    if (s_whole) {
-      s->done = 1;
-      s->done_tie = last_gain_pass < 0 ? 1 : 0;
-    } else if (last_gain_pass > 0) {  // the gain threshold is complete: the tie passes start
-      s->threshold = s->prefix;
-      s->prefix = 0ull;
-      s->mask = 0ull;
-    }
-  }
+  if (!s_last) return;
+  if (threadIdx.x == 0) s->arrivals = 0;
+  pick_digit(p, shift, bits, last_gain_pass);
 }
 
 __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
@@ -1212,22 +1226,20 @@ namespace alloc {
 // The `sum` pipeline on prepared parameters (state and row statistics in place).
 int launch_sum(Params p, hipStream_t s) {
   const int rows = p.rows;
-  hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
   // the gain threshold, kDigitBits at a time from the top of the 64-bit key
   for (int top = 64; top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
-    hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, shift == 0 ? 1 : 0);
+    hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits,
+                       shift == 0 ? 1 : 0);
   }
   // among the blocks at the threshold: newer block, earlier request (the tie key)
   static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
   for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
-    hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits);
-    hipLaunchKernelGGL(alloc::pick_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
+    hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
   }
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
@@ -1362,7 +1374,6 @@ namespace alloc {
 // The `maxmin` pipeline on prepared parameters (every workspace pointer in place).
 int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   Params &p = m.p;
-  hipLaunchKernelGGL(alloc::clear_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p.state);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const bool wide = width > alloc::kMaxWidth;
