@@ -732,41 +732,25 @@ void shares_wave_kernel(const Params p) {
     if (!s_last) return;
     // this group's own slots, written before it knew it was last, are cleared as well
     if (b < n) store_slot(&part[(int64_t)group * p.width + b], 0u);
-    // the contributor counts, by one thread (a slot is cleared only after its last read)
     if (threadIdx.x == 0) {
       store_slot(&counts[group], 0u);
       __hip_atomic_store(&p.arrivals[out_row], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int total = count;
-      bool lost = false;
-      for (int g0 = 0; g0 < p.groups; g0 += kBatch) {
-        uint32_t c[kBatch];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int g = g0 + k;
-          c[k] = g < p.groups && g != group ? load_slot(&counts[g]) : 1u;
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-          const int g = g0 + k;
-          if (g < p.groups && g != group) {
-            c[k] = landed(&counts[g], c[k]);
-            lost |= c[k] == 0u;
-            total += (int)c[k] - 1;
-            store_slot(&counts[g], 0u);
-          }
-        }
-      }
-      s_count[0] = lost ? -1 : total;
     }
-    // every group's partial of block b, in group order (this group's from registers)
+    // every group's partial of block b, in group order (this group's from registers), and, by
+    // thread 0 in the same batches, their contributor counts (a count slot is read by one thread
+    // only, so that it is cleared after its last read)
     float acc = 0.0f;
-    bool lost = false;
+    int total = count;
+    bool lost = false, lost_count = false;
+    const bool counter = threadIdx.x == 0;
     for (int g0 = 0; g0 < p.groups; g0 += kBatch) {
-      uint32_t x[kBatch];
+      uint32_t x[kBatch], c[kBatch];
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int g = g0 + k;
-        x[k] = g < p.groups && g != group && b < n ? load_slot(&part[(int64_t)g * p.width + b]) : 1u;
+        const bool other = g < p.groups && g != group;
+        x[k] = other && b < n ? load_slot(&part[(int64_t)g * p.width + b]) : 1u;
+        c[k] = other && counter ? load_slot(&counts[g]) : 1u;
       }
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
@@ -774,15 +758,24 @@ void shares_wave_kernel(const Params p) {
         float xv = 0.0f;
         if (g == group) {
           xv = v;
-        } else if (g < p.groups && b < n) {
-          x[k] = landed(&part[(int64_t)g * p.width + b], x[k]);
-          lost |= x[k] == 0u;
-          xv = __builtin_bit_cast(float, x[k] - 1u);
-          store_slot(&part[(int64_t)g * p.width + b], 0u);
+        } else if (g < p.groups) {
+          if (b < n) {
+            x[k] = landed(&part[(int64_t)g * p.width + b], x[k]);
+            lost |= x[k] == 0u;
+            xv = __builtin_bit_cast(float, x[k] - 1u);
+            store_slot(&part[(int64_t)g * p.width + b], 0u);
+          }
+          if (counter) {
+            c[k] = landed(&counts[g], c[k]);
+            lost_count |= c[k] == 0u;
+            total += (int)c[k] - 1;
+            store_slot(&counts[g], 0u);
+          }
         }
         acc = use_max ? fmaxf(acc, xv) : acc + xv;
       }
     }
+    if (counter) s_count[0] = lost_count ? -1 : total;
     __syncthreads();
     count = s_count[0];
     v = lost ? NAN : acc;
