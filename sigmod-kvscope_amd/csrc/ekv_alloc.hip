@@ -435,6 +435,8 @@ struct MaxminParams {
   int32_t *order;     // the requests, longest first: the sorting workgroups' order
   int32_t *level_count;  // per level j / kLevels, the requests' counts summed
   uint16_t *level_pos;   // per request and level j / kLevels, its position there
+  int32_t *level_count2;  // the second pass: per level low + j / kLevels^2 inside the first walk's bracket
+  uint16_t *level_pos2;   // per request and such level, its position there
   // requests wider than a sort in LDS (width > kMaxWidth): the device-wide segmented sort's inputs
   unsigned long long *keys_in;  // [rows][width]
   int32_t *vals_in;             // [rows][width]
@@ -543,7 +545,10 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   __shared__ int s_count[kOrderClasses], s_next[kOrderClasses];
   const int tid = threadIdx.x;
   const int rows = m.p.rows;
-  for (int j = tid; j < kLevels; j += kSortThreads) m.level_count[j] = 0;  // summed into by mm_levels_kernel
+  for (int j = tid; j < kLevels; j += kSortThreads) {  // summed into by the two level-count passes
+    m.level_count[j] = 0;
+    m.level_count2[j] = 0;
+  }
   if (tid < kOrderClasses) s_count[tid] = 0;
   __syncthreads();
   auto cls = [&](int r) { return min(m.p.row_stat[r].n / kOrderStep, kOrderClasses - 1); };
@@ -561,9 +566,10 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
 }
 
 // At most 64 VGPRs (8 waves per SIMD), so that two 16-wave sorting workgroups share a CU where their
-// LDS allows it (sorts of up to 8192 keys take 64 KB): at 82 VGPRs one held the CU alone.
+// LDS allows it (sorts of up to 8192 keys take 64 KB): at 82 VGPRs one held the CU alone.  The
+// 12-key sort's 96 KB of LDS keeps it alone on a CU whatever its registers.
 template <int MAX_ITEMS>
-__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(MAX_ITEMS <= 8 ? 8 : 4)))
 void mm_sort_kernel(const MaxminParams m) {
   using Largest = typename RequestSort<MAX_ITEMS>::storage_type;
   constexpr int kMid = MAX_ITEMS < 8 ? MAX_ITEMS : 8;
@@ -735,6 +741,69 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
   }
 }
 
+// The first kLevelBits steps of the bisection over counts summed at kLevels levels: [jl, jh] of
+// those levels, jh = jl + 1 (the same decisions: a level rises when its count fits the free blocks).
+__device__ __forceinline__ void walk_levels(const int *s_level, long long free_blocks, int &jl, int &jh) {
+  jl = 0;
+  jh = kLevels;
+  for (int it = 0; it < kLevelBits; ++it) {
+    const int jm = (jl + jh) >> 1;
+    if ((long long)s_level[jm] <= free_blocks) jl = jm; else jh = jm;
+  }
+}
+
+// The second level-count pass: the next kLevelBits steps the same way.  Every workgroup repeats the
+// first walk (the summed counts staged in LDS), then counts each of its requests at the levels
+// low + j / kLevels^2 (0 < j < kLevels) inside the walk's bracket [low, high] -- exactly the mids
+// the bisection's next steps visit -- searching only between the request's positions at low and
+// high from the first pass.
+__global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminParams m) {
+  constexpr int kMine = (kLevels + kLevelThreads - 1) / kLevelThreads;
+  __shared__ int s_level[kLevels];
+  const Params &p = m.p;
+  const State *s = p.state;
+  if (s->mode != kSelect || s->error) return;
+  for (int j = threadIdx.x; j < kLevels; j += kLevelThreads) s_level[j] = m.level_count[j];
+  __syncthreads();
+  int jl, jh;
+  walk_levels(s_level, s->free_blocks, jl, jh);
+  const double low = (double)jl / kLevels;
+  constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
+  int mine[kMine];
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) mine[i] = 0;
+  for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    const MaxminRow mr = m.mrow[r];
+    const int open = mr.open;
+    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+    const int lo0 = jl > 0 ? pos_row[jl] : 0;
+    const int hi0 = jh < kLevels ? pos_row[jh] : open;
+    const double *pre = m.prefix + (int64_t)r * p.width;
+    const double shift = 2.0 * (double)r;
+    uint16_t *pos2 = m.level_pos2 + (int64_t)r * kLevels;
+#pragma unroll
+    for (int i = 0; i < kMine; ++i) {
+      const int j = i * kLevelThreads + threadIdx.x;
+      if (j < 1 || j >= kLevels) continue;
+      const double level = low + (double)j * kSub;  // exact: both terms are multiples of kSub
+      const double need = level - mr.base;
+      const double q = (need - 1e-12) + shift;
+      int a = lo0, b = hi0;
+      while (a < b) {  // first position whose shifted total is >= q
+        const int c = (a + b) >> 1;
+        if (pre[c] + shift < q) a = c + 1; else b = c;
+      }
+      pos2[j] = (uint16_t)a;
+      mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMine; ++i) {
+    const int j = i * kLevelThreads + threadIdx.x;
+    if (j >= 1 && j < kLevels && mine[i] > 0) atomicAdd(&m.level_count2[j], mine[i]);
+  }
+}
+
 // the level's bisection and the leftover, one workgroup
 // RPT: requests per thread (1, 2, 4 or 8 by the request count), so the common case keeps its state
 // in registers
@@ -775,16 +844,21 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
     pos = a;
     return need <= 1e-12 ? 0 : min(a + 1, open[j]);
   };
-  // the first kLevelBits steps, over the summed counts at the levels j / kLevels
+  // the first 2 kLevelBits steps: walks over the summed counts of the two level-count passes, at
+  // the levels j / kLevels, then low + j / kLevels^2 inside the first walk's bracket
   __shared__ int s_level[kLevels];
   for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count[j];
   __syncthreads();
-  int jl = 0, jh = kLevels;
-  for (int it = 0; it < kLevelBits; ++it) {
-    const int jm = (jl + jh) >> 1;
-    if ((long long)s_level[jm] <= free_blocks) jl = jm; else jh = jm;
-  }
-  double low = (double)jl / kLevels, high = (double)jh / kLevels;
+  int jl, jh;
+  walk_levels(s_level, free_blocks, jl, jh);
+  __syncthreads();
+  for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count2[j];
+  __syncthreads();
+  int jl2, jh2;
+  walk_levels(s_level, free_blocks, jl2, jh2);
+  constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
+  const double low1 = (double)jl / kLevels;
+  double low = low1 + (double)jl2 * kSub, high = low1 + (double)jh2 * kSub;
   // the brackets those steps leave: the positions at low and high, where each side has moved.  A
   // request's count never falls as the level rises, so one whose counts at low and high agree keeps
   // that count at every level between them.
@@ -793,20 +867,22 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
   for (int j = 0; j < kRowsPerThread; ++j) {
     f_low[j] = f_high[j] = f_mid[j] = 0;
     if (tid + j * kBisectThreads >= p.rows) continue;
-    // the positions at the levels reached come from mm_levels_kernel; the ends 0 and 1 (never a
-    // step's level) are searched, for the counts there
+    // the positions at the levels reached come from the level-count passes (a bracket end that the
+    // second walk did not move is a first-pass level); the ends 0 and 1 (never a step's level) are
+    // searched, for the counts there
     const int r = tid + j * kBisectThreads;
     const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+    const uint16_t *pos2_row = m.level_pos2 + (int64_t)r * kLevels;
     int pos_low, pos_high;
-    if (jl > 0) {
-      pos_low = pos_row[jl];
+    if (jl2 > 0 || jl > 0) {
+      pos_low = jl2 > 0 ? pos2_row[jl2] : pos_row[jl];
       f_low[j] = (low - base[j]) <= 1e-12 ? 0 : min(pos_low + 1, open[j]);
     } else {
       f_low[j] = count_at(j, low, pos_low);
       pos_low = 0;
     }
-    if (jh < kLevels) {
-      pos_high = pos_row[jh];
+    if (jh2 < kLevels || jh < kLevels) {
+      pos_high = jh2 < kLevels ? pos2_row[jh2] : pos_row[jh];
       f_high[j] = (high - base[j]) <= 1e-12 ? 0 : min(pos_high + 1, open[j]);
     } else {
       f_high[j] = count_at(j, high, pos_high);
@@ -815,7 +891,7 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
     lo[j] = pos_low;
     hi[j] = pos_high;
   }
-  int it = kLevelBits;
+  int it = 2 * kLevelBits;
   while (it < 60) {
     const double mid = (low + high) / 2;
     long long local = 0, active = 0;
@@ -1251,7 +1327,7 @@ int launch_sum(Params p, hipStream_t s) {
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, order, level_count, level_pos, vals_out, prefix, total;
+  size_t state, row_stat, mrow, order, level_count, level_pos, level_count2, level_pos2, vals_out, prefix, total;
   size_t keys_in, vals_in, seg_begin, seg_end, sort_temp, sort_temp_bytes;  // rows wider than kMaxWidth
 };
 
@@ -1284,6 +1360,10 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
   l.level_pos = at;
   at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
+  l.level_count2 = at;
+  at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
+  l.level_pos2 = at;
+  at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
@@ -1315,6 +1395,8 @@ void set_maxmin_buffers(const MaxminLayout &l, uintptr_t base, alloc::MaxminPara
   m.order = (int32_t *)(base + l.order);
   m.level_count = (int32_t *)(base + l.level_count);
   m.level_pos = (uint16_t *)(base + l.level_pos);
+  m.level_count2 = (int32_t *)(base + l.level_count2);
+  m.level_pos2 = (uint16_t *)(base + l.level_pos2);
   if (l.sort_temp_bytes > 0) {
     m.keys_in = (unsigned long long *)(base + l.keys_in);
     m.vals_in = (int32_t *)(base + l.vals_in);
@@ -1412,6 +1494,7 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   else
     hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, level_grid, dim3(alloc::kLevelThreads), 0, s,
                        m);
+  hipLaunchKernelGGL(alloc::mm_levels2_kernel, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
   if (rows <= alloc::kBisectThreads)
     hipLaunchKernelGGL(alloc::mm_bisect_kernel<1>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   else if (rows <= 2 * alloc::kBisectThreads)
