@@ -500,6 +500,7 @@ constexpr int kSortThreads = 1024;
 
 template <int ITEMS>
 using RequestSort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
+constexpr int kSortLowBits = 24;  // the key bits the first sort leaves out
 
 template <int ITEMS>
 __device__ __forceinline__ void sort_request(const MaxminParams &m, const RowStat &st, int r,
@@ -525,7 +526,46 @@ __device__ __forceinline__ void sort_request(const MaxminParams &m, const RowSta
     keys[i] = (pos < n && !pinned) ? gain_key(share_value(st, score[i])) : 0ull;
     vals[i] = pos;
   }
-  RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage);
+  // Bits 24-63 first, five passes: shares computed from float32 scores that differ, differ there (by
+  // at least 2^28 in their float64 bits).  The sort is stable, so the order is final unless two
+  // neighbours agree there and the later one's bits 0-23 are larger; then the request is sorted
+  // again on all 64 bits, from that order (which keeps equal keys in block order).
+  __shared__ int s_resort;
+  if (threadIdx.x == 0) s_resort = 0;
+  RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage, kSortLowBits, 64);
+  __syncthreads();  // the sort's storage is free; s_resort is 0
+  unsigned long long *s_keys = reinterpret_cast<unsigned long long *>(&storage);
+  static_assert(sizeof(typename RequestSort<ITEMS>::storage_type) >= sizeof(unsigned long long) * ITEMS * kSortThreads,
+                "the sorted keys fit the sort's storage");
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) s_keys[i * kSortThreads + threadIdx.x] = keys[i];
+  __syncthreads();
+  bool unsorted = false;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int pos = i * kSortThreads + threadIdx.x;
+    if (pos > 0 && pos < n) {
+      const unsigned long long prev = s_keys[pos - 1], k = keys[i];
+      constexpr unsigned long long kLow = (1ull << kSortLowBits) - 1ull;
+      unsorted |= (k >> kSortLowBits) == (prev >> kSortLowBits) && (k & kLow) > (prev & kLow);
+    }
+  }
+  if (unsorted) s_resort = 1;
+  __syncthreads();
+  if (s_resort) {
+    // the keys and block indices back to their sorted order per thread (blocked), then all 64 bits
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) keys[i] = s_keys[threadIdx.x * ITEMS + i];
+    __syncthreads();
+    int *s_vals = reinterpret_cast<int *>(&storage);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) s_vals[i * kSortThreads + threadIdx.x] = vals[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) vals[i] = s_vals[threadIdx.x * ITEMS + i];
+    __syncthreads();
+    RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage);
+  }
   const int64_t row0 = (int64_t)r * p.width;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {  // striped: position i * kSortThreads + thread

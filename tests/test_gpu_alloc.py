@@ -198,6 +198,28 @@ def test_maxmin_float64_scores_zero_rows_and_long_rows():
         assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
 
 
+@pytest.mark.parametrize("spread", [2.0 ** -40, 2.0 ** -30, 2.0 ** -26])
+def test_maxmin_shares_that_differ_only_in_low_bits(spread):
+    # the per-request sort orders the top 40 bits of each share's key first and sorts again on all 64
+    # bits only when two neighbours agree there but are out of order below: shares a few float64
+    # ulps apart (1 + k * spread, a handful of distinct values per row) take that second sort, next to
+    # rows whose shares differ high up
+    rng = np.random.default_rng(int(-np.log2(spread)))
+    scores = []
+    for n in (8192, 4096, 3000, 1024, 700, 64):
+        s = 0.5 * (1.0 + rng.integers(0, 7, size=n) * spread)
+        if n == 3000:
+            s = rng.random(n)  # no close neighbours: the first sort stands
+        scores.append(s)
+    pinned = [oa.default_pins(len(s)) for s in scores]
+    total = sum(len(s) for s in scores)
+    for frac in (0.1, 0.5, 0.9):
+        budget = max(int(frac * total), sum(int(q.sum()) for q in pinned))
+        reqs = [allocation.Request(scores=s, pinned=q) for s, q in zip(scores, pinned)]
+        print(f"spread {spread}, budget {budget}", flush=True)
+        assert same(allocation.allocate(reqs, budget, "maxmin"), oa.allocate_maxmin(scores, pinned, budget)), frac
+
+
 def test_maxmin_ties_in_rows_sorted_in_lds():
     # each request's blocks are sorted in LDS (a stable radix sort by share desc, so equal shares keep
     # block order): rows full of exactly equal shares must keep the stable order the reference's
