@@ -48,6 +48,36 @@ def test_sum_float64_scores_and_explicit_pins():
         assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, weights, budget)), trial
 
 
+def test_sum_row_totals_are_numpy_sums_bit_for_bit():
+    # every ranking divides by NumPy's float64 sum of the clamped scores; a total one ulp off would
+    # shift each share by about an ulp, which the keep masks rarely show, so the totals are read back
+    # from the workspace (its state block, then one 24-byte statistic per row: the total first) and
+    # compared bit for bit: lengths across the leaf sizes (1..128), the pairwise splits and several
+    # 8192-value runs, with values over many binades so that the order of the additions shows
+    rng = np.random.default_rng(21)
+    lengths = [1, 2, 7, 8, 9, 15, 16, 17, 127, 128, 129, 136, 255, 256, 257, 1000, 1024, 4095, 4096,
+               4097, 8191, 8192, 8193, 12288, 16385, 20000]
+    width = max(lengths)
+    rows = len(lengths)
+    scores = np.zeros((rows, width))
+    for r, n in enumerate(lengths):
+        scores[r, :n] = rng.random(n) * 10.0 ** rng.integers(-12, 4, size=n)
+        scores[r, : n : 5] *= -1.0  # clamped to 0
+    state = allocation.sum_workspace_bytes(0) - 256
+    stat = allocation.sum_workspace_bytes(1) - allocation.sum_workspace_bytes(0)
+    workspace = torch.zeros(allocation.sum_workspace_bytes(rows), dtype=torch.uint8, device="cuda")
+    s_dev = torch.from_numpy(scores).cuda()
+    b_dev = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    allocation.sum_keep(s_dev, b_dev, budget=sum(lengths) // 2, workspace=workspace)
+    torch.cuda.synchronize()
+    raw = workspace.cpu().numpy()
+    base = (-workspace.data_ptr()) % 256 + state
+    for r, n in enumerate(lengths):
+        got = raw[base + r * stat: base + r * stat + 8].view(np.float64)[0]
+        want = np.maximum(scores[r, :n], 0.0).sum()
+        assert got.tobytes() == np.float64(want).tobytes(), (n, got, want)
+
+
 def test_sum_rows_past_one_reduction_run():
     # rows of more than 8192 blocks: NumPy's total adds two runs' pairwise sums
     rng = np.random.default_rng(8)
