@@ -305,8 +305,9 @@ int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blo
  * the lowest retained share (pinned shares plus the kept open blocks, each request's open blocks
  * taken in stable descending share order) by the reference's 60-step bisection of the level, then
  * gives the leftover one block at a time to the request of the lowest (retained share, index).
- * rows <= 8192, width <= 65535 (requests up to 12288 blocks sort in LDS, wider ones through a
- * device-wide segmented radix sort whose storage the workspace includes).  workspace:
+ * rows <= 65535 (past 8192 requests the bisection keeps each request's state in the workspace),
+ * width <= 65535 (requests up to 12288 blocks sort in LDS, wider ones through a device-wide
+ * segmented radix sort whose storage the workspace includes).  workspace:
  * ekv_rank_maxmin_workspace(rows, width) bytes of device memory.
  */
 size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width);
@@ -330,7 +331,7 @@ int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *
  * past the row and in every row that takes no part.  summary (int64[6], may be NULL): budget, blocks
  * of the requests, pinned blocks, status, requests, free.  workspace:
  * ekv_controller_keep_workspace(objective, rows, width) bytes the call may overwrite.  rows at most
- * 65535 (`sum`) or 8192 (`maxmin`), width at most 262144 (`sum`) or 65535 (`maxmin`).
+ * 65535, width at most 262144 (`sum`) or 65535 (`maxmin`).
  */
 size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width);
 int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,

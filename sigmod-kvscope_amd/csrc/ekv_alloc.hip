@@ -420,7 +420,8 @@ __global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
 
 // ---- maxmin --------------------------------------------------------------------------------
 constexpr int kBisectThreads = 1024;
-constexpr int kMaxMaxminRows = kBisectThreads * 8;  // at most 8 requests per bisection thread
+constexpr int kMaxMaxminRegRows = kBisectThreads * 8;  // at most 8 requests per bisection thread in registers
+constexpr int kMaxMaxminRows = 65535;                  // more than that many: the bisection state in memory
 
 struct MaxminRow {
   double base;  // NumPy's sum of the pinned shares
@@ -437,6 +438,10 @@ struct MaxminParams {
   uint16_t *level_pos;   // per request and level j / kLevels, its position there
   int32_t *level_count2;  // the second pass: per level low + j / kLevels^2 inside the first walk's bracket
   uint16_t *level_pos2;   // per request and such level, its position there
+  // more requests than the bisection's registers hold (mm_bisect_mem_kernel): each request's
+  // bracket, counts there and at the step's mid, and its count and retained share, in memory
+  int32_t *b_lo, *b_hi, *b_flo, *b_fhi, *b_fmid, *b_pmid, *b_count;
+  double *b_retained;
   // requests wider than a sort in LDS (width > kMaxWidth): the device-wide segmented sort's inputs
   unsigned long long *keys_in;  // [rows][width]
   int32_t *vals_in;             // [rows][width]
@@ -850,7 +855,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
 template <int RPT>
 __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminParams m) {
   constexpr int kRowsPerThread = RPT;
-  static_assert(RPT >= 1 && RPT * kBisectThreads <= kMaxMaxminRows, "requests per thread");
+  static_assert(RPT >= 1 && RPT * kBisectThreads <= kMaxMaxminRegRows, "requests per thread");
   __shared__ long long s_red[kBisectThreads / kWave];
   __shared__ double s_best[kBisectThreads / kWave];
   const Params &p = m.p;
@@ -1146,6 +1151,204 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
   }
 }
 
+// The bisection and the leftover for more requests than the register form holds: the same walks,
+// steps, wave-0 finish and leftover passes as mm_bisect_kernel, each request's state in memory and
+// every loop over the requests strided over the workgroup (requests r = tid, tid + 1024, ..., so a
+// scan chunk by chunk keeps index order).
+__global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const MaxminParams m) {
+  __shared__ long long s_red[kBisectThreads / kWave];
+  __shared__ double s_best[kBisectThreads / kWave];
+  __shared__ int s_level[kLevels];
+  const Params &p = m.p;
+  const State *s = p.state;
+  if (s->mode != kSelect || s->error) return;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const int rows = p.rows;
+  const long long free_blocks = s->free_blocks;
+  auto count_in = [&](int r, double base, int open, double level, int a, int b, int &pos) -> int {
+    const double need = level - base;
+    const double shift = 2.0 * (double)r;
+    const double q = (need - 1e-12) + shift;
+    const double *pre = m.prefix + (int64_t)r * p.width;
+    while (a < b) {  // first position whose shifted total is >= q
+      const int c = (a + b) >> 1;
+      if (pre[c] + shift < q) a = c + 1; else b = c;
+    }
+    pos = a;
+    return need <= 1e-12 ? 0 : min(a + 1, open);
+  };
+  // the first 2 kLevelBits steps: the two level-count passes' walks
+  for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count[j];
+  __syncthreads();
+  int jl, jh;
+  walk_levels(s_level, free_blocks, jl, jh);
+  __syncthreads();
+  for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count2[j];
+  __syncthreads();
+  int jl2, jh2;
+  walk_levels(s_level, free_blocks, jl2, jh2);
+  constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
+  const double low1 = (double)jl / kLevels;
+  double low = low1 + (double)jl2 * kSub, high = low1 + (double)jh2 * kSub;
+  for (int r = tid; r < rows; r += kBisectThreads) {
+    const MaxminRow mr = m.mrow[r];
+    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+    const uint16_t *pos2_row = m.level_pos2 + (int64_t)r * kLevels;
+    int pos_low, pos_high, f_low, f_high;
+    if (jl2 > 0 || jl > 0) {
+      pos_low = jl2 > 0 ? pos2_row[jl2] : pos_row[jl];
+      f_low = (low - mr.base) <= 1e-12 ? 0 : min(pos_low + 1, mr.open);
+    } else {
+      f_low = count_in(r, mr.base, mr.open, low, 0, mr.open, pos_low);
+      pos_low = 0;
+    }
+    if (jh2 < kLevels || jh < kLevels) {
+      pos_high = jh2 < kLevels ? pos2_row[jh2] : pos_row[jh];
+      f_high = (high - mr.base) <= 1e-12 ? 0 : min(pos_high + 1, mr.open);
+    } else {
+      f_high = count_in(r, mr.base, mr.open, high, 0, mr.open, pos_high);
+      pos_high = mr.open;
+    }
+    m.b_lo[r] = pos_low;
+    m.b_hi[r] = pos_high;
+    m.b_flo[r] = f_low;
+    m.b_fhi[r] = f_high;
+  }
+  int it = 2 * kLevelBits;
+  while (it < 60) {
+    const double mid = (low + high) / 2;
+    long long local = 0, active = 0;
+    for (int r = tid; r < rows; r += kBisectThreads) {
+      const MaxminRow mr = m.mrow[r];
+      active += m.b_flo[r] != m.b_fhi[r] ? 1 : 0;
+      int pos;
+      const int f = count_in(r, mr.base, mr.open, mid, m.b_lo[r], m.b_hi[r], pos);
+      m.b_fmid[r] = f;
+      m.b_pmid[r] = pos;
+      local += f;
+    }
+    const long long packed = block_sum<kBisectThreads>(local + (active << 32), s_red);
+    const long long total = packed & 0xffffffffll;
+    const bool up = total <= free_blocks;
+    if (up) low = mid; else high = mid;
+    for (int r = tid; r < rows; r += kBisectThreads) {
+      if (up) {
+        m.b_lo[r] = m.b_pmid[r];
+        m.b_flo[r] = m.b_fmid[r];
+      } else {
+        m.b_hi[r] = m.b_pmid[r];
+        m.b_fhi[r] = m.b_fmid[r];
+      }
+    }
+    ++it;
+    if ((packed >> 32) <= kWave) break;  // at most a wave's worth of requests can still change
+  }
+  if (it < 60) {
+    // the rest of the steps in wave 0 over the requests still changing, as in mm_bisect_kernel
+    __shared__ int s_nact, s_act_row[kWave], s_act_lo[kWave], s_act_hi[kWave], s_act_open[kWave];
+    __shared__ double s_act_base[kWave], s_level_pair[2];
+    if (tid == 0) s_nact = 0;
+    __syncthreads();
+    long long fixed_local = 0;
+    for (int r = tid; r < rows; r += kBisectThreads) {
+      const int fl = m.b_flo[r];
+      if (fl != m.b_fhi[r]) {
+        const MaxminRow mr = m.mrow[r];
+        const int i = atomicAdd(&s_nact, 1);
+        s_act_row[i] = r;
+        s_act_lo[i] = m.b_lo[r];
+        s_act_hi[i] = m.b_hi[r];
+        s_act_open[i] = mr.open;
+        s_act_base[i] = mr.base;
+      } else {
+        fixed_local += fl;
+      }
+    }
+    const long long fixed = block_sum<kBisectThreads>(fixed_local, s_red);  // its barriers publish the list
+    if (wave == 0) {
+      const bool mine = lane < s_nact;
+      const int r = mine ? s_act_row[lane] : 0;
+      int a_lo = mine ? s_act_lo[lane] : 0, a_hi = mine ? s_act_hi[lane] : 0;
+      const int a_open = mine ? s_act_open[lane] : 0;
+      const double a_base = mine ? s_act_base[lane] : 0.0;
+      for (; it < 60; ++it) {
+        const double mid = (low + high) / 2;
+        int f = 0, pos = a_lo;
+        if (mine) f = count_in(r, a_base, a_open, mid, a_lo, a_hi, pos);
+        const bool up = fixed + (long long)wave_sum_int(f) <= free_blocks;
+        if (up) {
+          low = mid;
+          a_lo = pos;
+        } else {
+          high = mid;
+          a_hi = pos;
+        }
+      }
+      if (lane == 0) {
+        s_level_pair[0] = low;
+        s_level_pair[1] = high;
+      }
+    }
+    __syncthreads();
+    low = s_level_pair[0];
+    high = s_level_pair[1];
+  }
+  // counts at the final level (searched inside each request's bracket, a superset of where it lies)
+  long long used = 0;
+  for (int r = tid; r < rows; r += kBisectThreads) {
+    const MaxminRow mr = m.mrow[r];
+    int pos;
+    const int c = count_in(r, mr.base, mr.open, low, m.b_lo[r], m.b_hi[r], pos);
+    m.b_count[r] = c;
+    m.b_retained[r] = mr.base + (c ? m.prefix[(int64_t)r * p.width + c - 1] : 0.0);
+    used += c;
+  }
+  long long leftover = free_blocks - block_sum<kBisectThreads>(used, s_red);
+  // the leftover by levels (allocation.py:157-166), as mm_bisect_kernel: one pass serves every
+  // request tied at the lowest level in index order, the scan taken chunk by chunk of requests
+  __shared__ int s_scan[kBisectThreads / kWave];
+  while (leftover > 0) {
+    double low_level = INFINITY;
+    for (int r = tid; r < rows; r += kBisectThreads)
+      if (m.b_count[r] < m.mrow[r].open) low_level = fmin(low_level, m.b_retained[r]);
+    for (int msk = 32; msk >= 1; msk >>= 1) low_level = fmin(low_level, __shfl_xor(low_level, msk, kWave));
+    if (lane == 0) s_best[wave] = low_level;
+    __syncthreads();
+    low_level = s_best[0];
+    for (int w = 1; w < kBisectThreads / kWave; ++w) low_level = fmin(low_level, s_best[w]);
+    __syncthreads();
+    if (low_level == INFINITY) break;  // every request keeps all its blocks
+    long long served = 0;  // blocks the tied requests of the earlier chunks take
+    for (int r0 = 0; r0 < rows; r0 += kBisectThreads) {
+      const int r = r0 + tid;
+      int c = 0, open = 0, take = 0;
+      double next_share = 0.0;
+      bool tied = false;
+      if (r < rows) {
+        c = m.b_count[r];
+        open = m.mrow[r].open;
+        tied = c < open && m.b_retained[r] == low_level;
+      }
+      if (tied) {
+        const RowStat st = p.row_stat[r];
+        next_share = share_of(p, st, r, m.vals_out[(int64_t)r * p.width + c]);
+        take = low_level + next_share == low_level ? open - c : 1;
+      }
+      int pass_total;
+      const long long before = served + block_exclusive_scan<kBisectThreads>(take, s_scan, pass_total);
+      const long long got = tied ? max(0LL, min((long long)take, leftover - before)) : 0LL;
+      if (got > 0) {
+        m.b_count[r] = c + (int)got;
+        if (take == 1) m.b_retained[r] = low_level + next_share;  // the level popped plus the kept block's share
+      }
+      served += pass_total;
+    }
+    leftover -= min(served, leftover);
+    __syncthreads();  // every request's count and share are stored before the next pass reads them
+  }
+  for (int r = tid; r < rows; r += kBisectThreads) m.mrow[r].counts = m.b_count[r];
+}
+
 __global__ __launch_bounds__(kThreads) void mm_keep_kernel(const MaxminParams m) {
   const Params &p = m.p;
   const int r = blockIdx.x;
@@ -1367,7 +1570,8 @@ int launch_sum(Params p, hipStream_t s) {
 namespace {
 
 struct MaxminLayout {
-  size_t state, row_stat, mrow, order, level_count, level_pos, level_count2, level_pos2, vals_out, prefix, total;
+  size_t state, row_stat, mrow, order, level_count, level_pos, level_count2, level_pos2, bisect, vals_out, prefix,
+      total;
   size_t keys_in, vals_in, seg_begin, seg_end, sort_temp, sort_temp_bytes;  // rows wider than kMaxWidth
 };
 
@@ -1404,6 +1608,8 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
   l.level_pos2 = at;
   at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
+  l.bisect = at;  // seven int32 arrays and one double array of rows entries (the memory bisection's state)
+  at = align256(at + (size_t)rows * (7 * sizeof(int32_t) + sizeof(double)) + 8 * 256);
   l.vals_out = at;
   at = align256(at + cells * 4);
   l.prefix = at;
@@ -1437,6 +1643,22 @@ void set_maxmin_buffers(const MaxminLayout &l, uintptr_t base, alloc::MaxminPara
   m.level_pos = (uint16_t *)(base + l.level_pos);
   m.level_count2 = (int32_t *)(base + l.level_count2);
   m.level_pos2 = (uint16_t *)(base + l.level_pos2);
+  {
+    const int rows = m.p.rows;  // set by the callers before the buffers
+    uintptr_t at = base + l.bisect;
+    auto take_ints = [&](int32_t *&dst) {
+      dst = (int32_t *)at;
+      at = (at + (size_t)rows * sizeof(int32_t) + 255) & ~(uintptr_t)255;
+    };
+    take_ints(m.b_lo);
+    take_ints(m.b_hi);
+    take_ints(m.b_flo);
+    take_ints(m.b_fhi);
+    take_ints(m.b_fmid);
+    take_ints(m.b_pmid);
+    take_ints(m.b_count);
+    m.b_retained = (double *)at;
+  }
   if (l.sort_temp_bytes > 0) {
     m.keys_in = (unsigned long long *)(base + l.keys_in);
     m.vals_in = (int32_t *)(base + l.vals_in);
@@ -1535,7 +1757,9 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
     hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, level_grid, dim3(alloc::kLevelThreads), 0, s,
                        m);
   hipLaunchKernelGGL(alloc::mm_levels2_kernel, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
-  if (rows <= alloc::kBisectThreads)
+  if (rows > alloc::kMaxMaxminRegRows)
+    hipLaunchKernelGGL(alloc::mm_bisect_mem_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
+  else if (rows <= alloc::kBisectThreads)
     hipLaunchKernelGGL(alloc::mm_bisect_kernel<1>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
   else if (rows <= 2 * alloc::kBisectThreads)
     hipLaunchKernelGGL(alloc::mm_bisect_kernel<2>, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);

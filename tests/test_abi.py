@@ -79,6 +79,9 @@ def test_shape_limits_are_refused_on_the_host():
         ekv_hip.call("ekv_rank_sum", P, wide, P, 0, 0, 0, 4, wide, 10, P, wide, 0, P, 1 << 20, 0)
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_rank_maxmin", P, 65536, P, 0, 0, 4, 65536, 10, P, 65536, 0, P, 1 << 20, 0)
+    # maxmin: more than 65535 requests
+    with pytest.raises(ValueError, match="rows"):
+        ekv_hip.call("ekv_rank_maxmin", P, 8, P, 0, 0, 65536, 8, 10, P, 8, 0, P, 1 << 30, 0)
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_controller_keep", ekv_hip.OBJ_MAXMIN, P, ekv_hip.F64, 65536, P, P, 0, 0, 0, 0, 4, 65536,
                      4, 0, 0.5, P, 65536, 0, P, 1 << 30, 0)

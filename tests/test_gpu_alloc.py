@@ -286,9 +286,10 @@ def test_maxmin_view_build_configuration():
         assert bad == 0 and int(summary[3]) == 0
 
 
-@pytest.mark.parametrize("rows", [1500, 3000, 6000, 8192])
+@pytest.mark.parametrize("rows", [1500, 3000, 6000, 8192, 8193, 20000])
 def test_maxmin_many_requests(rows):
-    # past 1024 requests each bisection thread carries 2, 4 or 8 of them
+    # past 1024 requests each bisection thread carries 2, 4 or 8 of them; past 8192 the bisection
+    # keeps every request's state in the workspace
     rng = np.random.default_rng(rows)
     sizes = rng.integers(1, 30, size=rows)
     scores = [rng.random(int(n)) for n in sizes]

@@ -103,6 +103,20 @@ def test_random_batches(seed):
     run(shares, lengths, evidence, fraction, recent, cap, audited, released, weights, objective)
 
 
+@pytest.mark.parametrize("rows", [8193, 12000])
+def test_maxmin_more_requests_than_the_bisection_registers(rows):
+    # past 8192 measured rows the bisection keeps each request's state in the workspace
+    rng = np.random.default_rng(rows)
+    width = 24
+    lengths = rng.integers(0, width + 4, size=rows)
+    evidence = rng.random(rows) < 0.9
+    shares = rng.dirichlet(np.full(width, 0.3), size=rows)
+    shares[::11, ::2] = shares[::11, :1]  # ties inside requests
+    for fraction in (0.3, 0.7):
+        print(f"maxmin: {rows} rows, fraction {fraction}", flush=True)
+        run(shares, lengths, evidence, fraction, 2, 3, None, None, None, "maxmin")
+
+
 @pytest.mark.parametrize("objective", ["sum", "maxmin"])
 def test_view_build_configuration_at_cap_256(objective):
     c = workloads.config4()
