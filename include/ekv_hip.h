@@ -306,8 +306,9 @@ int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blo
  * taken in stable descending share order) by the reference's 60-step bisection of the level, then
  * gives the leftover one block at a time to the request of the lowest (retained share, index).
  * rows <= 65535 (past 8192 requests the bisection keeps each request's state in the workspace),
- * width <= 65535 (requests up to 12288 blocks sort in LDS, wider ones through a device-wide
- * segmented radix sort whose storage the workspace includes).  workspace:
+ * width <= 262144 (requests up to 12288 blocks sort in LDS, wider ones through a device-wide
+ * segmented radix sort whose storage the workspace includes, with rows x width below 2^31; the
+ * level positions take 32 bits past 65535 blocks).  workspace:
  * ekv_rank_maxmin_workspace(rows, width) bytes of device memory.
  */
 size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width);
@@ -331,7 +332,7 @@ int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *
  * past the row and in every row that takes no part.  summary (int64[6], may be NULL): budget, blocks
  * of the requests, pinned blocks, status, requests, free.  workspace:
  * ekv_controller_keep_workspace(objective, rows, width) bytes the call may overwrite.  rows at most
- * 65535, width at most 262144 (`sum`) or 65535 (`maxmin`).
+ * 65535, width at most 262144 (`maxmin` past 12288 blocks: rows x width below 2^31).
  */
 size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width);
 int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,

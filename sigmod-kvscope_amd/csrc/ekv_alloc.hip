@@ -44,7 +44,7 @@ namespace alloc {
 
 constexpr int kThreads = 256;
 constexpr int kMaxWidth = 12288;          // maxmin: a request sorted in one workgroup's LDS
-constexpr int kMaxMaxminWidth = 65535;    // maxmin past it: positions kept in 16 bits
+constexpr int kMaxMaxminWidth = 1 << 18;  // maxmin: positions in 16 bits up to 65535 blocks, 32 past it
 constexpr int kMaxSumWidth = 1 << 18;     // sum: the per-row loops stream the row; the tie key's block field
 constexpr int kMaxRows = 65535;  // the tie key holds the request in 16 bits
 
@@ -435,9 +435,10 @@ struct MaxminParams {
   double *prefix;     // per request, the running totals of its open shares in that order
   int32_t *order;     // the requests, longest first: the sorting workgroups' order
   int32_t *level_count;  // per level j / kLevels, the requests' counts summed
-  uint16_t *level_pos;   // per request and level j / kLevels, its position there
+  void *level_pos;       // per request and level j / kLevels, its position there (16 or 32 bits: pos32)
   int32_t *level_count2;  // the second pass: per level low + j / kLevels^2 inside the first walk's bracket
-  uint16_t *level_pos2;   // per request and such level, its position there
+  void *level_pos2;       // per request and such level, its position there
+  int32_t pos32;          // positions in 32 bits (rows wider than 65535 blocks)
   // more requests than the bisection's registers hold (mm_bisect_mem_kernel): each request's
   // bracket, counts there and at the step's mid, and its count and retained share, in memory
   int32_t *b_lo, *b_hi, *b_flo, *b_fhi, *b_fmid, *b_pmid, *b_count;
@@ -454,6 +455,18 @@ struct MaxminParams {
 // every one exact in float64, as are the steps' mids (low + high) / 2 on the way there)
 constexpr int kLevelBits = 10;
 constexpr int kLevels = 1 << kLevelBits;
+
+// a stored level position of request r at level j (the arrays hold rows x kLevels entries)
+__device__ __forceinline__ int pos_at(const MaxminParams &m, const void *a, int r, int j) {
+  const int64_t i = (int64_t)r * kLevels + j;
+  return m.pos32 ? (int)reinterpret_cast<const uint32_t *>(a)[i] : (int)reinterpret_cast<const uint16_t *>(a)[i];
+}
+__device__ __forceinline__ void set_pos(const MaxminParams &m, void *a, int r, int j, int v) {
+  const int64_t i = (int64_t)r * kLevels + j;
+  if (m.pos32) reinterpret_cast<uint32_t *>(a)[i] = (uint32_t)v;
+  else reinterpret_cast<uint16_t *>(a)[i] = (uint16_t)v;
+}
+
 
 // per request, one wave: NumPy's sum of the pinned shares (the base) and the request's counts.  The
 // pinned blocks are listed in order first: in LDS, or for rows wider than it holds (WIDE) in the
@@ -762,7 +775,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
   const double *s_tot = CAP > 0 ? s_lds : pre;
   __syncthreads();
   const double shift = 2.0 * (double)r;
-  uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
+
 #pragma unroll
   for (int i = 0; i < kMine; ++i) {
     const int j = i * kLevelThreads + threadIdx.x;
@@ -775,7 +788,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminPa
       const int c = (a + b) >> 1;
       if (s_tot[c] + shift < q) a = c + 1; else b = c;
     }
-    pos_row[j] = (uint16_t)a;
+    set_pos(m, m.level_pos, r, j, a);
     mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
   }
   }
@@ -820,12 +833,11 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
   for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
     const MaxminRow mr = m.mrow[r];
     const int open = mr.open;
-    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
-    const int lo0 = jl > 0 ? pos_row[jl] : 0;
-    const int hi0 = jh < kLevels ? pos_row[jh] : open;
+    const int lo0 = jl > 0 ? pos_at(m, m.level_pos, r, jl) : 0;
+    const int hi0 = jh < kLevels ? pos_at(m, m.level_pos, r, jh) : open;
     const double *pre = m.prefix + (int64_t)r * p.width;
     const double shift = 2.0 * (double)r;
-    uint16_t *pos2 = m.level_pos2 + (int64_t)r * kLevels;
+
 #pragma unroll
     for (int i = 0; i < kMine; ++i) {
       const int j = i * kLevelThreads + threadIdx.x;
@@ -838,7 +850,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
         const int c = (a + b) >> 1;
         if (pre[c] + shift < q) a = c + 1; else b = c;
       }
-      pos2[j] = (uint16_t)a;
+      set_pos(m, m.level_pos2, r, j, a);
       mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
     }
   }
@@ -916,18 +928,17 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
     // second walk did not move is a first-pass level); the ends 0 and 1 (never a step's level) are
     // searched, for the counts there
     const int r = tid + j * kBisectThreads;
-    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
-    const uint16_t *pos2_row = m.level_pos2 + (int64_t)r * kLevels;
+
     int pos_low, pos_high;
     if (jl2 > 0 || jl > 0) {
-      pos_low = jl2 > 0 ? pos2_row[jl2] : pos_row[jl];
+      pos_low = jl2 > 0 ? pos_at(m, m.level_pos2, r, jl2) : pos_at(m, m.level_pos, r, jl);
       f_low[j] = (low - base[j]) <= 1e-12 ? 0 : min(pos_low + 1, open[j]);
     } else {
       f_low[j] = count_at(j, low, pos_low);
       pos_low = 0;
     }
     if (jh2 < kLevels || jh < kLevels) {
-      pos_high = jh2 < kLevels ? pos2_row[jh2] : pos_row[jh];
+      pos_high = jh2 < kLevels ? pos_at(m, m.level_pos2, r, jh2) : pos_at(m, m.level_pos, r, jh);
       f_high[j] = (high - base[j]) <= 1e-12 ? 0 : min(pos_high + 1, open[j]);
     } else {
       f_high[j] = count_at(j, high, pos_high);
@@ -1192,18 +1203,17 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const Max
   double low = low1 + (double)jl2 * kSub, high = low1 + (double)jh2 * kSub;
   for (int r = tid; r < rows; r += kBisectThreads) {
     const MaxminRow mr = m.mrow[r];
-    const uint16_t *pos_row = m.level_pos + (int64_t)r * kLevels;
-    const uint16_t *pos2_row = m.level_pos2 + (int64_t)r * kLevels;
+
     int pos_low, pos_high, f_low, f_high;
     if (jl2 > 0 || jl > 0) {
-      pos_low = jl2 > 0 ? pos2_row[jl2] : pos_row[jl];
+      pos_low = jl2 > 0 ? pos_at(m, m.level_pos2, r, jl2) : pos_at(m, m.level_pos, r, jl);
       f_low = (low - mr.base) <= 1e-12 ? 0 : min(pos_low + 1, mr.open);
     } else {
       f_low = count_in(r, mr.base, mr.open, low, 0, mr.open, pos_low);
       pos_low = 0;
     }
     if (jh2 < kLevels || jh < kLevels) {
-      pos_high = jh2 < kLevels ? pos2_row[jh2] : pos_row[jh];
+      pos_high = jh2 < kLevels ? pos_at(m, m.level_pos2, r, jh2) : pos_at(m, m.level_pos, r, jh);
       f_high = (high - mr.base) <= 1e-12 ? 0 : min(pos_high + 1, mr.open);
     } else {
       f_high = count_in(r, mr.base, mr.open, high, 0, mr.open, pos_high);
@@ -1602,12 +1612,13 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   at = align256(at + (size_t)rows * sizeof(int32_t));
   l.level_count = at;
   at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
+  const size_t pos_bytes = width > 65535 ? sizeof(uint32_t) : sizeof(uint16_t);
   l.level_pos = at;
-  at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
+  at = align256(at + (size_t)rows * alloc::kLevels * pos_bytes);
   l.level_count2 = at;
   at = align256(at + (size_t)alloc::kLevels * sizeof(int32_t));
   l.level_pos2 = at;
-  at = align256(at + (size_t)rows * alloc::kLevels * sizeof(uint16_t));
+  at = align256(at + (size_t)rows * alloc::kLevels * pos_bytes);
   l.bisect = at;  // seven int32 arrays and one double array of rows entries (the memory bisection's state)
   at = align256(at + (size_t)rows * (7 * sizeof(int32_t) + sizeof(double)) + 8 * 256);
   l.vals_out = at;
@@ -1640,9 +1651,10 @@ void set_maxmin_buffers(const MaxminLayout &l, uintptr_t base, alloc::MaxminPara
   m.prefix = (double *)(base + l.prefix);
   m.order = (int32_t *)(base + l.order);
   m.level_count = (int32_t *)(base + l.level_count);
-  m.level_pos = (uint16_t *)(base + l.level_pos);
+  m.level_pos = (void *)(base + l.level_pos);
+  m.pos32 = m.p.width > 65535 ? 1 : 0;  // as the layout sized them
   m.level_count2 = (int32_t *)(base + l.level_count2);
-  m.level_pos2 = (uint16_t *)(base + l.level_pos2);
+  m.level_pos2 = (void *)(base + l.level_pos2);
   {
     const int rows = m.p.rows;  // set by the callers before the buffers
     uintptr_t at = base + l.bisect;
@@ -1685,6 +1697,9 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   if (rows < 0 || rows > alloc::kMaxMaxminRows || width < 1 || width > alloc::kMaxMaxminWidth)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: rows %d (max %d), width %d (max %d)", rows, alloc::kMaxMaxminRows,
                 width, alloc::kMaxMaxminWidth);
+  if (width > alloc::kMaxWidth && (int64_t)rows * width > INT_MAX)
+    return fail(EKV_EINVAL, "ekv_rank_maxmin: %d rows x %d blocks past the device-wide sort's 32-bit offsets", rows,
+                width);
   if (budget < 0) return fail(EKV_EINVAL, "ekv_rank_maxmin: the budget cannot be negative");
   if (rows == 0) return EKV_OK;
   const MaxminLayout l = maxmin_layout(rows, width);
@@ -1835,6 +1850,9 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
   if (rows < 0 || rows > max_rows || width < 1 || width > max_width)
     return fail(EKV_EINVAL, "ekv_controller_keep: rows %d (max %d), width %d (max %d)", rows, max_rows, width,
                 max_width);
+  if (objective == EKV_OBJ_MAXMIN && width > alloc::kMaxWidth && (int64_t)rows * width > INT_MAX)
+    return fail(EKV_EINVAL, "ekv_controller_keep: %d rows x %d blocks past the device-wide sort's 32-bit offsets",
+                rows, width);
   if (recent_blocks < 0 || cap_above_blocks < 0)
     return fail(EKV_EINVAL, "ekv_controller_keep: recent_blocks %d, cap_above_blocks %d", recent_blocks,
                 cap_above_blocks);

@@ -142,14 +142,16 @@ def test_sum_rows_wider_than_a_register_row():
         run(shares, lengths, evidence, fraction, 4, 256, audited=audited, released=released, weights=weights)
 
 
-def test_maxmin_rows_wider_than_a_sort_in_lds():
-    # the maxmin rule on rows past 12288 blocks (the device-wide segmented sort)
+@pytest.mark.parametrize("width", [30000, 70000])
+def test_maxmin_rows_wider_than_a_sort_in_lds(width):
+    # the maxmin rule on rows past 12288 blocks (the device-wide segmented sort), and past 65535
+    # (level positions in 32 bits)
     rng = np.random.default_rng(22)
-    rows, width = 4, 30000
+    rows = 4
     shares = rng.random((rows, width))
-    lengths = np.array([30000, 12289, 20000, 500])
+    lengths = np.array([width, 12289, 20000, 500])
     evidence = np.array([1, 1, 1, 1])
-    audited = np.array([29000, 12289, 15000, 500])
+    audited = np.array([width - 1000, 12289, 15000, 500])
     released = (rng.random((rows, width)) < 0.03).astype(np.uint8)
     for fraction in (0.3, 0.7):
         run(shares, lengths, evidence, fraction, 4, 256, audited=audited, released=released, objective="maxmin")
