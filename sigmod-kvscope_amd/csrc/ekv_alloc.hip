@@ -14,18 +14,22 @@
 // then to the earlier request.  The threshold is found by a radix select over order-preserving
 // 64-bit keys of the float64 gains (six passes of 11-bit digits over every open block, the gains
 // recomputed in each pass), then among the blocks at the threshold by a select over the 30-bit
-// (block desc, request asc) key (three passes).  All state lives in a caller-provided workspace that a
-// kernel clears first, so the launches need no host synchronisation and no memset.
+// (block desc, request asc) key (three passes).  A pass stops the select once the free blocks end at
+// a bucket's end, and each pass's last workgroup picks its digit.  All state lives in a
+// caller-provided workspace that the budget kernel clears first, so the launches need no host
+// synchronisation and no memset.
 //
 // maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
 // the lowest request first (observe/allocation.py:126-166).  Per request: the pinned shares' NumPy
 // sum (base), its open blocks in stable descending share order (a block radix sort in LDS over the
-// same order-preserving keys, one workgroup per request), and their running float64 totals, added
-// in that order as np.cumsum does by one lane per request.  The 60-step bisection of the level runs in one workgroup: a request's count at
-// a level is min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the
-// shifted-by-2r comparison NumPy's single search makes, and every request keeps the bracket of
-// positions its count can still take, so later steps search a few entries.  The leftover goes one
-// block at a time to the request of the lowest (retained, index), found by a workgroup argmin.
+// same order-preserving keys, one workgroup per request; past 12288 blocks a device-wide segmented
+// sort), and their running float64 totals, added in that order as np.cumsum does by one lane per
+// request.  The 60-step bisection of the level: a request's count at a level is
+// min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the shifted-by-2r comparison
+// NumPy's single search makes.  Its first 20 steps are walks over counts that two kernels sum over
+// every CU at the levels they can reach; the rest run in one workgroup, every request keeping the
+// bracket of positions its count can still take.  The leftover goes to the requests tied at the
+// lowest (retained share, index) level, a pass at a time, as the reference's heap hands it out.
 #pragma clang fp contract(off)
 
 #include <limits.h>
