@@ -5,9 +5,11 @@
 //
 // Design (gfx950, wave64):
 //  * Work list.  The live tiles of the selected rows, times the audited KV heads, form one
-//    flat list.  Every workgroup builds the per-row tile offsets in LDS from lens/select with a
-//    block scan, so the launch needs no host-side knowledge of the lengths, no scratch memory
-//    and no second kernel; it is identical on every step and can be captured in a graph.
+//    flat list.  A self-contained launch has every workgroup build the per-row tile offsets in
+//    LDS from lens/select with a block scan, so it needs no host-side knowledge of the lengths,
+//    no scratch memory and no second kernel; a planned launch reads the list from a step plan
+//    built once per decode step (below).  Both are identical on every step and can be captured
+//    in a graph.
 //  * Two kernels.  16-bit and fp8 keys (d = 64, 128, 256) in blocks of at least 16 tokens take
 //    tile_lse_cu_kernel: one 12-wave workgroup per compute unit, an equal slice of the list
 //    per CU, and the CU's waves share the slice through an LDS counter (a CU serves its loads
@@ -782,9 +784,9 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
 // The step plan.  Every audit launch of a decode step reads the same view buffers (block
 // table, lengths, selected rows, query tokens); only the layer, its queries and its keys
 // change.  So the work list the self-contained kernel rebuilds in every launch -- the tiles of
-// each selected row, their scan, each tile's row and block ids -- is built once per step, by two
-// small kernels, into a plan buffer that holds, for each workgroup of the audit grid, the count
-// of its tiles and their descriptors, contiguous.  A planned launch then starts with one load of
+// each selected row, their scan, each tile's row and block ids -- is built once per step (by one
+// kernel up to 4096 rows, two small kernels past that) into a plan buffer that holds, for each
+// workgroup of the audit grid, the count of its tiles and their descriptors, contiguous.  A planned launch then starts with one load of
 // the wave's first descriptor before its first key requests, and reads its later descriptors
 // one tile ahead, as the self-contained kernel reads them from LDS.
 //
