@@ -243,10 +243,11 @@ __device__ __forceinline__ void view_row(const Params &p, int row, int L, const 
   int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
+    // kept: at its rank among the kept; dropped: after the kept ones, in order (one store either way)
     const int b = b0 + i;
-    if (b >= W) continue;
-    if ((kept_bits >> i) & 1u) s_out[before++] = entry[i];
-    else s_out[total_kept + (b - before)] = entry[i];  // dropped: after the kept ones, in order
+    const bool kept = (kept_bits >> i) & 1u;
+    if (b < W) s_out[kept ? before : total_kept + (b - before)] = entry[i];
+    before += kept ? 1 : 0;
   }
   __syncthreads();
   int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
@@ -698,8 +699,7 @@ __device__ __forceinline__ int key_mode(uint32_t mag, int sgn) {
 // compact_block_table (runtime/block_view.py:36-56) on that keep, the row assembled in the same LDS.
 template <int PER>
 __device__ __forceinline__ void keep_and_view(const Params &p, int row, const RowInfo &me, int L,
-                                              const uint32_t (&key)[PER], const int32_t (&entry)[PER],
-                                              bool decide, long long quota, int mode, uint32_t *s_row,
+                                              const uint32_t (&key)[PER], bool decide, long long quota, int mode, uint32_t *s_row,
                                               int *s_hist, int *s_scan, int *s_sel) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -710,24 +710,35 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
   // the thread's run is contiguous, so they are one range of its bits
   const uint32_t open_bits = bit_range(max(1, b0) - b0, min(me.pin_at - b0, PER));
   uint32_t keep_bits = ~0u;  // rows without evidence read in full, controller.py:401
+  const bool any_open = open_bits != 0u;
+  const int open_count = (int)(me.exist - me.pinned);
+  const bool select = decide && quota > 0 && quota < open_count;
+  const int copy = lane & 3;
   if (decide) {
     // keys, larger first: an open block's is at least 1 (by value: the score's bits + 1 for a
     // positive score, else 1; inf last: 1 for +inf, else 2; tie: 1), a closed block's is 0 and is
     // never counted.  Slot i of thread t sits at i * kThreads + t: lane-consecutive, free of bank
     // conflicts.  A thread whose run holds no open block (past a short row) neither writes nor
-    // reads its slots.
-    const bool any_open = open_bits != 0u;
+    // reads its slots.  When the select runs, the keys' top digits are counted as they are
+    // written, so that its first pass reads nothing back.
     if (any_open) {
+      // the key of a raw score under the row's mode, the mode's test outside the loop
+      const uint32_t fin_k = mode == 2 ? 2u : 1u;
+      const bool by_value = mode == 1;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        uint32_t k;
-        if (mode == 1) k = (uint32_t)max((int)key[i], 0) + 1u;
-        else if (mode == 2) k = key[i] == 0x7f800000u ? 1u : 2u;
-        else k = 1u;
-        s_row[i * kThreads + tid] = ((open_bits >> i) & 1u) ? k : 0u;
+        const uint32_t k = by_value ? (uint32_t)max((int)key[i], 0) + 1u : (key[i] == 0x7f800000u ? 1u : fin_k);
+        const bool open = (open_bits >> i) & 1u;
+        s_row[i * kThreads + tid] = open ? k : 0u;
+        if (select && open) atomicAdd(&s_hist[(k >> 24) * 4 + copy], 1);
       }
     }
-    const int open_count = (int)(me.exist - me.pinned);
+  }
+  // the table run, requested once the raw scores are no longer needed (with both held the run
+  // would not fit the registers); it arrives while the select runs
+  int32_t entry[PER];
+  load_run<PER>(p, row, entry);
+  if (decide) {
     uint32_t open_keep = 0;
     if (quota >= open_count) {
       open_keep = ~0u;
@@ -738,24 +749,31 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
       uint32_t prefix = 0, mask = 0;
       int k_rem = (int)quota;
       bool whole = false;
-      const int copy = lane & 3;
 #pragma unroll 1
       for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
-        if (any_open) {
+        if (pass > 0 && any_open) {
+          // four keys read before their counts are added: an LDS atomic holds back every later
+          // LDS read, so reads issued one by one would each wait a full LDS latency
 #pragma unroll
-          for (int i = 0; i < PER; ++i) {
-            const uint32_t k = s_row[i * kThreads + tid];
-            if (k != 0u && (k & mask) == prefix) atomicAdd(&s_hist[((k >> shift) & 255) * 4 + copy], 1);
+          for (int g = 0; g < PER; g += 4) {
+            uint32_t kk[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kk[j] = s_row[(g + j) * kThreads + tid];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (kk[j] != 0u && (kk[j] & mask) == prefix) atomicAdd(&s_hist[((kk[j] >> shift) & 255) * 4 + copy], 1);
           }
         }
         __syncthreads();
         if (wave == 0) {
-          // lane l holds digits 255 - 4l .. 252 - 4l; a scan over the lanes counts the keys above
+          // lane l holds digits 255 - 4l .. 252 - 4l, the four bins' copies 64 contiguous bytes
+          // from one address; a scan over the lanes counts the keys above
+          int4 *h = reinterpret_cast<int4 *>(&s_hist[4 * (252 - 4 * lane)]);
           int c[4], s4 = 0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int4 h4 = *reinterpret_cast<const int4 *>(&s_hist[4 * (255 - 4 * lane - j)]);
+          for (int j = 0; j < 4; ++j) {  // digit 255 - 4l - j
+            const int4 h4 = h[3 - j];
             c[j] = h4.x + h4.y + h4.z + h4.w;
             s4 += c[j];
             asm volatile("" ::: "memory");  // one bin's copies in registers at a time
@@ -774,8 +792,7 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
             }
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j)  // cleared for the next pass
-            *reinterpret_cast<int4 *>(&s_hist[4 * (255 - 4 * lane - j)]) = make_int4(0, 0, 0, 0);
+          for (int j = 0; j < 4; ++j) h[j] = make_int4(0, 0, 0, 0);  // cleared for the next pass
         }
         __syncthreads();
         prefix |= (uint32_t)s_sel[0] << shift;
@@ -848,10 +865,11 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
   int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
+    // kept: at its rank among the kept; dropped: after the kept ones, in order (one store either way)
     const int b = b0 + i;
-    if (b >= W) continue;
-    if ((kept_bits >> i) & 1u) s_out[before++] = entry[i];
-    else s_out[total_kept + (b - before)] = entry[i];  // dropped: after the kept ones, in order
+    const bool kept = (kept_bits >> i) & 1u;
+    if (b < W) s_out[kept ? before : total_kept + (b - before)] = entry[i];
+    before += kept ? 1 : 0;
   }
   __syncthreads();
   int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
@@ -1043,11 +1061,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
     qs[3] = sgn;
   }
   quota_reduce<4, 2>(qs, s_red);
-  int32_t entry[PER];  // the table run
-  load_run<PER>(p, row, entry);  // after the barriers: with the scores in flight it would not fit
   const long long leftover = bg.free_blocks - qs[0];
   const long long quota = bg.keep_all ? q.open : q.floor + (qs[1] < leftover ? 1 : 0);
-  keep_and_view<PER>(p, row, me, L, key, entry, decide, quota, key_mode((uint32_t)qs[2], qs[3]), s_row, s_hist,
+  keep_and_view<PER>(p, row, me, L, key, decide, quota, key_mode((uint32_t)qs[2], qs[3]), s_row, s_hist,
                      s_scan, s_sel);
 }
 
