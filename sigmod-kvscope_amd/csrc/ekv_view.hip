@@ -174,10 +174,11 @@ __global__ __launch_bounds__(kThreads) void view_lds_kernel(const Params p) {
   if (p.view_table != nullptr) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
+      // kept: at its rank among the kept; dropped: after the kept ones, in order (one store either way)
       const int b = b0 + i;
-      if (b >= W) continue;
-      if ((kept_bits >> i) & 1u) s_out[before++] = entry[i];
-      else s_out[total_kept + (b - before)] = entry[i];  // dropped: after the kept ones, in order
+      const bool kept = (kept_bits >> i) & 1u;
+      if (b < W) s_out[kept ? before : total_kept + (b - before)] = entry[i];
+      before += kept ? 1 : 0;
     }
     __syncthreads();
     int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
