@@ -131,6 +131,61 @@ int ekv_audit_tile_lse_planned(const void *q, int q_dtype, int64_t q_stride_toke
                                int32_t plan_width, void *stream);
 
 /*
+ * 1 when ekv_audit_tile_lse_planned has a planned (MFMA) form for the shape -- 16-bit queries and
+ * keys (or fp8 keys with bf16 queries), head_dim 64, 128 or 256, tiles of 32 tokens or more -- and
+ * so ekv_audit_tile_lse_layers takes it; 0 otherwise.
+ */
+int ekv_audit_planned_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size);
+
+/* One layer of a multi-layer audit launch (ekv_audit_tile_lse_layers). */
+typedef struct ekv_audit_layer {
+  const void *q;       /* the layer's queries, with the call's shared strides */
+  const void *keys;    /* the layer's key cache view, with the call's shared strides */
+  int32_t layer;       /* the plane layer its records go to */
+  int32_t group_first; /* its first audited KV head (layer % kv_heads for one group) */
+  int32_t q_head0;     /* the query head that q's head 0 holds: 0, or group_first * group_rows
+                          for a staged copy of the group's heads (ekv_audit_stage_queries) */
+  float scale;         /* its logit scale */
+  float k_scale;       /* its key dequantisation scale (1 for 16-bit keys) */
+  int32_t pad;
+} ekv_audit_layer_t;
+
+/*
+ * The planned audit of several layers of one decode step in one launch per 32 layers: the records
+ * and cycles of ekv_audit_tile_lse_planned for each entry of `layers`, bit for bit, after every
+ * layer has run.  Replaces the per-layer launches of RecordingPlane.record
+ * (runtime/audit_kernel.py:196-265): a step's launches differ only in the layer (its queries, keys,
+ * records and scale), so one launch amortises the launch's fixed costs (first key requests, the
+ * spread of the workgroups' ends) over all of them.  The shared arguments are those of
+ * ekv_audit_tile_lse_planned.  With q_by_row != 0, row r's query is row r of each layer's q (a
+ * staged copy) instead of token qrow[r].  Only shapes with ekv_audit_planned_shape() != 0.
+ */
+int ekv_audit_tile_lse_layers(const ekv_audit_layer_t *layers, int32_t n_layers, int32_t q_by_row,
+                              int q_dtype, int64_t q_stride_token, int64_t q_stride_head, int kv_dtype,
+                              int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head,
+                              const int32_t *table, int64_t table_stride, const int32_t *lens,
+                              const int32_t *qrow, const uint8_t *select, const uint32_t *flag, float *lse,
+                              int64_t lse_plane_stride, int64_t lse_layer_stride, int64_t lse_row_stride,
+                              int32_t cells, uint64_t *cycles, int32_t cycles_rows, int32_t groups,
+                              int32_t group_rows, int32_t rows, int32_t width, int32_t block_size,
+                              int32_t tile_blocks, int32_t head_dim, const void *plan, size_t plan_bytes,
+                              int32_t plan_rows, int32_t plan_width, void *stream);
+
+/*
+ * A layer's queries staged for ekv_audit_tile_lse_layers, so that a launch after the last layer
+ * reads them after the engine has reused the query memory (the query tensor of runtime/audit_kernel.py
+ * :196-203 lives only for its layer's forward):
+ *     staged[r * staged_row_stride + h * head_dim + e] = q[qrow[r] * q_stride_token
+ *                                                         + (head_first + h) * q_stride_head + e]
+ * for h < heads, e < head_dim and every row r < rows with select[r] != 0, when *flag != 0 (nothing
+ * otherwise, like the audit).  16-bit or fp32 queries; 16-byte-aligned rows.
+ */
+int ekv_audit_stage_queries(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                            int32_t head_first, int32_t heads, int32_t head_dim, const int32_t *qrow,
+                            const uint8_t *select, const uint32_t *flag, int32_t rows, void *staged,
+                            int64_t staged_row_stride, void *stream);
+
+/*
  * Exact per-block attention shares of the chosen rows, from the statistic planes.
  * Replaces read_tile_rows + normalize_tile_lse (observe/tile_shares.py:129-173 and :58-103),
  * computing on the device what the reference copies to the host and normalises with NumPy.
@@ -182,7 +237,8 @@ int ekv_tile_shares_ws(const float *lse, int64_t lse_plane_stride, int64_t lse_l
  * with EKV_EINVAL (e.g. 128 rows x 512 blocks x 32 layers need 8.7 MB and fit).  The scratch
  * starts zeroed, as a workspace must.  Every call on one
  * device uses that device's one scratch: calls that overlap on one device (two streams, two
- * threads, two graphs replayed at once) race and must be ordered by the caller.
+ * threads, two graphs replayed at once) race, so a process calls it from one stream at a time
+ * (or orders its streams).
  */
 #define EKV_TILE_SHARES_SCRATCH_BYTES (16u << 20)
 int ekv_tile_shares_noalloc(const float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride,
@@ -190,6 +246,25 @@ int ekv_tile_shares_noalloc(const float *lse, int64_t lse_plane_stride, int64_t 
                             const int32_t *row_ids, const int32_t *row_blocks, int32_t nrows,
                             int32_t tile_blocks, int32_t aggregate, float *shares, int64_t shares_stride,
                             void *stream);
+
+/*
+ * The workspace's status, after a failure of the split form's wait.  The single-kernel form waits,
+ * a bounded number of reloads, for the partials of a row's other workgroups; a partial that has not
+ * landed by then is taken as lost, the row comes out as NaN, and the workspace's sticky status word
+ * is set, because the lost value may still land in its slot after the call.  While it is set every
+ * call on that workspace leaves the slots alone and returns NaN rows.  No counterpart in the
+ * reference (its normalisation runs on the host).
+ * ekv_tile_shares_status: waits for the device, then reads the status word of `workspace` (NULL:
+ * this device's scratch of ekv_tile_shares_noalloc) into *status (0: sound).
+ * ekv_tile_shares_reset: zeroes `workspace_bytes` of `workspace` (NULL: the scratch) on `stream`
+ * with a kernel, status included, after the calls before it on that stream.
+ * ekv_tile_shares_test_wait: for tests of this failure path only -- sets, for every later call in
+ * the process, the reloads of the wait (0: the default) and, with lose != 0, makes every wait run
+ * to its limit without taking a value, so that the path runs with every kernel ending normally.
+ */
+int ekv_tile_shares_status(const void *workspace, int32_t *status);
+int ekv_tile_shares_reset(void *workspace, size_t workspace_bytes, void *stream);
+int ekv_tile_shares_test_wait(int32_t spin_limit, int32_t lose);
 
 /*
  * The same normalisation from u values already formed, u[layer][row][block][cell]

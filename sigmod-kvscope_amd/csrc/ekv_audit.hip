@@ -991,66 +991,141 @@ __device__ __forceinline__ void load_desc(const TileDesc *d, u32x4 &lo, u32x4 &h
   hi = *reinterpret_cast<const u32x4 *>(src + 16);
 }
 
-// The planned form of tile_lse_cu_kernel: the same chunks, dots, records and timer; the tiles
-// of workgroup b are its plan's descriptors, wave w starting at item w and the waves then taking
-// items from an LDS counter, one ahead.  An item is (tile, audited head), tile-major.
+// The layers of one planned launch.  A decode step's audit launches differ only in the layer:
+// its queries, its key cache, its records and its scale.  One launch can take up to
+// kMaxLaunchLayers of them, so the launch's fixed costs (the first key requests, the spread of the
+// workgroups' ends) are paid once for all of them.
+constexpr int kMaxLaunchLayers = 32;
+
+struct LayerArgs {
+  const char *q;         // the layer's queries
+  const char *keys;      // the layer's key cache
+  float *lse;            // the statistic planes, offset to the layer
+  float scale2;          // scale * k_scale * log2(e): scores in log2 units
+  int32_t group_first;   // the first audited KV head
+  int32_t q_head0;       // the query head that q's head 0 holds (a staged copy starts at the group)
+  int32_t pad;
+};
+static_assert(sizeof(LayerArgs) == 40, "packed layer arguments");
+
+struct LayerSet {
+  LayerArgs l[kMaxLaunchLayers];
+  int32_t n;         // layers in the launch
+  int32_t q_by_row;  // queries indexed by row (a staged copy), not by the row's query token
+};
+
+// The planned form of tile_lse_cu_kernel over one or more layers: the same chunks, dots, records
+// and timer.  For layer j of the launch, workgroup b takes the plan's split (b + j) mod grid, so
+// that over the layers every workgroup's share of tiles differs from another's by at most one
+// tile (the split gives the first T mod grid splits one tile more), and its splits are adjacent
+// in the list (their rows follow one another).  Items run layer by layer; an item is
+// (tile, audited head), tile-major.  Wave w starts at item w and the waves then take items from an
+// LDS counter, one ahead.
 template <int MODE, int HEAD_DIM, int MT>
-__global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Params p, const PlanView plan) {
+__global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Params p, const PlanView plan,
+                                                                    const LayerSet ls) {
   using S = MfmaShape<MODE, HEAD_DIM>;
   using C = CuShape<MODE, HEAD_DIM, MT>;
   constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
   constexpr int NW = C::kWaves;
 
   __shared__ int s_next;
+  __shared__ int s_pref[kMaxLaunchLayers + 1];  // items before each layer of the launch
   __shared__ u32x4 s_tr[NW][C::kStash];
   __shared__ unsigned long long s_cycles[kCycleSlots];
 
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int groups = p.groups;
-  const TileDesc *dl = plan.desc + (int64_t)blockIdx.x * plan.cap;
-  // the flag, the workgroup's count and first row, and the wave's first descriptor: one latency
-  // (a relaxed load: a volatile one is completed before the next load is issued)
+  const int grid = gridDim.x;
+  const int nl = ls.n;
+  auto split_of = [&](int j) { return (int)((blockIdx.x + (unsigned)j) % (unsigned)grid); };
+  // the flag, the first split's count and first row, the layers' counts and the wave's first
+  // descriptor: one latency (a relaxed load: a volatile one is completed before the next is issued)
   uint32_t flag = __hip_atomic_load(p.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int2 wg = plan.wg[blockIdx.x];
-  // wave w starts at item w; the rest come from the LDS counter
+  int cnt = 0;  // wave 0: lane j holds layer j's split count
+  if (wave == 0 && lane < nl) cnt = plan.wg[split_of(lane)].x;
   u32x4 d_lo, d_hi;
-  load_desc(dl + min(groups == 1 ? wave : wave / groups, plan.cap - 1), d_lo, d_hi);
-  // all four are waited for here, together: otherwise the compiler tests the flag before it
-  // issues the other loads, a second memory latency before the first key request
-  asm volatile("" : "+v"(flag), "+v"(wg.x), "+v"(wg.y) : "v"(d_lo), "v"(d_hi));
-  // the parameters of the first key and query requests, read with the others (a scalar-cache miss
+  load_desc(plan.desc + (int64_t)blockIdx.x * plan.cap + min(groups == 1 ? wave : wave / groups, plan.cap - 1), d_lo,
+            d_hi);
+  // all are waited for here, together: otherwise the compiler tests the flag before it issues the
+  // other loads, a second memory latency before the first key request
+  asm volatile("" : "+v"(flag), "+v"(wg.x), "+v"(wg.y), "+v"(cnt) : "v"(d_lo), "v"(d_hi));
+  // the first layer's parameters and the shared strides, read with the others (a scalar-cache miss
   // after the barrier would be one more latency)
-  const char *keys_base = p.keys, *q_base = p.q;
+  const char *keys0 = ls.l[0].keys, *q0 = ls.l[0].q;
   int64_t k_block = p.k_stride_block, k_pos = p.k_stride_pos, k_head = p.k_stride_head;
   int64_t q_tok = p.q_stride_token, q_head = p.q_stride_head;
-  asm volatile("" : "+s"(keys_base), "+s"(q_base), "+s"(k_block), "+s"(k_pos), "+s"(k_head), "+s"(q_tok),
-               "+s"(q_head));
+  asm volatile("" : "+s"(keys0), "+s"(q0), "+s"(k_block), "+s"(k_pos), "+s"(k_head), "+s"(q_tok), "+s"(q_head));
   if (flag == 0u) return;  // runtime/audit_kernel.py:64
-  if (threadIdx.x == 0) s_next = NW;
+  if (wave == 0) {
+    // items before each layer: an inclusive scan of the clipped counts over wave 0's lanes
+    const int items_j = min(cnt, plan.cap) * groups;
+    const int inc = wave_inclusive_scan(items_j);
+    if (lane < nl) s_pref[lane + 1] = inc;
+    if (lane == 0) {
+      s_pref[0] = 0;
+      s_next = NW;
+    }
+  }
   if (p.cycles != nullptr)
     for (int k = threadIdx.x; k < kCycleSlots; k += kCuThreads) s_cycles[k] = 0ull;
-  const int items = __builtin_amdgcn_readfirstlane(min(wg.x, plan.cap)) * groups;
-  const int row0 = __builtin_amdgcn_readfirstlane(wg.y);
-  __syncthreads();  // s_next and the timer slots are set before any take
+  const int row0 = __builtin_amdgcn_readfirstlane(wg.y);  // the first split's first row: the timer slots' base
+  __syncthreads();  // s_next, the layer offsets and the timer slots are set before any take
+  const int items = __builtin_amdgcn_readfirstlane(s_pref[nl]);
 
   const int n = lane & 15;  // A: token of the M-tile; B / C: query row
   const int c = lane >> 4;  // dim piece within a k-step; C: token quad
   const int nsub = p.nsub;  // chunks per tile
   const int bs = p.block_size;
   const int G = p.group_rows;
+  const bool by_row = ls.q_by_row != 0;
   u32x4 *tr = s_tr[wave];
   const int row_in = lane / S::kPieces;  // load instruction: the lane's row and piece
   const int piece = lane % S::kPieces;
   uint32_t voff[NLD];
 #pragma unroll
   for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * k_pos + piece * 16);
-  const float scale2 = p.scale * kLog2e;
+
+  // A wave's position in the launch's items: the layer of its latest taken item and that layer's
+  // item range.  Items a wave takes only grow, so the walk moves forward.
+  struct Walk {
+    int j, lo, hi;
+  };
+  auto walk_to = [&](Walk &w, int item) {
+    while (item >= w.hi) {
+      ++w.j;
+      w.lo = w.hi;
+      w.hi = __builtin_amdgcn_readfirstlane(s_pref[w.j + 1]);
+    }
+  };
+  auto desc_of = [&](const Walk &w, int item) {
+    return plan.desc + (int64_t)split_of(w.j) * plan.cap + (item - w.lo) / groups;
+  };
+
+  struct Layer {
+    const char *q, *keys;
+    float *lse;
+    float scale2;
+    int group_first, q_head0;
+  };
+  auto layer_of = [&](int j) -> Layer {
+    j = __builtin_amdgcn_readfirstlane(j);  // a uniform index: scalar loads of the kernel arguments
+    Layer L;
+    L.q = ls.l[j].q;
+    L.keys = ls.l[j].keys;
+    L.lse = ls.l[j].lse;
+    L.scale2 = ls.l[j].scale2;
+    L.group_first = ls.l[j].group_first;
+    L.q_head0 = ls.l[j].q_head0;
+    return L;
+  };
 
   struct Tile {
-    int row, h, k, valid, id0, id1, qtok;
+    int row, h, k, valid, id0, id1, qtok, j;
   };
-  auto describe = [&](const u32x4 &lo, const u32x4 &hi, int item) -> Tile {
+  auto describe = [&](const u32x4 &lo, const u32x4 &hi, const Walk &w, int item) -> Tile {
     Tile t;
     t.row = __builtin_amdgcn_readfirstlane((int)lo[0]);
     t.k = __builtin_amdgcn_readfirstlane((int)lo[1]);
@@ -1058,7 +1133,8 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
     t.qtok = __builtin_amdgcn_readfirstlane((int)lo[3]);
     t.id0 = __builtin_amdgcn_readfirstlane((int)hi[0]);
     t.id1 = __builtin_amdgcn_readfirstlane((int)hi[1]);
-    t.h = groups == 1 ? 0 : item % groups;
+    t.h = groups == 1 ? 0 : (item - w.lo) % groups;
+    t.j = w.j;
     return t;
   };
   auto take = [&]() -> int {
@@ -1066,13 +1142,13 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
     if (lane == 0) v = atomicAdd(&s_next, 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  auto load_chunk = [&](u32x4 (&D)[MT * NLD], const Tile &T, int sub) {
-    const int64_t head_off = (int64_t)(p.group_first + T.h) * k_head;
+  auto load_chunk = [&](u32x4 (&D)[MT * NLD], const Tile &T, const Layer &L, int sub) {
+    const int64_t head_off = (int64_t)(L.group_first + T.h) * k_head;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int tpos = sub * CH + 16 * mt;
       const int id = tpos < bs ? T.id0 : T.id1;
-      const char *src = keys_base + (int64_t)id * k_block + head_off + (int64_t)(tpos % bs) * k_pos;
+      const char *src = L.keys + (int64_t)id * k_block + head_off + (int64_t)(tpos % bs) * k_pos;
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         uint32_t o = voff[j];
@@ -1081,8 +1157,10 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
       }
     }
   };
-  auto load_query = [&](u32x4 (&Q)[KS], const Tile &T) {
-    const char *qrow = q_base + (int64_t)T.qtok * q_tok + (int64_t)((p.group_first + T.h) * G + n) * q_head;
+  auto load_query = [&](u32x4 (&Q)[KS], const Tile &T, const Layer &L) {
+    const int qi = by_row ? T.row : T.qtok;
+    const char *qrow =
+        L.q + (int64_t)qi * q_tok + (int64_t)((L.group_first + T.h) * G + n - L.q_head0) * q_head;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
@@ -1118,7 +1196,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
   };
 
   const bool timed = p.cycles != nullptr;
-  // the timer: a run of one row's and head's tiles is timed once, where it ends
+  // the timer: a run of one layer's, row's and head's tiles is timed once, where it ends
   auto time_tile = [&](const Tile &T, uint64_t &mark) {
     const uint64_t now = __builtin_amdgcn_s_memtime();
     if (T.h == 0 && T.row < p.cycles_rows && lane == 0) {
@@ -1130,21 +1208,22 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
   };
   // the chunk's tile max and sum, folded into the tile's running (m, l); at the tile's last chunk
   // its record goes into each of its blocks the row reaches (runtime/audit_kernel.py:97-109)
-  auto reduce_chunk = [&](const f32x4_t (&acc)[MT], const Tile &T, int sub, float &m_run, float &l_run) {
+  auto reduce_chunk = [&](const f32x4_t (&acc)[MT], const Tile &T, const Layer &L, int sub, float &m_run,
+                          float &l_run) {
     const int tok0 = sub * CH;  // within the tile
     float sc[4 * MT];
     if (tok0 + CH <= T.valid) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sc[4 * mt + e] = acc[mt][e] * scale2;
+        for (int e = 0; e < 4; ++e) sc[4 * mt + e] = acc[mt][e] * L.scale2;
     } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int tok = tok0 + 16 * mt + 4 * c + e;
-          sc[4 * mt + e] = tok < T.valid ? acc[mt][e] * scale2 : -INFINITY;
+          sc[4 * mt + e] = tok < T.valid ? acc[mt][e] * L.scale2 : -INFINITY;
         }
     }
     float mx = sc[0];
@@ -1167,7 +1246,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
     if (sub == nsub - 1) {
       const int blk = kTileBlocks * T.k + c;
       if (c < kTileBlocks && n < G && c * bs < T.valid) {
-        float *cell = p.lse + (int64_t)T.row * p.row_stride + T.h * G + (int64_t)blk * p.cells + n;
+        float *cell = L.lse + (int64_t)T.row * p.row_stride + T.h * G + (int64_t)blk * p.cells + n;
         cell[0] = m_run * kLn2;
         cell[p.plane_stride] = l_run;
       }
@@ -1177,45 +1256,61 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
   };
 
   if (wave < items) {
-    Tile T = describe(d_lo, d_hi, wave);
+    Walk w{0, 0, __builtin_amdgcn_readfirstlane(s_pref[1])};
+    if (wave >= w.hi) {  // a first layer with fewer items than waves: the wave's first item is later
+      walk_to(w, wave);
+      load_desc(desc_of(w, wave), d_lo, d_hi);
+    }
+    Tile T = describe(d_lo, d_hi, w, wave);
+    Layer cur = T.j == 0 ? Layer{q0, keys0, ls.l[0].lse, ls.l[0].scale2, ls.l[0].group_first, ls.l[0].q_head0}
+                         : layer_of(T.j);
     int ahead = take();  // the wave's next item, its descriptor read a tile early
-    if (ahead < items) load_desc(dl + ahead / groups, d_lo, d_hi);
+    if (ahead < items) {
+      walk_to(w, ahead);
+      load_desc(desc_of(w, ahead), d_lo, d_hi);
+    }
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4_t acc[MT];
     // one chunk in flight per wave: it goes to LDS when it arrives and the next is requested at once
     u32x4 A[MT * NLD], qb[KS], qn[KS];
-    load_query(qb, T);
-    load_chunk(A, T, 0);
+    load_query(qb, T, cur);
+    load_chunk(A, T, cur, 0);
     int sub = 0;
     uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
     while (true) {
       Tile N = T;
+      Layer next = cur;
       int nsub_next = sub + 1;
       bool more = true, new_query = false;
       if (nsub_next == nsub) {
         more = ahead < items;
         if (more) {
-          N = describe(d_lo, d_hi, ahead);
+          N = describe(d_lo, d_hi, w, ahead);
+          if (N.j != T.j) next = layer_of(N.j);
           nsub_next = 0;
           ahead = take();
-          if (ahead < items) load_desc(dl + ahead / groups, d_lo, d_hi);
-          new_query = N.row != T.row || N.h != T.h;
+          if (ahead < items) {
+            walk_to(w, ahead);
+            load_desc(desc_of(w, ahead), d_lo, d_hi);
+          }
+          new_query = N.row != T.row || N.h != T.h || N.j != T.j;
         }
       }
       stash_chunk(A);  // waits for the chunk
       if (more) {
-        load_chunk(A, N, nsub_next);
-        if (new_query) load_query(qn, N);
+        load_chunk(A, N, next, nsub_next);
+        if (new_query) load_query(qn, N, next);
       }
       mma_stashed(qb, acc);
-      reduce_chunk(acc, T, sub, m_run, l_run);
-      if (timed && sub == nsub - 1 && (!more || N.row != T.row || N.h != T.h)) time_tile(T, mark);
+      reduce_chunk(acc, T, cur, sub, m_run, l_run);
+      if (timed && sub == nsub - 1 && (!more || new_query)) time_tile(T, mark);
       if (!more) break;
       if (new_query) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) qb[s] = qn[s];
       }
       T = N;
+      cur = next;
       sub = nsub_next;
     }
   }
@@ -1225,6 +1320,33 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_planned_kernel(const Para
       const unsigned long long cyc = s_cycles[threadIdx.x];
       if (cyc != 0ull) atomicAdd((unsigned long long *)(p.cycles + row0 + threadIdx.x), cyc);
     }
+  }
+}
+
+// The step's queries staged per layer, for a launch that audits several layers after they have
+// run: staged[r][h][:] = q[qrow[r]][head_first + h][:] for the selected rows (nothing with the flag
+// off).  A workgroup copies 16 rows in 16-byte pieces.
+constexpr int kStageThreads = 256;
+constexpr int kStageRows = 16;
+
+__global__ __launch_bounds__(kStageThreads) void stage_queries_kernel(
+    const char *q, int64_t q_stride_token, int64_t q_stride_head, int32_t head_first, int32_t heads,
+    int32_t row_bytes, const int32_t *qrow, const uint8_t *select, const uint32_t *flag, int32_t rows, char *staged,
+    int64_t staged_row_stride) {
+  if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) return;
+  const int pieces_head = row_bytes / 16;
+  const int pieces_row = heads * pieces_head;
+  const int r_first = blockIdx.x * kStageRows;
+  const int r_end = min(r_first + kStageRows, rows);
+  for (int i = threadIdx.x; i < (r_end - r_first) * pieces_row; i += kStageThreads) {
+    const int r = r_first + i / pieces_row;
+    if (select[r] == 0) continue;
+    const int rem = i % pieces_row;
+    const int h = rem / pieces_head;
+    const int pc = rem % pieces_head;
+    const u32x4 v = *(const u32x4 *)(q + (int64_t)qrow[r] * q_stride_token + (int64_t)(head_first + h) * q_stride_head +
+                                     16 * pc);
+    *(u32x4 *)(staged + (int64_t)r * staged_row_stride + (int64_t)h * row_bytes + 16 * pc) = v;
   }
 }
 
@@ -1348,15 +1470,15 @@ using namespace ekv::audit;
 namespace ekv {
 namespace audit {
 
-using PlannedFn = void (*)(const Params, const PlanView);
+using PlannedFn = void (*)(const Params, const PlanView, const LayerSet);
 
 template <int MODE, int HD>
 PlannedFn pick_planned_mt(bool wide) {
   constexpr int kRowBytes = MfmaShape<MODE, HD>::kRowBytes;
   if constexpr (kRowBytes <= 128) {
-    if (wide) return tile_lse_planned_kernel<MODE, HD, chunk_mtiles(kRowBytes, true)>;
+    if (wide) return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, true)>;
   }
-  return tile_lse_planned_kernel<MODE, HD, chunk_mtiles(kRowBytes, false)>;
+  return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, false)>;
 }
 
 template <int MODE>
@@ -1542,6 +1664,19 @@ int check_plan(const void *plan, size_t plan_bytes, int32_t plan_rows, int32_t p
   return EKV_OK;
 }
 
+// One planned launch of the layers `ls` on the plan's grid.
+int launch_planned(PlannedFn fn, const Params &p, const LayerSet &ls, const void *plan, int32_t plan_rows,
+                   int32_t plan_width, void *stream, const char *what) {
+  const int grid = plan_grid();
+  const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
+  PlanView v;
+  v.wg = (const int2 *)((const char *)plan + Lp.wg);
+  v.desc = (const TileDesc *)((const char *)plan + Lp.desc);
+  v.cap = Lp.cap;
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v, ls);
+  return check_hip(hipGetLastError(), what);
+}
+
 }  // namespace audit
 }  // namespace ekv
 
@@ -1639,12 +1774,100 @@ extern "C" int ekv_audit_tile_lse_planned(
     hipLaunchKernelGGL(L.fn, dim3((unsigned)L.blocks), dim3(L.threads), L.lds, (hipStream_t)stream, p);
     return check_hip(hipGetLastError(), "ekv_audit_tile_lse_planned launch");
   }
-  const int grid = plan_grid();
-  const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
-  PlanView v;
-  v.wg = (const int2 *)((const char *)plan + Lp.wg);
-  v.desc = (const TileDesc *)((const char *)plan + Lp.desc);
-  v.cap = Lp.cap;
-  hipLaunchKernelGGL(L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v);
-  return check_hip(hipGetLastError(), "ekv_audit_tile_lse_planned launch");
+  LayerSet ls{};
+  ls.n = 1;
+  ls.q_by_row = 0;
+  ls.l[0] = LayerArgs{p.q, p.keys, p.lse, p.scale * kLog2e, p.group_first, 0, 0};
+  return launch_planned(L.planned, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_planned launch");
+}
+
+extern "C" int ekv_audit_planned_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size) {
+  if (block_size <= 0) return 0;
+  int mode;
+  if (kv_dtype == EKV_F16 && q_dtype == EKV_F16) mode = kModeF16;
+  else if (kv_dtype == EKV_BF16 && q_dtype == EKV_BF16) mode = kModeBF16;
+  else if (kv_dtype == EKV_FP8_E4M3 && q_dtype == EKV_BF16) mode = kModeFp8Bf16;
+  else return 0;
+  (void)mode;
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (kTileBlocks * block_size) % 32 == 0 &&
+         ((kTileBlocks * block_size) & (kTileBlocks * block_size - 1)) == 0;
+}
+
+extern "C" int ekv_audit_tile_lse_layers(
+    const ekv_audit_layer_t *layers, int32_t n_layers, int32_t q_by_row, int q_dtype, int64_t q_stride_token,
+    int64_t q_stride_head, int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos, int64_t k_stride_head,
+    const int32_t *table, int64_t table_stride, const int32_t *lens, const int32_t *qrow, const uint8_t *select,
+    const uint32_t *flag, float *lse, int64_t lse_plane_stride, int64_t lse_layer_stride, int64_t lse_row_stride,
+    int32_t cells, uint64_t *cycles, int32_t cycles_rows, int32_t groups, int32_t group_rows, int32_t rows,
+    int32_t width, int32_t block_size, int32_t tile_blocks, int32_t head_dim, const void *plan, size_t plan_bytes,
+    int32_t plan_rows, int32_t plan_width, void *stream) {
+  if (layers == nullptr || n_layers < 0) return fail(EKV_EINVAL, "ekv_audit_tile_lse_layers: no layer list");
+  if (n_layers == 0) return EKV_OK;
+  if (!ekv_audit_planned_shape(q_dtype, kv_dtype, head_dim, block_size))
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse_layers: dtype %d / %d, head_dim %d, block %d has no planned form",
+                q_dtype, kv_dtype, head_dim, block_size);
+  // the shared arguments, checked with the first layer's pointers; every layer's own below
+  Params p;
+  Launch L;
+  int rc = audit_setup(layers[0].q, q_dtype, q_stride_token, q_stride_head, layers[0].keys, kv_dtype, k_stride_block,
+                       k_stride_pos, k_stride_head, layers[0].k_scale, table, table_stride, lens, qrow, select, flag,
+                       lse, lse_plane_stride, lse_layer_stride, lse_row_stride, cells, cycles, cycles_rows,
+                       layers[0].scale, layers[0].layer, layers[0].group_first, groups, group_rows, rows, width,
+                       block_size, tile_blocks, head_dim, 0, true, p, L);
+  if (rc != EKV_OK) return rc;
+  rc = check_plan(plan, plan_bytes, plan_rows, plan_width, rows, width, "ekv_audit_tile_lse_layers");
+  if (rc != EKV_OK || rows == 0) return rc;
+  const int qbytes = dtype_bytes(q_dtype);
+  for (int i = 0; i < n_layers; ++i) {
+    const ekv_audit_layer_t &e = layers[i];
+    if (e.q == nullptr || e.keys == nullptr || e.layer < 0)
+      return fail(EKV_EINVAL, "ekv_audit_tile_lse_layers: layer entry %d has a null pointer or a negative layer", i);
+    if ((((uintptr_t)e.q | (uintptr_t)e.keys) & 15) != 0)
+      return fail(EKV_EINVAL, "ekv_audit_tile_lse_layers: layer entry %d's query or key rows are not 16-byte aligned", i);
+    if (e.group_first < 0 || e.q_head0 < 0 || e.q_head0 > e.group_first * group_rows)
+      return fail(EKV_EINVAL, "ekv_audit_tile_lse_layers: layer entry %d: group %d with staged head %d", i,
+                  e.group_first, e.q_head0);
+  }
+  (void)qbytes;
+  for (int first = 0; first < n_layers; first += kMaxLaunchLayers) {
+    LayerSet ls{};
+    ls.n = std::min(kMaxLaunchLayers, n_layers - first);
+    ls.q_by_row = q_by_row != 0;
+    for (int i = 0; i < ls.n; ++i) {
+      const ekv_audit_layer_t &e = layers[first + i];
+      ls.l[i] = LayerArgs{(const char *)e.q, (const char *)e.keys, lse + (int64_t)e.layer * lse_layer_stride,
+                          e.scale * e.k_scale * kLog2e, e.group_first, e.q_head0, 0};
+    }
+    rc = launch_planned(L.planned, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_layers launch");
+    if (rc != EKV_OK) return rc;
+  }
+  return EKV_OK;
+}
+
+extern "C" int ekv_audit_stage_queries(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                                       int32_t head_first, int32_t heads, int32_t head_dim, const int32_t *qrow,
+                                       const uint8_t *select, const uint32_t *flag, int32_t rows, void *staged,
+                                       int64_t staged_row_stride, void *stream) {
+  if (q == nullptr || qrow == nullptr || select == nullptr || flag == nullptr || staged == nullptr)
+    return fail(EKV_EINVAL, "ekv_audit_stage_queries: null pointer argument");
+  const int qbytes = dtype_bytes(q_dtype);
+  if (qbytes == 0 || q_dtype == EKV_FP8_E4M3)
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_stage_queries: query dtype %d", q_dtype);
+  if (rows < 0 || heads <= 0 || head_first < 0 || head_dim <= 0)
+    return fail(EKV_EINVAL, "ekv_audit_stage_queries: rows %d, heads %d from %d, head_dim %d", rows, heads, head_first,
+                head_dim);
+  const int64_t row_bytes = (int64_t)head_dim * qbytes;
+  if (staged_row_stride < (int64_t)heads * head_dim)
+    return fail(EKV_EINVAL, "ekv_audit_stage_queries: a staged row of %lld elements holds fewer than %d heads",
+                (long long)staged_row_stride, heads);
+  const uint64_t align = (uint64_t)q | (uint64_t)staged | (uint64_t)(q_stride_token * qbytes) |
+                         (uint64_t)(q_stride_head * qbytes) | (uint64_t)(staged_row_stride * qbytes) |
+                         (uint64_t)row_bytes;
+  if ((align & 15) != 0) return fail(EKV_EINVAL, "ekv_audit_stage_queries: rows must be 16-byte aligned");
+  if (rows == 0) return EKV_OK;
+  const int blocks = (rows + kStageRows - 1) / kStageRows;
+  hipLaunchKernelGGL(stage_queries_kernel, dim3(blocks), dim3(kStageThreads), 0, (hipStream_t)stream, (const char *)q,
+                     q_stride_token * qbytes, q_stride_head * qbytes, head_first, heads, (int32_t)row_bytes, qrow,
+                     select, flag, rows, (char *)staged, staged_row_stride * qbytes);
+  return check_hip(hipGetLastError(), "ekv_audit_stage_queries launch");
 }

@@ -56,6 +56,7 @@ constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
 constexpr int kWaveLayers = 8;   // the wave form: one layer per wave, 8 waves per workgroup
 constexpr int kMaxArrivalRows = 65536;  // rows whose arrival counters the workspace holds
+constexpr size_t kHeaderBytes = 256;    // the workspace's status word, then padding
 constexpr size_t kArrivalBytes = (size_t)kMaxArrivalRows * sizeof(int32_t);
 
 struct Params {
@@ -72,6 +73,9 @@ struct Params {
   float *part;         // split form: [rows][groups][width] partial sums (or maxes)
   int32_t *part_count; // split form: [rows][groups] contributing (layer, query row) pairs
   int32_t *arrivals;   // wave form: [rows] workgroups of the row done so far (0 between calls)
+  int32_t *status;     // wave form: the workspace's sticky status word (non-zero after a lost slot)
+  int32_t spin_limit;  // wave form: reloads of a slot before its value is taken as lost
+  int32_t lose;        // wave form, for tests of the failure path: no slot is ever seen as landed
 };
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -578,12 +582,13 @@ __device__ __forceinline__ void store_slot(uint32_t *at, uint32_t v) {
   __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// the slot's value once it has landed (0 when it was first read), or 0 after kSpinLimit reloads
-__device__ __forceinline__ uint32_t landed(const uint32_t *at, uint32_t first) {
-  uint32_t v = first;
-  for (int k = 0; v == 0u && k < kSpinLimit; ++k) {
+// the slot's value once it has landed (0 when it was first read), or 0 after `limit` reloads (with
+// `lose`, a test of the failure path, no value is taken: every wait runs to its limit)
+__device__ __forceinline__ uint32_t landed(const uint32_t *at, uint32_t first, int limit, bool lose) {
+  uint32_t v = lose ? 0u : first;
+  for (int k = 0; v == 0u && k < limit; ++k) {
     __builtin_amdgcn_s_sleep(1);
-    v = load_slot(at);
+    v = lose ? 0u : load_slot(at);
   }
   return v;
 }
@@ -604,6 +609,7 @@ void shares_wave_kernel(const Params p) {
   __shared__ int s_count[NW];
   __shared__ float s_red[NW];
   __shared__ int s_last;
+  __shared__ int s_status;
   const int out_row = blockIdx.x / p.groups;
   const int group = blockIdx.x - out_row * p.groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = lane_id();
@@ -702,6 +708,8 @@ void shares_wave_kernel(const Params p) {
     }
   }
   if (lane == 0) s_count[wave] = contributors;
+  if (threadIdx.x == 0)
+    s_status = p.groups > 1 ? __hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
   __syncthreads();
 
   // the group's partial of block b = threadIdx.x, over its layers in order
@@ -714,6 +722,12 @@ void shares_wave_kernel(const Params p) {
 #pragma unroll
   for (int w = 0; w < NW; ++w) count += s_count[w];
 
+  if (p.groups > 1 && s_status != 0) {
+    // A slot of an earlier call was lost and may still be written: until the workspace is reset,
+    // no slot is used and the row comes out without evidence (NaN).
+    if (group == 0 && b < p.width) p.shares[(int64_t)out_row * p.shares_stride + b] = NAN;
+    return;
+  }
   if (p.groups > 1) {
     // The partials and counts cross workgroups (and XCDs) through device-coherent stores and
     // loads, which pass the per-XCD L2 caches; a fence would instead write back and invalidate
@@ -760,13 +774,13 @@ void shares_wave_kernel(const Params p) {
           xv = v;
         } else if (g < p.groups) {
           if (b < n) {
-            x[k] = landed(&part[(int64_t)g * p.width + b], x[k]);
+            x[k] = landed(&part[(int64_t)g * p.width + b], x[k], p.spin_limit, p.lose != 0);
             lost |= x[k] == 0u;
             xv = __builtin_bit_cast(float, x[k] - 1u);
             store_slot(&part[(int64_t)g * p.width + b], 0u);
           }
           if (counter) {
-            c[k] = landed(&counts[g], c[k]);
+            c[k] = landed(&counts[g], c[k], p.spin_limit, p.lose != 0);
             lost_count |= c[k] == 0u;
             total += (int)c[k] - 1;
             store_slot(&counts[g], 0u);
@@ -776,6 +790,10 @@ void shares_wave_kernel(const Params p) {
       }
     }
     if (counter) s_count[0] = lost_count ? -1 : total;
+    // a lost slot's value may land after this call: the sticky status keeps later calls off the
+    // workspace until ekv_tile_shares_reset clears it
+    if (lost || (counter && lost_count))
+      __hip_atomic_store(p.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     count = s_count[0];
     v = lost ? NAN : acc;
@@ -863,8 +881,13 @@ int split_groups(int nrows, int layers) {
 // call's shape, and no call writes partials over them.
 size_t split_workspace(int nrows, int width, int layers) {
   const size_t parts = (size_t)nrows * layers * width * sizeof(float);
-  return kArrivalBytes + ((parts + 255) / 256) * 256 + (size_t)nrows * layers * sizeof(int32_t);
+  return kHeaderBytes + kArrivalBytes + ((parts + 255) / 256) * 256 + (size_t)nrows * layers * sizeof(int32_t);
 }
+
+// The wave form's wait for a slot, for every call in the process: the reloads before a slot is
+// taken as lost, and (tests of the failure path only) whether every wait is made to run to it.
+int g_spin_limit = kSpinLimit;
+int g_lose = 0;
 
 // the register form's layers per group for J blocks per thread (at most 12 quads of each plane)
 constexpr int reg_layers(int J) { return J == 1 ? 8 : (J == 4 ? 2 : 4); }
@@ -897,8 +920,11 @@ int launch(Params p, int nrows, void *workspace, size_t workspace_bytes, void *s
   const int group_layers = (p.layers + p.groups - 1) / p.groups;  // the largest group
   if (split) {
     const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
-    p.arrivals = (int32_t *)workspace;
-    p.part = (float *)((char *)workspace + kArrivalBytes);
+    p.status = (int32_t *)workspace;
+    p.spin_limit = g_spin_limit;
+    p.lose = g_lose;
+    p.arrivals = (int32_t *)((char *)workspace + kHeaderBytes);
+    p.part = (float *)((char *)workspace + kHeaderBytes + kArrivalBytes);
     p.part_count = (int32_t *)((char *)p.part + ((parts + 255) / 256) * 256);
   }
   const size_t lds = (size_t)2 * group_layers * cp * sizeof(float);
@@ -1077,6 +1103,53 @@ extern "C" int ekv_tile_shares_noalloc(const float *lse, int64_t lse_plane_strid
   p.shares = shares;
   p.shares_stride = shares_stride;
   return shares::launch(p, nrows, ws, (size_t)EKV_TILE_SHARES_SCRATCH_BYTES, stream);
+}
+
+namespace ekv {
+namespace shares {
+
+// Zeroes a workspace (a kernel, not a memset, so that a captured graph can hold it).
+__global__ __launch_bounds__(256) void clear_kernel(uint4 *ws, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    ws[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+}  // namespace shares
+}  // namespace ekv
+
+extern "C" int ekv_tile_shares_status(const void *workspace, int32_t *status) {
+  if (status == nullptr) return fail(EKV_EINVAL, "ekv_tile_shares_status: null status");
+  void *ws = const_cast<void *>(workspace);
+  if (ws == nullptr) {
+    const int rc = device_scratch(&ws);
+    if (rc != EKV_OK) return rc;
+  }
+  int rc = check_hip(hipDeviceSynchronize(), "ekv_tile_shares_status synchronize");
+  if (rc != EKV_OK) return rc;
+  return check_hip(hipMemcpy(status, ws, sizeof(int32_t), hipMemcpyDeviceToHost), "ekv_tile_shares_status copy");
+}
+
+extern "C" int ekv_tile_shares_reset(void *workspace, size_t workspace_bytes, void *stream) {
+  void *ws = workspace;
+  size_t bytes = workspace_bytes;
+  if (ws == nullptr) {
+    const int rc = device_scratch(&ws);
+    if (rc != EKV_OK) return rc;
+    bytes = (size_t)EKV_TILE_SHARES_SCRATCH_BYTES;
+  }
+  if (((uintptr_t)ws & 15) != 0 || bytes % 16 != 0)
+    return fail(EKV_EINVAL, "ekv_tile_shares_reset: the workspace must be 16-byte aligned and sized");
+  const size_t n16 = bytes / 16;
+  if (n16 == 0) return EKV_OK;
+  const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 4096);
+  hipLaunchKernelGGL(shares::clear_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (uint4 *)ws, n16);
+  return check_hip(hipGetLastError(), "ekv_tile_shares_reset launch");
+}
+
+extern "C" int ekv_tile_shares_test_wait(int32_t spin_limit, int32_t lose) {
+  shares::g_spin_limit = spin_limit > 0 ? spin_limit : shares::kSpinLimit;
+  shares::g_lose = lose != 0;
+  return EKV_OK;
 }
 
 extern "C" int ekv_normalize_tile_lse(const float *u, int64_t u_layer_stride, int64_t u_row_stride,

@@ -27,6 +27,22 @@ _f32 = ctypes.c_float
 _f64 = ctypes.c_double
 _sz = ctypes.c_size_t
 
+
+class AuditLayer(ctypes.Structure):
+    """``ekv_audit_layer_t``: one layer of a multi-layer audit launch."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("keys", ctypes.c_void_p),
+        ("layer", ctypes.c_int32),
+        ("group_first", ctypes.c_int32),
+        ("q_head0", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("k_scale", ctypes.c_float),
+        ("pad", ctypes.c_int32),
+    ]
+
+
 _SIGNATURES: dict[str, list] = {
     "ekv_last_error": [],
     "ekv_abi_version": [],
@@ -58,10 +74,33 @@ _SIGNATURES: dict[str, list] = {
         _p, _sz, _i32, _i32,  # plan, plan bytes, plan rows, plan width
         _p,  # stream
     ],
+    "ekv_audit_planned_shape": [_i32, _i32, _i32, _i32],
+    "ekv_audit_tile_lse_layers": [
+        ctypes.POINTER(AuditLayer), _i32, _i32,  # layers, count, queries by row
+        _i32, _i64, _i64,  # q dtype, strides
+        _i32, _i64, _i64, _i64,  # kv dtype, strides
+        _p, _i64, _p, _p, _p, _p,  # table, stride, lens, qrow, select, flag
+        _p, _i64, _i64, _i64, _i32,  # lse, plane / layer / row strides, cells
+        _p, _i32,  # cycles, cycles_rows
+        _i32, _i32,  # groups, group_rows
+        _i32, _i32, _i32, _i32, _i32,  # rows, width, block_size, tile_blocks, head_dim
+        _p, _sz, _i32, _i32,  # plan, plan bytes, plan rows, plan width
+        _p,  # stream
+    ],
+    "ekv_audit_stage_queries": [
+        _p, _i32, _i64, _i64,  # q, q dtype, strides
+        _i32, _i32, _i32,  # head_first, heads, head_dim
+        _p, _p, _p, _i32,  # qrow, select, flag, rows
+        _p, _i64,  # staged, staged row stride
+        _p,  # stream
+    ],
     "ekv_tile_shares": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_tile_shares_workspace": [_i32, _i32, _i32],
     "ekv_tile_shares_ws": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p, _sz, _p],
     "ekv_tile_shares_noalloc": [_p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _p],
+    "ekv_tile_shares_status": [_p, ctypes.POINTER(_i32)],
+    "ekv_tile_shares_reset": [_p, _sz, _p],
+    "ekv_tile_shares_test_wait": [_i32, _i32],
     "ekv_normalize_tile_lse": [_p, _i64, _i64, _i32, _i32, _i32, _p, _i32, _i32, _i32, _p, _i64, _p],
     "ekv_rank_uniform": [
         _p, _i64, _p, _p, _p, _i64, _p, _i32, _p, _i64, _i32, _i32, _f64, _i64, _p, _i64, _p, _p,
@@ -117,6 +156,12 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built: run `python sigmod-kvscope_amd/build.py` (or __graft_entry__.build())"
         )
+    # One HIP runtime per process, and the same in every process: torch ships its own, and the
+    # library binds to whichever copy is loaded first.  Loading torch's first means a serving process
+    # (which imports torch before anything else) and a reader process agree, so the IPC handles one
+    # exports open in the other (handles of different runtime versions do not).
+    import torch  # noqa: F401
+
     lib = ctypes.CDLL(LIB_PATH)
     for name, args in _SIGNATURES.items():
         fn = getattr(lib, name)

@@ -206,6 +206,24 @@ def shares_workspace_bytes(rows: int, width: int, layers: int) -> int:
     return int(ekv_hip.load().ekv_tile_shares_workspace(int(rows), int(width), int(layers)))
 
 
+def check_workspace(workspace: torch.Tensor | None) -> None:
+    """Raise ``RuntimeError`` when a call on ``workspace`` (None: this device's scratch of the
+    allocation-free form) lost a partial: its rows came out as NaN and the slot may have been
+    written after the call.  The workspace is reset first, so the next call runs on a sound one.
+    Waits for the device."""
+    import ctypes
+
+    status = ctypes.c_int32(0)
+    address = 0 if workspace is None else workspace.data_ptr()
+    ekv_hip.call("ekv_tile_shares_status", address, ctypes.byref(status))
+    if status.value == 0:
+        return
+    ekv_hip.call("ekv_tile_shares_reset", address, 0 if workspace is None else workspace.numel(), 0)
+    ekv_hip.synchronize()
+    raise RuntimeError("a share partial never reached the workgroup that adds a row's partials: those rows are "
+                       "NaN; the workspace has been reset")
+
+
 class DeviceTileShareSource:
     """Reads the live rows' shares with the normalisation on the device.
 
@@ -257,4 +275,5 @@ class DeviceTileShareSource:
             self.tile_blocks, self.aggregate, out=out, workspace=self._workspace,
         )
         shares[wanted] = out.cpu().numpy()  # waits for the copies and the kernels
+        check_workspace(self._workspace)
         return shares

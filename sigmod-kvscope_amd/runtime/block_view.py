@@ -336,6 +336,9 @@ class DecodeView:
         audited rows are the rows of that step's batch."""
         if self._pending is None:
             return
+        flush = getattr(self.audit, "flush", None)
+        if flush is not None:
+            flush()  # layers an audit kernel still holds for one launch
         if self._device is not None and self._device.type == "cuda":
             torch.cuda.synchronize(self._device)
         rows, st = self._pending, self._state

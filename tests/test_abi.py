@@ -45,7 +45,7 @@ def test_argument_errors_map_to_value_error():
 
 COMPUTE = ("ekv_audit_tile_lse", "ekv_tile_shares", "ekv_tile_shares_ws", "ekv_tile_shares_noalloc", "ekv_normalize_tile_lse",
            "ekv_rank_uniform", "ekv_rank_uniform_ws", "ekv_rank_uniform_view", "ekv_rank_sum", "ekv_rank_maxmin", "ekv_compact_view",
-           "ekv_build_view", "ekv_compact_slots", "ekv_controller_keep")
+           "ekv_build_view", "ekv_compact_slots", "ekv_controller_keep", "ekv_audit_stage_queries")
 
 
 def test_every_entry_point_rejects_null_pointers_on_the_host():
@@ -111,3 +111,30 @@ def test_shape_limits_are_refused_on_the_host():
             bad[0] = ekv_hip.OBJ_MAXMIN
         with pytest.raises(ValueError, match=match):
             ekv_hip.call("ekv_controller_keep", *bad)
+
+
+def test_the_multi_layer_audit_refuses_bad_layer_lists_on_the_host():
+    import pytest
+
+    lib = ekv_hip.load()
+    args = [0] * len(lib.ekv_audit_tile_lse_layers.argtypes)
+    args[0] = None
+    args[1] = 1
+    with pytest.raises(ValueError, match="layer list"):
+        ekv_hip.call("ekv_audit_tile_lse_layers", *args)
+    # a shape without a planned form (fp32 keys) is refused before anything else
+    one = (ekv_hip.AuditLayer * 1)(ekv_hip.AuditLayer(256, 256, 0, 0, 0, 1.0, 1.0, 0))
+    args = [one, 1, 1, ekv_hip.F32, 512, 128, ekv_hip.F32, 1 << 16, 1024, 128] + [0] * (len(args) - 10)
+    args[-8], args[-7], args[-6] = 16, 2, 128  # block size, tiles of 2 blocks, head dim
+    with pytest.raises(ValueError, match="planned form"):
+        ekv_hip.call("ekv_audit_tile_lse_layers", *args)
+
+
+def test_planned_shapes():
+    lib = ekv_hip.load()
+    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 16) == 1
+    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.FP8_E4M3, 128, 32) == 1
+    assert lib.ekv_audit_planned_shape(ekv_hip.F16, ekv_hip.F16, 64, 16) == 1
+    assert lib.ekv_audit_planned_shape(ekv_hip.F32, ekv_hip.F32, 128, 16) == 0  # the VALU kernel
+    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 8) == 0  # 16-token tiles
+    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 32, 16) == 0

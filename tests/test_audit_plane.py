@@ -84,3 +84,83 @@ def test_newest_rows_check(monkeypatch, tmp_path):
     with open(os.path.join(tmp_path, f"ekv_coverage_{os.getpid()}.json"), "w") as f:
         f.write(json.dumps(unsafe) + "\n")
     plane.require_newest_rows()  # checked once
+
+
+# -- RecordingPlane's host rules, without a device ------------------------------------------------
+
+
+def host_plane(rows):
+    """A RecordingPlane with host tensors in place of its device buffers, for its host-side rules."""
+    import torch
+
+    from runtime.audit_kernel import RecordingPlane
+
+    plane = RecordingPlane.__new__(RecordingPlane)
+    plane.rows = rows
+    plane._select = torch.zeros(rows, dtype=torch.uint8)
+    plane._token = torch.zeros(rows, dtype=torch.int32)
+    plane._pending = []
+    plane._plan_stale = False
+    return plane
+
+
+def test_select_clears_the_rows_past_a_shrinking_batch():
+    plane = host_plane(8)
+    plane.select(np.ones(8, bool), np.arange(8) * 3)
+    assert plane._select.tolist() == [1] * 8 and plane._token.tolist() == [0, 3, 6, 9, 12, 15, 18, 21]
+    plane._plan_stale = False
+    plane.select(np.array([1, 0, 1, 1], bool), np.array([5, 6, 7, 8]))
+    # rows 4-7 are no longer selected and their old query tokens are gone
+    assert plane._select.tolist() == [1, 0, 1, 1, 0, 0, 0, 0]
+    assert plane._token.tolist() == [5, 6, 7, 8, 0, 0, 0, 0]
+    assert plane._plan_stale  # the next record rebuilds the step plan
+    plane.select(np.zeros(0, bool), np.zeros(0, np.int64))
+    assert plane._select.tolist() == [0] * 8
+    with pytest.raises(ValueError, match="exceed"):
+        plane.select(np.ones(9, bool), np.arange(9))
+    with pytest.raises(ValueError, match="query tokens"):
+        plane.select(np.ones(4, bool), np.arange(3))
+
+
+def test_a_statistic_block_of_2_gib_is_refused_before_allocating():
+    from runtime.audit_kernel import IPC_LIMIT_BYTES, RecordingPlane
+
+    # 32 layers x 256 rows x 8192 blocks x 4 query rows x 2 planes x 4 B = 2.15 GB: refused with the limit named
+    with pytest.raises(ValueError, match=str(IPC_LIMIT_BYTES)):
+        RecordingPlane(32, 256, 8192, 4, 16)
+    # one cell fewer per block stays under it (the size rule alone; not constructed here)
+    assert 2 * 32 * 256 * 8192 * 3 * 4 < IPC_LIMIT_BYTES
+    with pytest.raises(ValueError, match="IPC"):
+        RecordingPlane(1, 1 << 16, 1 << 12, 2, 16)  # exactly 2 GiB
+
+
+def test_the_timer_is_published_with_the_keys_its_readers_need(monkeypatch, tmp_path):
+    """The timer's descriptor line carries pid, kernel, max_rows, timer_dev, timer_ipc and
+    timer_bytes (mlir_pass/lib/eKVTimer.cpp:588-590), on a line of its own, and the readers find it."""
+    import ekv_hip
+    from observe.zero_touch import find_published
+    from runtime.audit_kernel import RecordingPlane
+
+    monkeypatch.setenv("EKV_RUNTIME_DIR", str(tmp_path))
+    monkeypatch.setattr(ekv_hip, "ipc_handle", lambda address: address.to_bytes(64, "little"))
+    plane = RecordingPlane.__new__(RecordingPlane)
+    plane.pid = 4242
+    plane.rows, plane.width, plane._layers, plane.cells = 6, 10, 3, 4
+    plane._lse, plane._flag_dev, plane._table_dev, plane._cycles_dev = 1 << 20, 1 << 21, 1 << 22, 1 << 23
+    plane._publish()
+    lines = [json.loads(t) for t in open(os.path.join(tmp_path, "ekv_pass_4242.json"))]
+    assert len(lines) == 2
+    stat, timer = lines
+    assert "pid" not in stat and "timer_dev" not in stat  # a capture-buffer reader never takes the planes
+    assert stat["tile_lse_dev"] == 1 << 20 and stat["stat_flag_dev"] == 1 << 21
+    assert timer["pid"] == 4242 and timer["max_rows"] == 6 and timer["timer_dev"] == 1 << 23
+    assert timer["timer_bytes"] == 6 * 8 and timer["kernel"] == "ekv_audit_tile_lse"
+    assert bytes.fromhex(timer["timer_ipc"]) == (1 << 23).to_bytes(64, "little")
+    found = find_published(4242)
+    assert len(found) == 1 and found[0].timer_dev == 1 << 23 and found[0].timer_bytes == 48
+    assert found[0].max_rows == 6 and found[0].pid == 4242
+    # no timer: only the statistic line
+    plane._cycles_dev = 0
+    plane.pid = 4243
+    plane._publish()
+    assert find_published(4243) == []

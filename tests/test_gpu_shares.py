@@ -208,3 +208,67 @@ def test_one_workspace_across_shapes_is_left_zero():
         assert int(torch.count_nonzero(workspace)) == 0, what
         want = ots.normalize(ots.read_rows(planes, layers, np.arange(rows), 2), row_blocks, 2, aggregate)
         assert_close(reused.cpu().numpy().astype(np.float64), want, what=what)
+
+
+def test_a_lost_partial_sets_a_sticky_status_until_reset():
+    """The single-kernel split form waits a bounded number of reloads for a row's other partials.
+    Made to give up from the host (every wait runs to a limit of 8 reloads and takes nothing, so
+    every kernel ends normally), the rows come out NaN and the workspace's status is set; later calls
+    leave its slots alone (NaN rows) until check_workspace raises and resets it, after which a call
+    gives the first call's shares bit for bit and leaves the workspace zero.  The same for the
+    allocation-free form's scratch."""
+    import ctypes
+
+    import ekv_hip
+
+    rng = np.random.default_rng(313)
+    layers, rows, width, cells = 32, 6, 200, 4  # the wave form: four 8-layer groups per row
+    m = rng.normal(0, 3, (layers, rows, width, cells)).astype(np.float32)
+    l = rng.uniform(0.5, 30, (layers, rows, width, cells)).astype(np.float32)
+    planes = np.stack([m, l])
+    dev = planes_on_device(planes)
+    blocks = torch.from_numpy(rng.integers(1, width + 1, size=rows).astype(np.int32)).cuda()
+    workspace = torch.zeros(tile_shares.shares_workspace_bytes(rows, width, layers), dtype=torch.uint8, device="cuda")
+
+    def status(ws):
+        value = ctypes.c_int32(-1)
+        ekv_hip.call("ekv_tile_shares_status", 0 if ws is None else ws.data_ptr(), ctypes.byref(value))
+        return value.value
+
+    def call(ws):
+        return tile_shares.tile_shares(dev.data_ptr(), layers, layers, rows, width, cells, None, blocks, 2, "mean",
+                                       workspace=ws).cpu().numpy()
+
+    def call_noalloc():
+        out = torch.full((rows, width), 7.0, dtype=torch.float32, device="cuda")
+        stride = rows * width * cells
+        ekv_hip.call("ekv_tile_shares_noalloc", dev.data_ptr(), layers * stride, stride, width * cells, layers, cells,
+                     width, 0, blocks.data_ptr(), rows, 2, ekv_hip.AGG_MEAN, out.data_ptr(), width,
+                     ekv_hip.stream_handle())
+        return out.cpu().numpy()
+
+    good = call(workspace)
+    assert status(workspace) == 0 and not np.isnan(good).any()
+    for ws, run in ((workspace, lambda: call(workspace)), (None, call_noalloc)):
+        try:
+            ekv_hip.call("ekv_tile_shares_test_wait", 8, 1)
+            lost = run()
+        finally:
+            ekv_hip.call("ekv_tile_shares_test_wait", 0, 0)
+        try:
+            assert np.isnan(lost).all(), "a row whose partials were lost was not NaN"
+            assert status(ws) == 1
+            assert np.isnan(run()).all() and status(ws) == 1  # sticky: the slots are left alone
+            with pytest.raises(RuntimeError, match="reset"):
+                tile_shares.check_workspace(ws)
+            assert status(ws) == 0
+            again = run()
+            assert np.array_equal(again, good), "after the reset the shares differ from the first call's"
+            tile_shares.check_workspace(ws)  # sound: no error
+            if ws is not None:
+                assert int(torch.count_nonzero(ws)) == 0
+        finally:
+            if status(ws) != 0:  # leave the scratch sound for later tests whatever happened
+                ekv_hip.call("ekv_tile_shares_reset", 0 if ws is None else ws.data_ptr(),
+                             0 if ws is None else ws.numel(), 0)
+                ekv_hip.synchronize()
