@@ -116,7 +116,7 @@ int ekv_audit_plan(const int32_t *table, int64_t table_stride, const int32_t *le
  * scan of the rows, and for any number of rows (ekv_audit_tile_lse keeps per-row offsets in LDS and
  * takes at most 6000).  Replaces tile_lse_kernel + RecordingPlane.launch, runtime/audit_kernel.py
  * :34-109 and :224-265, as ekv_audit_tile_lse does.  Shapes without an MFMA form (fp32 keys,
- * 8-token blocks) run the self-contained kernel.
+ * 8-token blocks, fp8 rows of 32 dimensions) run its VALU form (ekv_audit_shape).
  */
 int ekv_audit_tile_lse_planned(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
                                const void *keys, int kv_dtype, int64_t k_stride_block, int64_t k_stride_pos,
@@ -131,11 +131,18 @@ int ekv_audit_tile_lse_planned(const void *q, int q_dtype, int64_t q_stride_toke
                                int32_t plan_width, void *stream);
 
 /*
- * 1 when ekv_audit_tile_lse_planned has a planned (MFMA) form for the shape -- 16-bit queries and
- * keys (or fp8 keys with bf16 queries), head_dim 64, 128 or 256, tiles of 32 tokens or more -- and
- * so ekv_audit_tile_lse_layers takes it; 0 otherwise.
+ * Which audit launches have a kernel for a shape: EKV_AUDIT_SELF_CONTAINED (ekv_audit_tile_lse) and
+ * EKV_AUDIT_PLANNED (ekv_audit_tile_lse_planned and ekv_audit_tile_lse_layers), or 0.  The planned
+ * launch takes every shape the reference's kernel takes (runtime/audit_kernel.py:73, :128-131): fp32,
+ * f16 and bf16 queries with keys of the same type, or fp8 keys with bf16 queries; head_dim 32 to 256
+ * (rows of 16 to 1024 bytes, powers of two); tiles of a power of two of tokens, 16 or more.  On the
+ * MFMA form: 16-bit or fp8 keys in tiles of 32 tokens or more (head_dim 32 for 16-bit keys, 64 to 256);
+ * the VALU form takes the rest.  The self-contained launch lacks some VALU shapes (head_dim 32 or 256
+ * on the VALU, rows of 64 bytes or less in 8-token blocks).
  */
-int ekv_audit_planned_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size);
+#define EKV_AUDIT_SELF_CONTAINED 1
+#define EKV_AUDIT_PLANNED 2
+int ekv_audit_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size);
 
 /* One layer of a multi-layer audit launch (ekv_audit_tile_lse_layers). */
 typedef struct ekv_audit_layer {
@@ -158,7 +165,7 @@ typedef struct ekv_audit_layer {
  * records and scale), so one launch amortises the launch's fixed costs (first key requests, the
  * spread of the workgroups' ends) over all of them.  The shared arguments are those of
  * ekv_audit_tile_lse_planned.  With q_by_row != 0, row r's query is row r of each layer's q (a
- * staged copy) instead of token qrow[r].  Only shapes with ekv_audit_planned_shape() != 0.
+ * staged copy) instead of token qrow[r].  Every shape with EKV_AUDIT_PLANNED in ekv_audit_shape().
  */
 int ekv_audit_tile_lse_layers(const ekv_audit_layer_t *layers, int32_t n_layers, int32_t q_by_row,
                               int q_dtype, int64_t q_stride_token, int64_t q_stride_head, int kv_dtype,

@@ -27,146 +27,11 @@
 #include <algorithm>
 #include <mutex>
 
-#include "ekv_common.hpp"
+#include "ekv_audit.hpp"
 
 namespace ekv {
 namespace audit {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kCuThreads = 768;  // tile_lse_cu_kernel: 12 waves, one workgroup per compute unit
-constexpr int kTileBlocks = 2;  // TILE_BLOCKS, runtime/audit_kernel.py:31
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kMaxRows = 6000;  // LDS holds two ints per row beside the kernels' staging buffers
-constexpr int kCycleSlots = 64;  // per-row cycle accumulators of a round in tile_lse_cu_kernel
-
-enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-struct Params {
-  const char *q;
-  int64_t q_stride_token, q_stride_head;  // bytes
-  const char *keys;
-  int64_t k_stride_block, k_stride_pos, k_stride_head;  // bytes
-  const int32_t *table;
-  int64_t table_stride;
-  const int32_t *lens;
-  const int32_t *qrow;
-  const uint8_t *select;
-  const uint32_t *flag;
-  float *lse;  // already offset to the layer
-  int64_t plane_stride, row_stride;
-  int32_t cells;
-  uint64_t *cycles;
-  int32_t cycles_rows;
-  float scale;  // scale * k_scale
-  int32_t group_first, groups, group_rows, rows, width, block_size, chunk_tiles, nsub, nsub_log2;
-};
-
-template <int MODE, int HEAD_DIM, int NL, int GP>
-struct Shape {
-  static constexpr int kKBytes = MODE == kModeF32 ? 4 : (MODE == kModeFp8Bf16 ? 1 : 2);
-  static constexpr int kQBytes = MODE == kModeF32 ? 4 : 2;
-  static constexpr int kRowBytes = HEAD_DIM * kKBytes;
-  static constexpr int kLPT = kRowBytes / 16;          // lanes per key row
-  static constexpr int kTPI = kWave / kLPT;            // tokens per load instruction
-  static constexpr int kEPL = 16 / kKBytes;            // key elements per lane per load
-  static constexpr int kQW = kEPL * kQBytes / 4;       // query words per head per lane
-  static constexpr int kOW = MODE == kModeFp8Bf16 ? 8 : 4;  // operand words per load
-  static constexpr int kV = NL * GP;                   // partial dots per lane
-  static constexpr int kVF = kV / kLPT;                // scores per lane after the reduction
-  static constexpr int kCT = NL * kTPI;                // tokens per chunk
-  // the shape is compiled only when a row is 16..1024 bytes and the transpose reduction
-  // leaves at least one score per lane
-  static constexpr bool kValid = kLPT >= 1 && kLPT <= kWave && (kLPT & (kLPT - 1)) == 0 && kV >= kLPT &&
-                                 kQW == kOW;
-  static constexpr int kLPH = !kValid ? 1 : (kVF <= NL ? NL / kVF : 1);  // lanes of a slot per head
-  static constexpr int kHPL = !kValid ? 1 : (kVF <= NL ? 1 : kVF / NL);  // heads per lane
-};
-
-__device__ __forceinline__ float as_float(uint32_t w) { return __builtin_bit_cast(float, w); }
-
-// Operand words of one 16-byte key load: the raw words, or fp8 pairs widened to bf16 pairs.
-template <int MODE>
-__device__ __forceinline__ void key_operand(const u32x4 k, uint32_t (&op)[MODE == kModeFp8Bf16 ? 8 : 4]) {
-  if constexpr (MODE == kModeFp8Bf16) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int w = (int)k[e];
-      op[2 * e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
-      op[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) op[e] = k[e];
-  }
-}
-
-template <int MODE, int OW>
-__device__ __forceinline__ float dot_words(const uint32_t (&qw)[OW], const uint32_t (&kw)[OW]) {
-  float acc = 0.0f;
-  if constexpr (MODE == kModeF32) {
-#pragma unroll
-    for (int e = 0; e < OW; ++e) acc = fmaf(as_float(qw[e]), as_float(kw[e]), acc);
-  } else if constexpr (MODE == kModeF16) {
-#pragma unroll
-    for (int e = 0; e < OW; ++e)
-      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, qw[e]), __builtin_bit_cast(f16x2_t, kw[e]),
-                                   acc, false);
-  } else {
-#pragma unroll
-    for (int e = 0; e < OW; ++e)
-      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, qw[e]),
-                                            __builtin_bit_cast(bf16x2_t, kw[e]), acc, false);
-  }
-  return acc;
-}
-
-// Transpose reduction over the LPT lanes of a token slot: on entry lane j of a slot holds N
-// partial sums a[0..N); on exit a[0..N/LPT) holds the complete sums of entries
-// j*N/LPT .. j*N/LPT + N/LPT - 1.  Each step halves the live entries: the lane with the mask
-// bit set keeps the upper half, its partner the lower half, and they swap the other halves.
-template <int CUR, int MASK, int N>
-__device__ __forceinline__ void transpose_reduce_step(float (&a)[N], int lane) {
-  if constexpr (MASK >= 1) {
-    constexpr int kHalf = CUR / 2;
-    const bool upper = (lane & MASK) != 0;
-#pragma unroll
-    for (int k = 0; k < kHalf; ++k) {
-      const float send = upper ? a[k] : a[k + kHalf];
-      const float keep = upper ? a[k + kHalf] : a[k];
-      a[k] = keep + shfl_xor(send, MASK);
-    }
-    transpose_reduce_step<kHalf, MASK / 2, N>(a, lane);
-  }
-}
-template <int N, int LPT>
-__device__ __forceinline__ void transpose_reduce(float (&a)[N], int lane) {
-  transpose_reduce_step<N, LPT / 2, N>(a, lane);
-}
-
-// Max / sum over the lanes that hold the same head: the low bits of the slot lane within a
-// head (LPH lanes) and every token slot (xor LPT .. 32).
-template <int LPH, int LPT>
-__device__ __forceinline__ float head_max(float v) {
-#pragma unroll
-  for (int m = 1; m < LPH; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
-#pragma unroll
-  for (int m = LPT; m < kWave; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
-  return v;
-}
-template <int LPH, int LPT>
-__device__ __forceinline__ float head_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < LPH; m <<= 1) v += shfl_xor(v, m);
-#pragma unroll
-  for (int m = LPT; m < kWave; m <<= 1) v += shfl_xor(v, m);
-  return v;
-}
 
 template <int MODE, int HEAD_DIM, int NL, int GP>
 __global__ __launch_bounds__(kThreads) void tile_lse_kernel(const Params p) {
@@ -794,14 +659,9 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
 // split points of the flat tile list over the grid, row_off[rows + 1] = each row's first tile,
 // desc[grid][cap] = the tiles of each workgroup in flat order.
 // ---------------------------------------------------------------------------------------
-constexpr int kMaxGrid = 1024;
 constexpr int kSplitThreads = 1024;
 constexpr int kFillThreads = 256;
 
-struct TileDesc {
-  int32_t row, k, valid, qtok, id0, id1, pad0, pad1;  // valid: tokens of the tile the row reaches
-};
-static_assert(sizeof(TileDesc) == 32, "a descriptor is two 16-byte loads");
 
 struct PlanLayout {
   int64_t wg, first, row_off, desc, bytes;
@@ -975,44 +835,6 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const PlanArgs a) {
   }
 }
 
-struct PlanView {
-  const int2 *wg;
-  const TileDesc *desc;
-  int32_t cap;
-};
-
-// A descriptor into VGPRs with a vector load (the offset register keeps it one: a scalar load
-// would be waited for with the wave's LDS traffic, both being counted by lgkmcnt).
-__device__ __forceinline__ void load_desc(const TileDesc *d, u32x4 &lo, u32x4 &hi) {
-  uint32_t o = 0;
-  asm volatile("" : "+v"(o));
-  const char *src = reinterpret_cast<const char *>(d) + o;
-  lo = *reinterpret_cast<const u32x4 *>(src);
-  hi = *reinterpret_cast<const u32x4 *>(src + 16);
-}
-
-// The layers of one planned launch.  A decode step's audit launches differ only in the layer:
-// its queries, its key cache, its records and its scale.  One launch can take up to
-// kMaxLaunchLayers of them, so the launch's fixed costs (the first key requests, the spread of the
-// workgroups' ends) are paid once for all of them.
-constexpr int kMaxLaunchLayers = 32;
-
-struct LayerArgs {
-  const char *q;         // the layer's queries
-  const char *keys;      // the layer's key cache
-  float *lse;            // the statistic planes, offset to the layer
-  float scale2;          // scale * k_scale * log2(e): scores in log2 units
-  int32_t group_first;   // the first audited KV head
-  int32_t q_head0;       // the query head that q's head 0 holds (a staged copy starts at the group)
-  int32_t pad;
-};
-static_assert(sizeof(LayerArgs) == 40, "packed layer arguments");
-
-struct LayerSet {
-  LayerArgs l[kMaxLaunchLayers];
-  int32_t n;         // layers in the launch
-  int32_t q_by_row;  // queries indexed by row (a staged copy), not by the row's query token
-};
 
 // The planned form of tile_lse_cu_kernel over one or more layers: the same chunks, dots, records
 // and timer.  For layer j of the launch, workgroup b takes the plan's split (b + j) mod grid, so
@@ -1402,6 +1224,9 @@ KernelFn pick_mfma_mt(bool wide) {
 template <int MODE>
 KernelFn pick_mfma_hd(int hd, bool wide) {
   switch (hd) {
+    case 32:
+      if constexpr (MODE != kModeFp8Bf16) return pick_mfma_mt<MODE, 32>(wide);  // fp8 rows of 32 B: the VALU
+      return nullptr;
     case 64: return pick_mfma_mt<MODE, 64>(wide);
     case 128: return pick_mfma_mt<MODE, 128>(wide);
     case 256: return pick_mfma_mt<MODE, 256>(wide);
@@ -1484,6 +1309,9 @@ PlannedFn pick_planned_mt(bool wide) {
 template <int MODE>
 PlannedFn pick_planned_hd(int hd, bool wide) {
   switch (hd) {
+    case 32:
+      if constexpr (MODE != kModeFp8Bf16) return pick_planned_mt<MODE, 32>(wide);
+      return nullptr;
     case 64: return pick_planned_mt<MODE, 64>(wide);
     case 128: return pick_planned_mt<MODE, 128>(wide);
     case 256: return pick_planned_mt<MODE, 256>(wide);
@@ -1502,8 +1330,10 @@ PlannedFn pick_planned(int mode, int hd, bool wide) {
 
 // The kernel choice and launch shape of one audit call.
 struct Launch {
-  KernelFn fn = nullptr;
+  KernelFn fn = nullptr;        // the self-contained kernel (none for some VALU shapes)
   PlannedFn planned = nullptr;  // the planned form, for the MFMA shapes
+  bool valu_planned = false;    // the planned form on the VALU (ekv_audit_valu.hip), for the others
+  int mode = 0, head_dim = 0;
   int threads = kThreads;
   size_t lds = 0;
   int64_t blocks = 0;
@@ -1551,10 +1381,14 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
   const int lpt = row_bytes / 16;
   const int tpi = kWave / lpt;
   const int tile_tokens = kTileBlocks * block_size;
-  // 16-bit and fp8 keys use the MFMA form when a 32-token chunk fits the tile; otherwise (fp32
-  // keys, block size 8) the dot products run on the VALU.
-  const bool use_mfma = mode != kModeF32 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
-                        tile_tokens % 32 == 0;
+  // 16-bit and fp8 keys use the MFMA form when a 32-token chunk fits the tile (and, for fp8, a
+  // k-step holds two 16-byte pieces of the row); otherwise (fp32 keys, blocks of 8 tokens, fp8 rows
+  // of 32 dimensions) the dot products run on the VALU
+  const bool use_mfma = mode != kModeF32 && tile_tokens % 32 == 0 &&
+                        (head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+                         (head_dim == 32 && mode != kModeFp8Bf16));
+  L.mode = mode;
+  L.head_dim = head_dim;
   int nsub = 1;
   if (use_mfma) {
     const bool wide = tile_tokens % 64 == 0;
@@ -1562,27 +1396,35 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
     L.planned = pick_planned(mode, head_dim, wide);
     nsub = tile_tokens / (16 * chunk_mtiles(row_bytes, wide));  // chunks of up to 8 KB of keys
     L.threads = kCuThreads;
+  } else if (planned) {
+    // the planned VALU form: lanes of 16, 8 or 4 bytes, so that a load instruction sits in a block
+    L.valu_planned = valu_planned_shape(mode, head_dim, block_size);
+    nsub = valu_planned_nsub(mode, head_dim, block_size, group_rows);
+    if (!L.valu_planned || nsub < 1)
+      return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no planned kernel for dtype %d, head_dim %d, block size %d",
+                  kv_dtype, head_dim, block_size);
   } else {
-    // A chunk is NL load instructions of TPI tokens (8 KB of keys at NL = 8).  A load
-    // instruction must sit inside one block, and a chunk inside one tile.
+    // The self-contained VALU form: a chunk is NL load instructions of TPI tokens of 16-byte lanes
+    // (8 KB of keys at NL = 8).  A load instruction must sit inside one block, and a chunk inside
+    // one tile; other shapes take the planned form.
     if (block_size % tpi != 0)
-      return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: block size %d is below the %d tokens of one load",
-                  block_size, tpi);
+      return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: block size %d is below the %d tokens of one load (a "
+                  "step plan takes this shape)", block_size, tpi);
     const int nl = tile_tokens / tpi >= 8 ? 8 : tile_tokens / tpi;
     const int gp = group_rows <= 4 ? 4 : (group_rows <= 8 ? 8 : 16);
     L.fn = pick(mode, head_dim, nl, gp);
     nsub = tile_tokens / (nl * tpi);
     L.threads = kThreads;
   }
-  if (L.fn == nullptr)
-    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, block size %d",
-                kv_dtype, head_dim, block_size);
-  // the self-contained kernels keep per-row tile offsets in LDS; a planned MFMA launch reads them
-  // from the plan and takes any number of rows
-  const bool row_lds = !(planned && use_mfma);
+  if (L.fn == nullptr && L.planned == nullptr && !L.valu_planned)
+    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: no kernel for dtype %d, head_dim %d, block size %d (a step "
+                "plan takes more shapes)", kv_dtype, head_dim, block_size);
+  // the self-contained kernels keep per-row tile offsets in LDS; a planned launch reads them from the
+  // plan and takes any number of rows
+  const bool row_lds = !planned;
   if (row_lds && rows > kMaxRows)
-    return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d rows; a launch without a step plan (or with fp32 keys or "
-                "8-token blocks) takes at most %d", rows, kMaxRows);
+    return fail(EKV_EINVAL, "ekv_audit_tile_lse: %d rows; a launch without a step plan takes at most %d", rows,
+                kMaxRows);
   // 16-byte loads of key rows and query slices
   const uint64_t kaddr = (uint64_t)keys | (uint64_t)(k_stride_block * kbytes) |
                          (uint64_t)(k_stride_pos * kbytes) | (uint64_t)(k_stride_head * kbytes);
@@ -1628,12 +1470,12 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
   // One resident wave per slot the GPU has: the work list is split evenly over the grid, so a
   // second round of workgroups would only add a tail.  chunk_tiles bounds the grid for small
   // batches (at least that many tiles per wave).
+  if (!row_lds) return EKV_OK;  // the planned launch's grid is one workgroup per compute unit
   L.lds = (size_t)(use_mfma ? 2 * rows + 1 : rows + 1) * sizeof(int);
   const int64_t max_tiles = (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks) * groups;
   const int64_t min_per_wave = p.chunk_tiles;
   const int waves = L.threads / kWave;
   int64_t blocks = (max_tiles + min_per_wave * waves - 1) / (min_per_wave * waves);
-  if (!row_lds) return EKV_OK;  // the planned launch's grid is one workgroup per compute unit
   const int resident = resident_blocks(L.fn, L.lds, L.threads);
   if (resident < 1)
     return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse: a workgroup of %d threads with %zu bytes of row data does "
@@ -1664,8 +1506,8 @@ int check_plan(const void *plan, size_t plan_bytes, int32_t plan_rows, int32_t p
   return EKV_OK;
 }
 
-// One planned launch of the layers `ls` on the plan's grid.
-int launch_planned(PlannedFn fn, const Params &p, const LayerSet &ls, const void *plan, int32_t plan_rows,
+// One planned launch of the layers `ls` on the plan's grid: the MFMA form, or the VALU one.
+int launch_planned(const Launch &L, const Params &p, const LayerSet &ls, const void *plan, int32_t plan_rows,
                    int32_t plan_width, void *stream, const char *what) {
   const int grid = plan_grid();
   const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
@@ -1673,7 +1515,9 @@ int launch_planned(PlannedFn fn, const Params &p, const LayerSet &ls, const void
   v.wg = (const int2 *)((const char *)plan + Lp.wg);
   v.desc = (const TileDesc *)((const char *)plan + Lp.desc);
   v.cap = Lp.cap;
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v, ls);
+  if (L.planned == nullptr)
+    return launch_valu_layers(L.mode, L.head_dim, p.block_size, p.group_rows, p, v, ls, grid, (hipStream_t)stream, what);
+  hipLaunchKernelGGL(L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v, ls);
   return check_hip(hipGetLastError(), what);
 }
 
@@ -1770,27 +1614,35 @@ extern "C" int ekv_audit_tile_lse_planned(
   if (rc != EKV_OK) return rc;
   rc = check_plan(plan, plan_bytes, plan_rows, plan_width, rows, width, "ekv_audit_tile_lse_planned");
   if (rc != EKV_OK || rows == 0) return rc;
-  if (L.planned == nullptr) {  // the VALU shapes have no planned form: the self-contained kernel
-    hipLaunchKernelGGL(L.fn, dim3((unsigned)L.blocks), dim3(L.threads), L.lds, (hipStream_t)stream, p);
-    return check_hip(hipGetLastError(), "ekv_audit_tile_lse_planned launch");
-  }
   LayerSet ls{};
   ls.n = 1;
   ls.q_by_row = 0;
-  ls.l[0] = LayerArgs{p.q, p.keys, p.lse, p.scale * kLog2e, p.group_first, 0, 0};
-  return launch_planned(L.planned, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_planned launch");
+  ls.l[0] = LayerArgs{p.q, p.keys, p.lse, p.scale * kLog2e, p.group_first, 0, p.scale};
+  return launch_planned(L, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_planned launch");
 }
 
-extern "C" int ekv_audit_planned_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size) {
-  if (block_size <= 0) return 0;
+extern "C" int ekv_audit_shape(int q_dtype, int kv_dtype, int32_t head_dim, int32_t block_size) {
   int mode;
-  if (kv_dtype == EKV_F16 && q_dtype == EKV_F16) mode = kModeF16;
+  if (kv_dtype == EKV_F32 && q_dtype == EKV_F32) mode = kModeF32;
+  else if (kv_dtype == EKV_F16 && q_dtype == EKV_F16) mode = kModeF16;
   else if (kv_dtype == EKV_BF16 && q_dtype == EKV_BF16) mode = kModeBF16;
   else if (kv_dtype == EKV_FP8_E4M3 && q_dtype == EKV_BF16) mode = kModeFp8Bf16;
   else return 0;
-  (void)mode;
-  return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (kTileBlocks * block_size) % 32 == 0 &&
-         ((kTileBlocks * block_size) & (kTileBlocks * block_size - 1)) == 0;
+  const int tile_tokens = kTileBlocks * block_size;
+  if (block_size <= 0 || (tile_tokens & (tile_tokens - 1)) != 0) return 0;
+  const int row_bytes = head_dim * dtype_bytes(kv_dtype);
+  if (row_bytes < 16 || row_bytes > 1024 || (row_bytes & (row_bytes - 1)) != 0) return 0;
+  const bool use_mfma = mode != kModeF32 && tile_tokens % 32 == 0 &&
+                        (head_dim == 64 || head_dim == 128 || head_dim == 256 ||
+                         (head_dim == 32 && mode != kModeFp8Bf16));
+  if (use_mfma) return EKV_AUDIT_SELF_CONTAINED | EKV_AUDIT_PLANNED;
+  int bits = valu_planned_shape(mode, head_dim, block_size) ? EKV_AUDIT_PLANNED : 0;
+  const int tpi = kWave / (row_bytes / 16);
+  if (block_size % tpi == 0) {
+    const int nl = tile_tokens / tpi >= 8 ? 8 : tile_tokens / tpi;
+    if (pick(mode, head_dim, nl, 4) != nullptr) bits |= EKV_AUDIT_SELF_CONTAINED;
+  }
+  return bits;
 }
 
 extern "C" int ekv_audit_tile_lse_layers(
@@ -1803,9 +1655,6 @@ extern "C" int ekv_audit_tile_lse_layers(
     int32_t plan_rows, int32_t plan_width, void *stream) {
   if (layers == nullptr || n_layers < 0) return fail(EKV_EINVAL, "ekv_audit_tile_lse_layers: no layer list");
   if (n_layers == 0) return EKV_OK;
-  if (!ekv_audit_planned_shape(q_dtype, kv_dtype, head_dim, block_size))
-    return fail(EKV_EUNSUPPORTED, "ekv_audit_tile_lse_layers: dtype %d / %d, head_dim %d, block %d has no planned form",
-                q_dtype, kv_dtype, head_dim, block_size);
   // the shared arguments, checked with the first layer's pointers; every layer's own below
   Params p;
   Launch L;
@@ -1836,9 +1685,9 @@ extern "C" int ekv_audit_tile_lse_layers(
     for (int i = 0; i < ls.n; ++i) {
       const ekv_audit_layer_t &e = layers[first + i];
       ls.l[i] = LayerArgs{(const char *)e.q, (const char *)e.keys, lse + (int64_t)e.layer * lse_layer_stride,
-                          e.scale * e.k_scale * kLog2e, e.group_first, e.q_head0, 0};
+                          e.scale * e.k_scale * kLog2e, e.group_first, e.q_head0, e.scale * e.k_scale};
     }
-    rc = launch_planned(L.planned, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_layers launch");
+    rc = launch_planned(L, p, ls, plan, plan_rows, plan_width, stream, "ekv_audit_tile_lse_layers launch");
     if (rc != EKV_OK) return rc;
   }
   return EKV_OK;

@@ -18,6 +18,7 @@ LIB_PATH = os.environ.get("EKV_HIP_LIB") or os.path.join(HERE, "lib", "libekv_hi
 OK, EINVAL, ELAUNCH, EUNSUPPORTED = 0, -1, -2, -3
 F32, F16, BF16, FP8_E4M3, F64 = 0, 1, 2, 3, 4
 AGG_MEAN, AGG_MAX = 0, 1
+AUDIT_SELF_CONTAINED, AUDIT_PLANNED = 1, 2
 OBJ_SUM, OBJ_MAXMIN = 0, 1
 
 _p = ctypes.c_void_p
@@ -74,7 +75,7 @@ _SIGNATURES: dict[str, list] = {
         _p, _sz, _i32, _i32,  # plan, plan bytes, plan rows, plan width
         _p,  # stream
     ],
-    "ekv_audit_planned_shape": [_i32, _i32, _i32, _i32],
+    "ekv_audit_shape": [_i32, _i32, _i32, _i32],
     "ekv_audit_tile_lse_layers": [
         ctypes.POINTER(AuditLayer), _i32, _i32,  # layers, count, queries by row
         _i32, _i64, _i64,  # q dtype, strides

@@ -291,7 +291,7 @@ class RecordingPlane(AuditPlane):
             q_code, k_code = ekv_hip.dtype_code(query.dtype), ekv_hip.dtype_code(keys.dtype)
         except ValueError:
             return False
-        return bool(ekv_hip.load().ekv_audit_planned_shape(q_code, k_code, keys.shape[3], self.block_size))
+        return bool(ekv_hip.load().ekv_audit_shape(q_code, k_code, keys.shape[3], self.block_size) & ekv_hip.AUDIT_PLANNED)
 
     def stage(self, layer: int, query: torch.Tensor, keys: torch.Tensor, scale: float, *, k_scale: float = 1.0,
               stream=None) -> "ekv_hip.AuditLayer":
@@ -427,6 +427,12 @@ class RecordingPlane(AuditPlane):
         self._check_layer(query, keys)
         kv_heads, dim = keys.shape[2], keys.shape[3]
         rows, width = self._batch_shape(table, lens)
+        if not planned and self._plan:
+            forms = ekv_hip.load().ekv_audit_shape(ekv_hip.dtype_code(query.dtype), ekv_hip.dtype_code(keys.dtype),
+                                                   dim, self.block_size)
+            if not forms & ekv_hip.AUDIT_SELF_CONTAINED and forms & ekv_hip.AUDIT_PLANNED:
+                self.plan(table, lens, stream=stream)  # only the planned launch has this shape
+                planned = True
         if planned and not self._plan:
             raise RuntimeError("this plane is too large for a step plan")
         if planned and self._inputs(table, lens) != self._plan_inputs:

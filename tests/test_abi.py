@@ -122,19 +122,34 @@ def test_the_multi_layer_audit_refuses_bad_layer_lists_on_the_host():
     args[1] = 1
     with pytest.raises(ValueError, match="layer list"):
         ekv_hip.call("ekv_audit_tile_lse_layers", *args)
-    # a shape without a planned form (fp32 keys) is refused before anything else
+    # a query type the keys do not pair with, and a null table, refused before any launch
     one = (ekv_hip.AuditLayer * 1)(ekv_hip.AuditLayer(256, 256, 0, 0, 0, 1.0, 1.0, 0))
-    args = [one, 1, 1, ekv_hip.F32, 512, 128, ekv_hip.F32, 1 << 16, 1024, 128] + [0] * (len(args) - 10)
-    args[-8], args[-7], args[-6] = 16, 2, 128  # block size, tiles of 2 blocks, head dim
-    with pytest.raises(ValueError, match="planned form"):
+    P = 256
+    args = [one, 1, 1, ekv_hip.F16, 512, 128, ekv_hip.BF16, 1 << 16, 1024, 128, P, 8, P, P, P, P, P, 1 << 20, 1 << 16,
+            64, 4, 0, 0, 1, 4, 4, 8, 16, 2, 128, P, 1 << 20, 4, 8, 0]
+    with pytest.raises(ValueError, match="not supported"):
+        ekv_hip.call("ekv_audit_tile_lse_layers", *args)
+    args[3] = ekv_hip.BF16
+    args[10] = 0
+    with pytest.raises(ValueError, match="null"):
         ekv_hip.call("ekv_audit_tile_lse_layers", *args)
 
 
-def test_planned_shapes():
+def test_audit_shapes():
     lib = ekv_hip.load()
-    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 16) == 1
-    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.FP8_E4M3, 128, 32) == 1
-    assert lib.ekv_audit_planned_shape(ekv_hip.F16, ekv_hip.F16, 64, 16) == 1
-    assert lib.ekv_audit_planned_shape(ekv_hip.F32, ekv_hip.F32, 128, 16) == 0  # the VALU kernel
-    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 8) == 0  # 16-token tiles
-    assert lib.ekv_audit_planned_shape(ekv_hip.BF16, ekv_hip.BF16, 32, 16) == 0
+    both = ekv_hip.AUDIT_SELF_CONTAINED | ekv_hip.AUDIT_PLANNED
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 16) == both
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.FP8_E4M3, 128, 32) == both
+    assert lib.ekv_audit_shape(ekv_hip.F16, ekv_hip.F16, 64, 16) == both
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.BF16, 32, 16) == both  # MFMA at 32 dimensions
+    assert lib.ekv_audit_shape(ekv_hip.F32, ekv_hip.F32, 128, 16) == both  # the VALU forms
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 8) == both
+    # the VALU shapes only a step plan takes: 32 or 256 dimensions on the VALU, small rows in 8-token blocks
+    for q, k, d, bs in ((ekv_hip.F32, ekv_hip.F32, 32, 16), (ekv_hip.F32, ekv_hip.F32, 256, 8),
+                        (ekv_hip.BF16, ekv_hip.BF16, 256, 8), (ekv_hip.BF16, ekv_hip.FP8_E4M3, 64, 8),
+                        (ekv_hip.BF16, ekv_hip.FP8_E4M3, 32, 16), (ekv_hip.BF16, ekv_hip.FP8_E4M3, 32, 8),
+                        (ekv_hip.BF16, ekv_hip.BF16, 32, 8)):
+        assert lib.ekv_audit_shape(q, k, d, bs) & ekv_hip.AUDIT_PLANNED, (q, k, d, bs)
+    assert lib.ekv_audit_shape(ekv_hip.F16, ekv_hip.BF16, 128, 16) == 0  # mixed 16-bit types
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.BF16, 96, 16) == 0  # rows of 192 bytes
+    assert lib.ekv_audit_shape(ekv_hip.BF16, ekv_hip.BF16, 128, 12) == 0  # tiles of 24 tokens
