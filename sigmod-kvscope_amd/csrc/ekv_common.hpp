@@ -146,16 +146,30 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
   return v;
 }
 
+// A workgroup barrier that orders LDS only: the wave's LDS requests complete, then every wave meets.
+// __syncthreads() also orders global memory, so each wave first waits for every load it has in flight;
+// a kernel whose waves share data only through LDS uses this one, and loads it issued ahead of their
+// use (a table run wanted at the end) stay in flight across the barrier.  The memory clobber keeps the
+// compiler from moving any memory access across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <bool LDS_ONLY>
+__device__ __forceinline__ void workgroup_barrier() {
+  if constexpr (LDS_ONLY) lds_barrier();
+  else __syncthreads();
+}
+
 // Exclusive scan across a workgroup of NT threads; `total` receives the sum.
-// `scratch` must hold NT / 64 ints of LDS.  Contains barriers: every thread must call it.
-template <int NT>
+// `scratch` must hold NT / 64 ints of LDS.  Contains barriers (LDS-only ones with LDS_ONLY): every
+// thread must call it.
+template <int NT, bool LDS_ONLY = false>
 __device__ __forceinline__ int block_exclusive_scan(int v, int *scratch, int &total) {
   constexpr int kWaves = NT / kWave;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   int inc = wave_inclusive_scan(v);
   if (lane == kWave - 1) scratch[wave] = inc;
-  __syncthreads();
+  workgroup_barrier<LDS_ONLY>();
   int base = 0, sum = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -163,7 +177,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int *scratch, int &to
     base += (w < wave) ? s : 0;
     sum += s;
   }
-  __syncthreads();
+  workgroup_barrier<LDS_ONLY>();
   total = sum;
   return base + inc - v;
 }

@@ -195,6 +195,43 @@ __device__ __forceinline__ void block_sums(long long (&v)[N], long long (*scratc
   __syncthreads();
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte loads of one row through a buffer descriptor whose extent is the row's first `entries`
+// 4-byte words: a group at or past the extent reads as zeros (the memory unit's range check), so
+// every load is issued without a per-thread branch, and none can reach past the row.  The caller
+// keeps the extent a multiple of 4 words from a 16-byte aligned base, so that no group straddles it.
+// A negative `first` is a group outside the extent too (its offset is set past any extent): it reads
+// zeros, and a store there writes nothing.
+struct RowLoader {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ RowLoader(const void *base, int entries)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, entries * 4, kRawBufferFormat)) {}
+  static __device__ __forceinline__ int offset(int first) { return first >= 0 ? first * 4 : kPastExtent; }
+  __device__ __forceinline__ u32x4 load(int first) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset(first), 0, 0);
+  }
+  __device__ __forceinline__ void store(int first, u32x4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, offset(first), 0, 0);
+  }
+  // 32-bit data format, the word selects left at zero (the format word of a raw gfx9 buffer)
+  static constexpr int kRawBufferFormat = 0x00020000;
+  static constexpr int kPastExtent = INT_MIN;  // 2^31 as the unsigned offset: past every extent
+};
+
+// The view row's tail.  compact_block_table keeps no block at or past the row's block count nv
+// (block_view.py:49-51) and orders the row stably, kept first: every kept block lies below nv, so each
+// block from nv on stays at its own index.  From the first whole 16-byte group at or past nv (the
+// value returned) the view row is the table row; the width when the rows are not whole 16-byte groups.
+__device__ __forceinline__ int view_tail_from(const Params &p, int row, int L) {
+  const int W = p.width;
+  const uintptr_t trow = (uintptr_t)(p.table + (int64_t)row * p.table_stride);
+  const uintptr_t vrow = (uintptr_t)(p.view_table + (int64_t)row * p.view_stride);
+  const long long n64 = L > 0 ? ((long long)L + p.block_size - 1) / p.block_size : 0;  // block_view.py:49
+  const bool whole_groups = (W & 3) == 0 && ((trow | vrow) & 15) == 0;
+  return whole_groups ? (int)min((n64 + 3) & ~3LL, (long long)W) : W;
+}
+
 // compact_block_table (runtime/block_view.py:36-56) of the row on the keep bytes in LDS, which the
 // ranking has just decided: keep'[b] = (keep[b] | b == 0 | b == n-1) & b < n for n = ceil(L / bs)
 // from the row's token length; the row's entries stably partitioned, keep' first, then the rest,
@@ -202,20 +239,24 @@ __device__ __forceinline__ void block_sums(long long (&v)[N], long long (*scratc
 // table loads), one block scan of the threads' kept counts places every entry, the row is assembled
 // in LDS and written with 16-byte stores.  (Loading the run at the kernel's entry, beside the
 // scores, was slower: 49 against 46 us at 1024 rows x 8192 blocks.)
+// With 16-byte loads (width a multiple of 4, the row aligned) only the groups below `extent` (a
+// multiple of 4, at most the width) are read; the rest of the run reads as zeros.
 template <int PER>
-__device__ __forceinline__ void load_run(const Params &p, int row, int32_t (&entry)[PER]) {
+__device__ __forceinline__ void load_run(const Params &p, int row, int32_t (&entry)[PER], int extent) {
   static_assert(PER % 4 == 0, "runs of whole 16-byte groups");
   const int W = p.width;
   const int32_t *trow = p.table + (int64_t)row * p.table_stride;
   const int b0 = threadIdx.x * PER;
-  if (b0 + PER <= W && ((uintptr_t)(trow + b0) & 15) == 0) {
+  if ((W & 3) == 0 && ((uintptr_t)trow & 15) == 0) {
+    // one test for the whole workgroup; the groups past the extent read as zeros
+    const RowLoader rl(trow, extent);
 #pragma unroll
     for (int g = 0; g < PER / 4; ++g) {
-      const int4 t4 = *reinterpret_cast<const int4 *>(trow + b0 + 4 * g);
-      entry[4 * g] = t4.x;
-      entry[4 * g + 1] = t4.y;
-      entry[4 * g + 2] = t4.z;
-      entry[4 * g + 3] = t4.w;
+      const u32x4 t4 = rl.load(b0 + 4 * g);
+      entry[4 * g] = (int32_t)t4.x;
+      entry[4 * g + 1] = (int32_t)t4.y;
+      entry[4 * g + 2] = (int32_t)t4.z;
+      entry[4 * g + 3] = (int32_t)t4.w;
     }
   } else {
 #pragma unroll
@@ -393,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
     }
     if constexpr (VIEW) {
       int32_t entry[kPer];
-      load_run<kPer>(p, row, entry);
+      load_run<kPer>(p, row, entry, p.width);
       __syncthreads();
       view_row<kPer>(p, row, view_len_in, c_in, entry, s_keep, s_out, s_scan);
     }
@@ -582,7 +623,7 @@ __global__ __launch_bounds__(kThreads) void rank_kernel(const Params p) {
   }
   if constexpr (VIEW) {
     int32_t entry[kPer];
-    load_run<kPer>(p, row, entry);
+    load_run<kPer>(p, row, entry, p.width);
     __syncthreads();
     view_row<kPer>(p, row, view_len_in, c_in, entry, s_keep, s_out, s_scan);
   }
@@ -606,11 +647,13 @@ template <int PER>
 __device__ __forceinline__ void load_scores_run(const Params &p, int row, int n, uint32_t (&key)[PER]) {
   const float *srow = p.scores + (int64_t)row * p.scores_stride;
   const int b0 = threadIdx.x * PER;
-  if (b0 + PER <= p.width && ((uintptr_t)(srow + b0) & 15) == 0) {
+  if ((p.width & 3) == 0 && ((uintptr_t)srow & 15) == 0) {
+    // one test for the whole workgroup; the extent is the live blocks rounded up to a whole group
+    // (at most the width), the groups past it read as zeros
+    const RowLoader rl(srow, min((n + 3) & ~3, p.width));
 #pragma unroll
     for (int g = 0; g < PER / 4; ++g) {
-      // a group past the row reads the row's first group instead (in range, no branch to wait in)
-      const uint4 v = *reinterpret_cast<const uint4 *>(srow + (b0 + 4 * g < n ? b0 + 4 * g : 0));
+      const u32x4 v = rl.load(b0 + 4 * g);
       key[4 * g] = v.x;
       key[4 * g + 1] = v.y;
       key[4 * g + 2] = v.z;
@@ -626,7 +669,7 @@ __device__ __forceinline__ void load_scores_run(const Params &p, int row, int n,
 }
 
 // Sum of N values over a workgroup of NT threads in one pass (every thread receives the sums).
-template <int NT, int N, class T>
+template <int NT, int N, class T, bool LDS_ONLY = false>
 __device__ __forceinline__ void block_sums_n(T (&v)[N], T (*scratch)[NT / kWave]) {
   constexpr int NW = NT / kWave;
   const int wave = threadIdx.x / kWave;
@@ -636,7 +679,7 @@ __device__ __forceinline__ void block_sums_n(T (&v)[N], T (*scratch)[NT / kWave]
     else v[j] = wave_sum_i64(v[j]);
     if (lane_id() == 0) scratch[j][wave] = v[j];
   }
-  __syncthreads();
+  workgroup_barrier<LDS_ONLY>();
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     T s = 0;
@@ -644,7 +687,7 @@ __device__ __forceinline__ void block_sums_n(T (&v)[N], T (*scratch)[NT / kWave]
     for (int w = 0; w < NW; ++w) s += scratch[j][w];
     v[j] = s;
   }
-  __syncthreads();
+  workgroup_barrier<LDS_ONLY>();
 }
 
 // bits [0, k) of a word (k clipped to [0, 32]), and bits [lo, hi)
@@ -734,10 +777,11 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
       }
     }
   }
-  // the table run, requested once the raw scores are no longer needed (with both held the run
-  // would not fit the registers); it arrives while the select runs
+  // the table run, requested once the raw scores are no longer needed (with both held, from the
+  // kernel's entry on, the registers spill); the barriers up to the view row's assembly order LDS
+  // only, so it streams in while the select runs
   int32_t entry[PER];
-  load_run<PER>(p, row, entry);
+  load_run<PER>(p, row, entry, W);
   if (decide) {
     uint32_t open_keep = 0;
     if (quota >= open_count) {
@@ -765,11 +809,15 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
               if (kk[j] != 0u && (kk[j] & mask) == prefix) atomicAdd(&s_hist[((kk[j] >> shift) & 255) * 4 + copy], 1);
           }
         }
-        __syncthreads();
+        lds_barrier();
         if (wave == 0) {
           // lane l holds digits 255 - 4l .. 252 - 4l, the four bins' copies 64 contiguous bytes
-          // from one address; a scan over the lanes counts the keys above
-          int4 *h = reinterpret_cast<int4 *>(&s_hist[4 * (252 - 4 * lane)]);
+          // from one address; a scan over the lanes counts the keys above.  (The lane's digits are
+          // derived in each pass, not held across the select: the empty asm keeps them from being
+          // hoisted out of the loop into registers the table run needs.)
+          int l = lane;
+          asm volatile("" : "+v"(l));
+          int4 *h = reinterpret_cast<int4 *>(&s_hist[4 * (252 - 4 * l)]);
           int c[4], s4 = 0;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {  // digit 255 - 4l - j
@@ -784,7 +832,7 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               if (acc < k_rem && acc + c[j] >= k_rem) {
-                s_sel[0] = 255 - 4 * lane - j;
+                s_sel[0] = 255 - 4 * l - j;
                 s_sel[1] = k_rem - acc;
                 s_sel[2] = acc + c[j] == k_rem ? 1 : 0;
               }
@@ -794,7 +842,7 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
 #pragma unroll
           for (int j = 0; j < 4; ++j) h[j] = make_int4(0, 0, 0, 0);  // cleared for the next pass
         }
-        __syncthreads();
+        lds_barrier();
         prefix |= (uint32_t)s_sel[0] << shift;
         mask |= 255u << shift;
         k_rem = s_sel[1];
@@ -823,7 +871,7 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
           }
         }
         int eq_total;
-        int before = block_exclusive_scan<kThreads>(__popc(eq_bits), s_scan, eq_total);
+        int before = block_exclusive_scan<kThreads, true>(__popc(eq_bits), s_scan, eq_total);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
           const bool eq = (eq_bits >> i) & 1u;
@@ -834,6 +882,24 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
       }
     }
     keep_bits = ~open_bits | open_keep;  // past the row, pinned: 1; open: decided
+  }
+  // The view row's tail (view_tail_from) is the table row: the thread's groups there go from its
+  // registers to the view row, in place; its other groups are assembled in LDS below.  (Stored before
+  // the keep bytes, whose stores a wait for the run's loads would wait for as well.  The tail's
+  // start and the rows' addresses are recomputed rather than held across the select, whose registers
+  // are all taken: the empty asm hides that the values are the same.)
+  L = __builtin_amdgcn_readfirstlane(L);  // both uniform; in scalar registers for the asm
+  row = __builtin_amdgcn_readfirstlane(row);
+  asm volatile("" : "+s"(L), "+s"(row));
+  const int tail_from = view_tail_from(p, row, L);
+  {
+    const RowLoader tail(p.view_table + (int64_t)row * p.view_stride + tail_from, W - tail_from);
+#pragma unroll
+    for (int g = 0; g < PER / 4; ++g) {
+      const u32x4 v = {(uint32_t)entry[4 * g], (uint32_t)entry[4 * g + 1], (uint32_t)entry[4 * g + 2],
+                       (uint32_t)entry[4 * g + 3]};
+      tail.store(b0 + 4 * g - tail_from, v);  // below the tail: a negative index, no store
+    }
   }
   uint8_t *keep_row = p.keep + (int64_t)row * p.keep_stride;
   if (b0 + PER <= W && ((uintptr_t)(keep_row + b0) & 3) == 0) {
@@ -850,9 +916,10 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
     for (int i = 0; i < PER; ++i)
       if (i < in_row) run[i] = (keep_bits >> i) & 1u;
   }
-  __syncthreads();  // every key is read before the view row overwrites them
+  lds_barrier();  // every key is read before the view row overwrites them
 
-  // ---- compact_block_table (runtime/block_view.py:36-56) of the row on that keep ------------
+  // ---- compact_block_table (runtime/block_view.py:36-56) of the row on that keep, blocks below
+  // tail_from (the tail is stored above) ---------------------------------------------------------
   int32_t *s_out = reinterpret_cast<int32_t *>(s_row);
   const int bs = p.block_size;
   const long long n64 = L > 0 ? ((long long)L + bs - 1) / bs : 0;  // block_view.py:49
@@ -862,28 +929,28 @@ __device__ __forceinline__ void keep_and_view(const Params &p, int row, const Ro
   const uint32_t kept_bits = (keep_bits | (b0 == 0 ? 1u : 0u) | (last_at >= 0 && last_at < PER ? 1u << last_at : 0u)) &
                              bits_below(min(min(nv, W) - b0, PER));
   int total_kept;
-  int before = block_exclusive_scan<kThreads>(__popc(kept_bits), s_scan, total_kept);
+  int before = block_exclusive_scan<kThreads, true>(__popc(kept_bits), s_scan, total_kept);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     // kept: at its rank among the kept; dropped: after the kept ones, in order (one store either way)
     const int b = b0 + i;
     const bool kept = (kept_bits >> i) & 1u;
-    if (b < W) s_out[kept ? before : total_kept + (b - before)] = entry[i];
+    if (b < tail_from) s_out[kept ? before : total_kept + (b - before)] = entry[i];
     before += kept ? 1 : 0;
   }
-  __syncthreads();
+  lds_barrier();
   int32_t *vrow = p.view_table + (int64_t)row * p.view_stride;
   if (((uintptr_t)vrow & 15) == 0) {
-    for (int q = tid; 4 * q < W; q += kThreads) {
-      if (4 * q + 3 < W) {
+    for (int q = tid; 4 * q < tail_from; q += kThreads) {
+      if (4 * q + 3 < tail_from) {
         *reinterpret_cast<int4 *>(vrow + 4 * q) =
             make_int4(s_out[4 * q], s_out[4 * q + 1], s_out[4 * q + 2], s_out[4 * q + 3]);
       } else {
-        for (int b = 4 * q; b < W; ++b) vrow[b] = s_out[b];
+        for (int b = 4 * q; b < tail_from; ++b) vrow[b] = s_out[b];
       }
     }
   } else {
-    for (int b = tid; b < W; b += kThreads) vrow[b] = s_out[b];
+    for (int b = tid; b < tail_from; b += kThreads) vrow[b] = s_out[b];
   }
   if (tid == 0) {  // block_view.py:53-55
     const int last = L - (int)(n64 - 1) * bs;
@@ -915,7 +982,7 @@ __device__ __forceinline__ void quota_reduce(int (&v)[N], int (*scratch)[kWaves]
 #pragma unroll
     for (int j = 0; j < N; ++j) scratch[j][wave] = v[j];
   }
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int j = 0; j < N; ++j) {
     int r = j < NS ? 0 : ((j - NS) % 2 == 0 ? 0 : INT_MIN);
@@ -928,7 +995,7 @@ __device__ __forceinline__ void quota_reduce(int (&v)[N], int (*scratch)[kWaves]
     }
     v[j] = r;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // The uniform ranking and the view in one kernel, one row per workgroup (four per compute unit, 64
@@ -956,15 +1023,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
 
   // ---- the row's counts and token length, every row's counts for the budget, then the row's
   // live scores ---------------------------------------------------------------------------------
-  const RowInfo me = row_info(p, row);
-  const int L = p.seq_lens[row];
-  // the counts of rows tid and tid + kThreads, then the row's scores: every load in flight at once
-  // (a load behind a null test of its array would be waited for before the next is issued)
-  constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
   // Every load is unconditional (an absent array is read through the block counts, in range, and
-  // ignored), so none waits inside a branch.
+  // ignored), so none waits inside a branch: the row's own four values, the counts of rows tid and
+  // tid + kThreads, then (once the row's block count is in) the row's scores, all in flight at once.
   const uint8_t *measured = p.measured != nullptr ? p.measured : reinterpret_cast<const uint8_t *>(p.blocks);
   const int32_t *pin_from = p.pin_from != nullptr ? p.pin_from : p.blocks;
+  const int my_blocks = p.blocks[row];
+  const int my_measured = measured[row];
+  const int my_pin_from = pin_from[row];
+  const int L = p.seq_lens[row];
+  const RowInfo me = row_info_of(p, my_blocks, p.measured == nullptr || my_measured != 0,
+                                 p.pin_from != nullptr ? my_pin_from : INT_MAX);
+  constexpr int kRegRows = 2;  // rows per thread whose open count stays in a register
   int nb[kRegRows], pf[kRegRows], ms[kRegRows];
 #pragma unroll
   for (int i = 0; i < kRegRows; ++i) {
@@ -1001,7 +1071,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))
     t5[3] += ri.exist - ri.pinned;
     t5[4] += 1;
   }
-  block_sums_n<kThreads>(t5, s_red);
+  block_sums_n<kThreads, 5, int, true>(t5, s_red);
   Budget bg;
   bg.total = t5[0];
   bg.floor_pins = t5[1];

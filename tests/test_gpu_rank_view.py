@@ -183,3 +183,47 @@ def test_more_rows_than_workgroups_fit_at_once(rows, width):
         keep, summary, view, view_lens = both(dev["scores"], dev["blocks"], dev["table"], dev["lens"], bs, **kw)
         want_view, want_lens = obv.compact(table, lens, keep.astype(bool), bs)
         assert np.array_equal(view, want_view) and np.array_equal(view_lens, want_lens), kw
+
+
+@pytest.mark.parametrize("width,view_pad,table_pad", [(8192, 0, 0), (8192, 1, 0), (8192, 0, 3), (4096, 4, 4),
+                                                      (2048, 0, 0), (2044, 0, 0), (2046, 0, 0)])
+def test_view_tail_in_place(width, view_pad, table_pad):
+    # Blocks from the row's view block count on keep their index in the view (the stable partition puts
+    # every kept block below it).  The kernel stores that tail straight from the table run when the rows
+    # are whole 16-byte groups (width a multiple of 4, table and view rows 16-byte aligned) and builds
+    # the rest in LDS.  Rows end at every residue mod 4; lengths are empty, negative or past the width;
+    # padded row strides misalign the table or the view rows (the whole row then goes through LDS).
+    # Every view entry is checked against the oracle (the buffer starts at a value no table entry
+    # holds), and the padding past the width stays untouched.
+    rng = np.random.default_rng(width + 10 * view_pad + table_pad)
+    rows, bs = 64, 16
+    nv = rng.integers(0, width + 1, size=rows)
+    nv[:12] = [0, 1, 2, 3, 4, 5, 6, 7, width - 1, width, width + 1, width + 5]
+    lens = np.where(nv > 0, (nv - 1) * bs + rng.integers(1, bs + 1, size=rows), 0).astype(np.int64)
+    lens[12], lens[13] = -5, -40  # no tokens: an empty view, the row in place
+    lens = lens.astype(np.int32)
+    blocks = rng.integers(0, width + 1, size=rows).astype(np.int32)
+    blocks[:4] = [0, width, 1, 2]
+    scores = rng.random((rows, width), dtype=np.float32)
+    table_full = rng.integers(0, 1 << 30, size=(rows, width + table_pad)).astype(np.int32)
+    dev_scores = torch.from_numpy(scores).cuda()
+    dev_blocks = torch.from_numpy(blocks).cuda()
+    dev_table = torch.from_numpy(table_full).cuda()
+    dev_lens = torch.from_numpy(lens).cuda()
+    keep = torch.empty(rows, width, dtype=torch.uint8, device="cuda")
+    summary = torch.zeros(6, dtype=torch.int64, device="cuda")
+    view = torch.full((rows, width + view_pad), -7, dtype=torch.int32, device="cuda")
+    view_lens = torch.empty(rows, dtype=torch.int32, device="cuda")
+    print(f"width {width}, view stride {width + view_pad}, table stride {width + table_pad}", flush=True)
+    ekv_hip.call("ekv_rank_uniform_view", dev_scores.data_ptr(), width, dev_blocks.data_ptr(), 0, 0, 0, rows, width,
+                 0.5, -1, keep.data_ptr(), width, summary.data_ptr(), dev_table.data_ptr(), width + table_pad,
+                 dev_lens.data_ptr(), bs, view.data_ptr(), width + view_pad, view_lens.data_ptr(), 0,
+                 ekv_hip.stream_handle())
+    want_keep, _ = uniform_keep(dev_scores, dev_blocks, fraction=0.5)
+    got_keep = keep.cpu().numpy()
+    assert np.array_equal(got_keep, want_keep.cpu().numpy())
+    want_view, want_lens = obv.compact(table_full[:, :width], lens, got_keep.astype(bool), bs)
+    got_view = view.cpu().numpy()
+    assert np.array_equal(got_view[:, :width], want_view)
+    assert (got_view[:, width:] == -7).all()
+    assert np.array_equal(view_lens.cpu().numpy(), want_lens)
