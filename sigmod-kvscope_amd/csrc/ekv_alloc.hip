@@ -37,7 +37,6 @@
 
 #include <algorithm>
 
-#include <rocprim/block/block_radix_sort.hpp>
 #include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "ekv_common.hpp"
@@ -511,89 +510,224 @@ __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
   }
 }
 
-// per request, one workgroup:
-// 1. the sort keys of its n blocks, the pinned ones keyed 0;
-// 2. a block radix sort of them in LDS, stable and descending, so equal keys (such as the pinned
-//    blocks' 0) keep block order and the padding keys 0 past n sort after every block;
-// 3. the sorted block indices, and the open blocks' shares in sorted order (for the totals).
-// The keys per thread (ITEMS) are the fewest that hold the request's n blocks, so a short request
-// sorts only its own length.
+// per request, one workgroup: its n blocks in stable descending order of their gain keys (the
+// pinned blocks keyed 0, after every open block, in block order), written as the sorted block
+// indices (vals_out) and the open blocks' shares in that order (prefix, for the totals).
+//
+// The sort is a least-significant-digit radix sort in LDS, 8 bits a pass, over elements that pack
+// a block's key bits 24-63 above its index (bits 0-13), so that one 64-bit word moves per block:
+// shares computed from float32 scores that differ, differ in those bits (by at least 2^28 in their
+// float64 bits).  The padding past n (key 0, index n and up) sorts after every block.  Where two
+// neighbours agree in those bits and the later one's bits 0-23 are larger, every run of equal top
+// bits is sorted again on (bits 0-23 descending, index ascending).
+//
+// A pass: each of the 16 waves owns a run of 64 * ITEMS consecutive positions and ranks it 64
+// positions (one per lane) at a time.  The lanes that share a digit are found from eight ballots of
+// its bits; a lane's rank in its wave is the wave's count of its digit so far (in LDS) plus the lanes
+// before it that share the digit, and those lanes store the count raised by their number.  The waves' counts, scanned digit by digit (descending) then wave by wave,
+// give each digit's first position for each wave, and every element moves to its place.  Equal digits
+// keep their order, so the passes compose into a stable sort.
 constexpr int kSortThreads = 1024;
-
-template <int ITEMS>
-using RequestSort = rocprim::block_radix_sort<unsigned long long, kSortThreads, ITEMS, int>;
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int kDigitBins = 256;
+constexpr int kIndexBits = 14;    // block indices below 2^14
 constexpr int kSortLowBits = 24;  // the key bits the first sort leaves out
+static_assert(kMaxWidth <= (1 << kIndexBits), "a block index fits the packed element");
+static_assert(kSortThreads == 4 * kDigitBins, "the count scan takes four counts of one digit a thread");
 
+template <int MAX_ITEMS>
+struct SortLds {
+  unsigned long long elem[MAX_ITEMS * kSortThreads];
+  unsigned int count[kSortWaves][kDigitBins];  // per wave and digit; scratch between the passes
+};
+
+// One pass over bits [lo, lo + 8) of the ITEMS * kSortThreads elements in `elem`.
 template <int ITEMS>
-__device__ __forceinline__ void sort_request(const MaxminParams &m, const RowStat &st, int r,
-                                             typename RequestSort<ITEMS>::storage_type &storage) {
-  const Params &p = m.p;
-  const int n = st.n, open = st.open;
-  const double *srow = p.scores + (int64_t)r * p.scores_stride;
-  const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
-  unsigned long long keys[ITEMS];
-  int vals[ITEMS];
-  double score[ITEMS];
-  uint8_t pin[ITEMS];
+__device__ __forceinline__ void radix_pass(unsigned long long *elem, unsigned int (*count)[kDigitBins], int lo) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int run0 = wave * kWave * ITEMS;
+  unsigned long long e[ITEMS];
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {  // every load issued before any is used
-    const int pos = threadIdx.x * ITEMS + i;
-    score[i] = pos < n ? srow[pos] : 0.0;
-    pin[i] = (prow != nullptr && pos < n) ? prow[pos] : 0;
-  }
+  for (int i = 0; i < ITEMS; ++i) e[i] = elem[run0 + i * kWave + lane];
+  unsigned int *cnt = count[wave];
+  // cleared before this wave's atomics below: one wave's LDS accesses take effect in order
+#pragma unroll
+  for (int j = 0; j < kDigitBins / kWave; ++j) cnt[j * kWave + lane] = 0u;
+  uint32_t info[ITEMS];  // the digit (bits 16-23, descending as ascending) and the rank in the wave
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    const int pos = threadIdx.x * ITEMS + i;
-    const bool pinned = prow != nullptr ? pin[i] != 0 : (pos == 0 || pos == n - 1);
-    keys[i] = (pos < n && !pinned) ? gain_key(share_value(st, score[i])) : 0ull;
-    vals[i] = pos;
+    const uint32_t d = 255u - (uint32_t)((e[i] >> lo) & 255u);
+    // the lanes whose digit is d, as two 32-bit halves: for each bit, the ballot of the lanes that
+    // have it, or its complement where d lacks it (f is all ones there)
+    uint32_t peer_lo = ~0u, peer_hi = ~0u;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint64_t set = __ballot((d >> b) & 1u);
+      const uint32_t f = (uint32_t)__builtin_amdgcn_sbfe((int)~d, b, 1);
+      peer_lo = __builtin_amdgcn_bitop3_b32(peer_lo, (uint32_t)set, f, 0x60);  // peer & (set ^ f)
+      peer_hi = __builtin_amdgcn_bitop3_b32(peer_hi, (uint32_t)(set >> 32), f, 0x60);
+    }
+    // the wave's count of d so far, then every lane with d stores the same new count (no lane
+    // diverges; this wave's LDS accesses take effect in order, so the next position reads it)
+    const uint32_t before = cnt[d];
+    cnt[d] = before + (uint32_t)(__popc(peer_lo) + __popc(peer_hi));
+    info[i] = (d << 16) | (before + __builtin_amdgcn_mbcnt_hi(peer_hi, __builtin_amdgcn_mbcnt_lo(peer_lo, 0u)));
+    // computed here: left to the compiler, the rank's parts (two masks and a count) would be carried
+    // to the moves after the scan instead of this one word
+    asm volatile("" : "+v"(info[i]));
   }
-  // Bits 24-63 first, five passes: shares computed from float32 scores that differ, differ there (by
-  // at least 2^28 in their float64 bits).  The sort is stable, so the order is final unless two
-  // neighbours agree there and the later one's bits 0-23 are larger; then the request is sorted
-  // again on all 64 bits, from that order (which keeps equal keys in block order).
-  __shared__ int s_resort;
-  if (threadIdx.x == 0) s_resort = 0;
-  RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage, kSortLowBits, 64);
-  __syncthreads();  // the sort's storage is free; s_resort is 0
-  unsigned long long *s_keys = reinterpret_cast<unsigned long long *>(&storage);
-  static_assert(sizeof(typename RequestSort<ITEMS>::storage_type) >= sizeof(unsigned long long) * ITEMS * kSortThreads,
-                "the sorted keys fit the sort's storage");
+  __syncthreads();  // every wave's counts are final and every element is in registers
+  {
+    // the counts in (digit, wave) order: thread t takes digit t / 4 and waves 4 (t % 4) .. + 3; the
+    // scan's scratch is the element array, free until the elements move
+    const int d = threadIdx.x >> 2, w0 = (threadIdx.x & 3) * 4;
+    uint32_t c[4];
+    int sum = 0;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) s_keys[i * kSortThreads + threadIdx.x] = keys[i];
-  __syncthreads();
-  bool unsorted = false;
+    for (int q = 0; q < 4; ++q) {
+      c[q] = count[w0 + q][d];
+      sum += (int)c[q];
+    }
+    int total;
+    int at = block_exclusive_scan<kSortThreads>(sum, reinterpret_cast<int *>(elem), total);
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int pos = i * kSortThreads + threadIdx.x;
-    if (pos > 0 && pos < n) {
-      const unsigned long long prev = s_keys[pos - 1], k = keys[i];
-      constexpr unsigned long long kLow = (1ull << kSortLowBits) - 1ull;
-      unsorted |= (k >> kSortLowBits) == (prev >> kSortLowBits) && (k & kLow) > (prev & kLow);
+    for (int q = 0; q < 4; ++q) {
+      count[w0 + q][d] = (uint32_t)at;
+      at += (int)c[q];
     }
   }
-  if (unsorted) s_resort = 1;
   __syncthreads();
-  if (s_resort) {
-    // the keys and block indices back to their sorted order per thread (blocked), then all 64 bits
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) keys[i] = s_keys[threadIdx.x * ITEMS + i];
-    __syncthreads();
-    int *s_vals = reinterpret_cast<int *>(&storage);
+  for (int i = 0; i < ITEMS; ++i) elem[count[wave][info[i] >> 16] + (info[i] & 0xffffu)] = e[i];
+  __syncthreads();
+}
+
+// the sort key of block b of a request from its score and pinned flag (0: pinned, or past its blocks)
+__device__ __forceinline__ unsigned long long block_key(const RowStat &st, bool masked, int b, double score,
+                                                        uint8_t pin) {
+  const bool pinned = masked ? pin != 0 : (b == 0 || b == st.n - 1);
+  const unsigned long long k = gain_key(share_value(st, score));
+  return (b >= st.n || pinned) ? 0ull : k;
+}
+
+template <int ITEMS, int MAX_ITEMS>
+__device__ __forceinline__ void sort_request(const MaxminParams &m, const RowStat &st, int r, SortLds<MAX_ITEMS> &lds) {
+  static_assert(ITEMS <= MAX_ITEMS, "the LDS holds the sort");
+  constexpr unsigned long long kIndexMask = (1ull << kIndexBits) - 1ull;
+  constexpr unsigned long long kLow = (1ull << kSortLowBits) - 1ull;
+  const Params &p = m.p;
+  const int n = st.n, open = st.open;
+  const int tid = threadIdx.x;
+  const double *srow = p.scores + (int64_t)r * p.scores_stride;
+  // Every load is unconditional and in range (indices clamped to the request's last block; without an
+  // explicit mask the pinned flags are read from the scores and ignored), so none waits in a branch.
+  const bool masked = p.pinned != nullptr;
+  const uint8_t *prow = masked ? p.pinned + (int64_t)r * p.pinned_stride : reinterpret_cast<const uint8_t *>(srow);
+  unsigned long long *elem = lds.elem;
+  constexpr int kStep = ITEMS < 4 ? ITEMS : 4;  // positions loaded at a time
+  // the full keys of the blocks that elements name, from their scores (in cache: just read), kStep
+  // at a time with every load issued before any is used
+  auto keys_of = [&](const int (&b)[ITEMS], unsigned long long (&k)[ITEMS]) {
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) s_vals[i * kSortThreads + threadIdx.x] = vals[i];
-    __syncthreads();
+    for (int i0 = 0; i0 < ITEMS; i0 += kStep) {
+      double sc[kStep];
+      uint8_t pn[kStep];
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) vals[i] = s_vals[threadIdx.x * ITEMS + i];
-    __syncthreads();
-    RequestSort<ITEMS>().sort_desc_to_striped(keys, vals, storage);
+      for (int i = 0; i < kStep; ++i) {
+        const int c = min(b[i0 + i], n - 1);
+        sc[i] = srow[c];
+        pn[i] = prow[c];
+      }
+#pragma unroll
+      for (int i = 0; i < kStep; ++i) k[i0 + i] = block_key(st, masked, b[i0 + i], sc[i], pn[i]);
+    }
+  };
+#pragma unroll
+  for (int i0 = 0; i0 < ITEMS; i0 += kStep) {
+    double score[kStep];
+    uint8_t pin[kStep];
+#pragma unroll
+    for (int i = 0; i < kStep; ++i) {  // every load issued before any is used
+      const int c = min((i0 + i) * kSortThreads + tid, n - 1);
+      score[i] = srow[c];
+      pin[i] = prow[c];
+    }
+#pragma unroll
+    for (int i = 0; i < kStep; ++i) {
+      const int pos = (i0 + i) * kSortThreads + tid;
+      const unsigned long long k = block_key(st, masked, pos, score[i], pin[i]);
+      elem[pos] = ((k >> kSortLowBits) << kIndexBits) | (unsigned long long)pos;
+    }
   }
-  const int64_t row0 = (int64_t)r * p.width;
+  __syncthreads();
+#pragma unroll 1
+  for (int lo = kIndexBits; lo < kIndexBits + 64 - kSortLowBits; lo += 8) radix_pass<ITEMS>(elem, lds.count, lo);
+
+  // Neighbours that tie in the top bits: each thread takes ITEMS consecutive positions (so that a
+  // scan over the threads numbers the runs of equal top bits in order) and the full keys of their blocks.
+  // (The thread index passes through an empty asm before each phase that derives addresses from it:
+  // otherwise the compiler computes every phase's addresses up front and holds them across the sort.)
+  int t = tid;
+  asm volatile("" : "+v"(t));
+  unsigned long long key[ITEMS];
+  int idx[ITEMS];
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {  // striped: position i * kSortThreads + thread
-    const int pos = i * kSortThreads + threadIdx.x;
-    if (pos < n) m.vals_out[row0 + pos] = vals[i];
-    if (pos < open) m.prefix[row0 + pos] = key_value(keys[i]);
+  for (int i = 0; i < ITEMS; ++i) idx[i] = (int)(elem[t * ITEMS + i] & kIndexMask);
+  keys_of(idx, key);
+  unsigned long long *last_key = reinterpret_cast<unsigned long long *>(&lds.count[0][0]);  // [kSortThreads]
+  unsigned int *resort = &lds.count[kSortWaves - 1][kDigitBins - 1];  // past last_key
+  static_assert(sizeof(unsigned long long) * kSortThreads < sizeof(lds.count), "the flag lies past last_key");
+  last_key[t] = key[ITEMS - 1];
+  if (t == 0) *resort = 0u;
+  __syncthreads();
+  const unsigned long long before = t > 0 ? last_key[t - 1] : 0ull;
+  {
+    bool unsorted = false;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int pos = t * ITEMS + i;
+      const unsigned long long prev = i > 0 ? key[i - 1] : before;
+      unsorted |= pos > 0 && pos < n && (key[i] >> kSortLowBits) == (prev >> kSortLowBits) && (key[i] & kLow) > (prev & kLow);
+    }
+    if (unsorted) *resort = 1u;
+  }
+  __syncthreads();
+  if (*resort != 0u) {
+    // each run of equal top bits again, on (bits 0-23, index): runs numbered in order by a scan of
+    // their first positions, elements packed as (~run, bits 0-23, index) and sorted on bits 14-51
+    // from the present order, which holds a run's blocks in block order
+    int starts = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const unsigned long long prev = i > 0 ? key[i - 1] : before;
+      starts += (t * ITEMS + i == 0 || (key[i] >> kSortLowBits) != (prev >> kSortLowBits)) ? 1 : 0;
+    }
+    int total_runs;
+    int run = block_exclusive_scan<kSortThreads>(starts, reinterpret_cast<int *>(elem), total_runs) - 1;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const unsigned long long prev = i > 0 ? key[i - 1] : before;
+      run += (t * ITEMS + i == 0 || (key[i] >> kSortLowBits) != (prev >> kSortLowBits)) ? 1 : 0;
+      elem[t * ITEMS + i] = ((~(unsigned long long)run & kIndexMask) << (kIndexBits + kSortLowBits)) |
+                              ((key[i] & kLow) << kIndexBits) | (unsigned long long)idx[i];
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int lo = kIndexBits; lo < 2 * kIndexBits + kSortLowBits; lo += 8) radix_pass<ITEMS>(elem, lds.count, lo);
+  }
+  // the outputs, striped (coalesced stores): position i * kSortThreads + thread
+  const int64_t row0 = (int64_t)r * p.width;
+  t = tid;
+  asm volatile("" : "+v"(t));
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) idx[i] = (int)(elem[i * kSortThreads + t] & kIndexMask);
+  keys_of(idx, key);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int pos = i * kSortThreads + t;
+    if (pos < n) m.vals_out[row0 + pos] = idx[i];
+    if (pos < open) m.prefix[row0 + pos] = key_value(key[i]);
   }
 }
 
@@ -627,36 +761,25 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[cls(r)], 1)] = r;
 }
 
-// At most 64 VGPRs (8 waves per SIMD), so that two 16-wave sorting workgroups share a CU where their
-// LDS allows it (sorts of up to 8192 keys take 64 KB): at 82 VGPRs one held the CU alone.  The
-// 12-key sort's 96 KB of LDS keeps it alone on a CU whatever its registers.
+// Two 16-wave sorting workgroups share a CU where their LDS allows it (sorts of up to 8192 blocks take
+// 80 KB), at most 64 VGPRs each (8 waves per SIMD); the 12-key sort's 112 KB keeps it alone on a CU.
 template <int MAX_ITEMS>
 __global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(MAX_ITEMS <= 8 ? 8 : 4)))
 void mm_sort_kernel(const MaxminParams m) {
-  using Largest = typename RequestSort<MAX_ITEMS>::storage_type;
-  constexpr int kMid = MAX_ITEMS < 8 ? MAX_ITEMS : 8;
-  static_assert(sizeof(typename RequestSort<1>::storage_type) <= sizeof(Largest) &&
-                    sizeof(typename RequestSort<2>::storage_type) <= sizeof(Largest) &&
-                    sizeof(typename RequestSort<4>::storage_type) <= sizeof(Largest) &&
-                    sizeof(typename RequestSort<kMid>::storage_type) <= sizeof(Largest),
-                "the largest sort's storage holds every smaller one");
-  static_assert(alignof(typename RequestSort<1>::storage_type) <= alignof(Largest) &&
-                    alignof(typename RequestSort<kMid>::storage_type) <= alignof(Largest),
-                "and is aligned for it");
-  __shared__ Largest storage;
+  __shared__ SortLds<MAX_ITEMS> lds;
   const int r = m.order[blockIdx.x];
   const RowStat st = m.p.row_stat[r];
-  auto &raw = storage;
+  if (st.n <= 0) return;
   if (st.n <= kSortThreads)
-    sort_request<1>(m, st, r, reinterpret_cast<typename RequestSort<1>::storage_type &>(raw));
+    sort_request<1>(m, st, r, lds);
   else if (st.n <= 2 * kSortThreads)
-    sort_request<2>(m, st, r, reinterpret_cast<typename RequestSort<2>::storage_type &>(raw));
+    sort_request<2>(m, st, r, lds);
   else if (MAX_ITEMS == 4 || st.n <= 4 * kSortThreads)
-    sort_request<4>(m, st, r, reinterpret_cast<typename RequestSort<4>::storage_type &>(raw));
+    sort_request<MAX_ITEMS < 4 ? MAX_ITEMS : 4>(m, st, r, lds);
   else if (MAX_ITEMS == 8 || st.n <= 8 * kSortThreads)
-    sort_request<kMid>(m, st, r, reinterpret_cast<typename RequestSort<kMid>::storage_type &>(raw));
+    sort_request<MAX_ITEMS < 8 ? MAX_ITEMS : 8>(m, st, r, lds);
   else
-    sort_request<MAX_ITEMS>(m, st, r, raw);
+    sort_request<MAX_ITEMS>(m, st, r, lds);
 }
 
 // Requests wider than a sort in LDS go through a device-wide segmented radix sort (rocPRIM's, stable,
@@ -691,65 +814,118 @@ __global__ __launch_bounds__(kThreads) void mm_wide_unpack_kernel(const MaxminPa
   }
 }
 
-// per request, one wave: the running totals of its sorted open shares (np.cumsum), in place. One
-// float64 chain per request, added by lane 0: the wave stages the shares through LDS a chunk at a
-// time with coalesced loads, the next chunk's loads in flight while lane 0 adds the current chunk
-// from LDS and stores the totals. One wave per request keeps every request's chain in flight at
-// once (one per SIMD at 1024 requests), where a workgroup that also sorted would run one at a time
-// per CU.
-constexpr int kTotalsChunk = 1024;  // values per chunk: 16 per lane
-constexpr int kChainBatch = 16;     // values lane 0 reads from LDS before adding them
+// the running totals of the requests' sorted open shares (np.cumsum), in place, one float64 chain per
+// request added in order.  A dependent float64 add takes ~21 cycles here, so a chain's adds set the
+// time; what else the chain lane issues must fit beside them.  Per-element memory instructions from
+// a single lane do not: with a chain wave on every SIMD they queue in each CU's memory pipeline and
+// double the time.  So one wave runs kChainsPerWave chains, lane q the request order[kChainsPerWave w
+// + q] (the requests longest first, so a wave's chains have about the same length), each lane's loads
+// and stores being those of one instruction for all its chains.  The wave stages a chunk of each
+// request in LDS with coalesced loads (the next chunk's loads in flight meanwhile); a chain lane reads
+// two shares per 16-byte LDS read, a batch ahead of adding them, and stores two totals at a time.
+constexpr int kTotalsChunk = 1024;  // values per chunk and request: 16 per lane
+constexpr int kChainBatch = 16;     // values a chain lane reads from LDS a batch ahead of adding them
+constexpr int kChainsPerWave = 2;
+constexpr int kChunkPad = kTotalsChunk + 2;  // the requests' chunks a bank apart
 
 __global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) {
-  static_assert(kTotalsChunk % kWave == 0 && kTotalsChunk % kChainBatch == 0, "whole batches per chunk");
+  static_assert(kTotalsChunk % kWave == 0 && kTotalsChunk % (2 * kChainBatch) == 0, "whole steps per chunk");
   constexpr int kPer = kTotalsChunk / kWave;
-  __shared__ double s_chunk[kTotalsChunk];
-  const int r = blockIdx.x;
+  constexpr int Q = kChainsPerWave;
+  __shared__ __align__(16) double s_chunk[Q * kChunkPad];
   const int lane = lane_id();
-  const int open = m.p.row_stat[r].open;
-  double *row = m.prefix + (int64_t)r * m.p.width;
-  double v[kPer];
+  int req[Q], open[Q];
+  int longest = 0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = j * kWave + lane;
-    v[j] = i < open ? row[i] : 0.0;
+  for (int q = 0; q < Q; ++q) {
+    const int k = blockIdx.x * Q + q;
+    req[q] = k < m.p.rows ? m.order[k] : -1;
+    open[q] = req[q] >= 0 ? m.p.row_stat[req[q]].open : 0;
+    longest = max(longest, open[q]);
   }
+  const double *row[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) row[q] = m.prefix + (int64_t)max(req[q], 0) * m.p.width;
+  // this lane's chain (lanes below Q): its request's row and length
+  const int my_open = lane < Q ? open[min(lane, Q - 1)] : 0;
+  double *my_row = m.prefix + (int64_t)max(lane < Q ? req[min(lane, Q - 1)] : 0, 0) * m.p.width;
+  double v[Q][kPer];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kWave + lane;
+      v[q][j] = i < open[q] ? row[q][i] : 0.0;
+    }
   // -0.0 + x is x for every x, so the first total is the first share itself, as in np.cumsum
   double acc = -0.0;
-  for (int c0 = 0; c0 < open; c0 += kTotalsChunk) {
+  for (int c0 = 0; c0 < longest; c0 += kTotalsChunk) {
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) s_chunk[j * kWave + lane] = v[j];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int q = 0; q < Q; ++q)
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {  // the next chunk
-      const int i = c0 + kTotalsChunk + j * kWave + lane;
-      v[j] = i < open ? row[i] : 0.0;
-    }
-    if (lane == 0) {
-      const int len = min(open - c0, kTotalsChunk);
-      double *out = row + c0;
-      for (int i0 = 0; i0 < len; i0 += kChainBatch) {
-        double x[kChainBatch];
+      for (int j = 0; j < kPer; ++j) s_chunk[q * kChunkPad + j * kWave + lane] = v[q][j];
+    __syncthreads();
 #pragma unroll
-        for (int k = 0; k < kChainBatch; ++k) x[k] = s_chunk[i0 + k];
+    for (int q = 0; q < Q; ++q)
 #pragma unroll
-        for (int k = 0; k < kChainBatch; ++k) {
-          acc += x[k];
-          x[k] = acc;
+      for (int j = 0; j < kPer; ++j) {  // the next chunk
+        const int i = c0 + kTotalsChunk + j * kWave + lane;
+        v[q][j] = i < open[q] ? row[q][i] : 0.0;
+      }
+    const int steps = min(longest - c0, kTotalsChunk);  // positions every chain lane walks
+    // positions below `whole` are inside every chain of the wave (an absent request, in the last wave,
+    // has none): their totals are stored without a test
+    int shortest = kTotalsChunk;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) shortest = min(shortest, open[q] - c0);
+    const int whole = max(shortest, 0) / (2 * kChainBatch) * (2 * kChainBatch);
+    if (lane < Q) {
+      // past the lane's own length the chain adds zeros (its total stays) and stores nothing
+      const int len = min(my_open - c0, kTotalsChunk);
+      const double2 *pair = reinterpret_cast<const double2 *>(s_chunk + lane * kChunkPad);
+      double2 *out = reinterpret_cast<double2 *>(my_row + c0);
+      constexpr int kPairs = kChainBatch / 2;
+      auto read = [&](double2 (&x)[kPairs], int first) {  // a batch from `first`, or a dummy past the chunk
+        const int at = first < kTotalsChunk ? first / 2 : 0;
+#pragma unroll
+        for (int k = 0; k < kPairs; ++k) x[k] = pair[at + k];
+      };
+      auto add = [&](double2 (&x)[kPairs], int first, bool test) {
+#pragma unroll
+        for (int k = 0; k < kPairs; ++k) {
+          acc += x[k].x;
+          x[k].x = acc;
+          acc += x[k].y;
+          x[k].y = acc;
         }
-        if (i0 + kChainBatch <= len) {
 #pragma unroll
-          for (int k = 0; k < kChainBatch; ++k) out[i0 + k] = x[k];
-        } else {
-#pragma unroll
-          for (int k = 0; k < kChainBatch; ++k)
-            if (i0 + k < len) out[i0 + k] = x[k];
+        for (int k = 0; k < kPairs; ++k) {
+          const int i = first + 2 * k;
+          if (!test) {
+            out[i / 2] = x[k];
+          } else {
+            if (i < len) my_row[c0 + i] = x[k].x;
+            if (i + 1 < len) my_row[c0 + i + 1] = x[k].y;
+          }
         }
+      };
+      double2 xa[kPairs], xb[kPairs];
+      read(xa, 0);
+      int i = 0;
+      for (; i < whole; i += 2 * kChainBatch) {
+        read(xb, i + kChainBatch);
+        add(xa, i, false);
+        read(xa, i + 2 * kChainBatch);
+        add(xb, i + kChainBatch, false);
+      }
+      for (; i < steps; i += 2 * kChainBatch) {
+        read(xb, i + kChainBatch);
+        add(xa, i, true);
+        read(xa, i + 2 * kChainBatch);
+        add(xb, i + kChainBatch, true);
       }
     }
-    __builtin_amdgcn_wave_barrier();  // lane 0's reads of the chunk are done before it is refilled
+    __syncthreads();  // the chain lanes' reads of the chunk are done before it is refilled
   }
 }
 
@@ -1764,7 +1940,8 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
     hipLaunchKernelGGL(alloc::mm_sort_kernel<12>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
-  hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3(rows), dim3(kWave), 0, s, m);
+  hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3((rows + alloc::kChainsPerWave - 1) / alloc::kChainsPerWave),
+                     dim3(kWave), 0, s, m);
   const dim3 level_grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 2));
   if (wide)
     hipLaunchKernelGGL(alloc::mm_levels_kernel<0>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
