@@ -388,9 +388,9 @@ int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blo
  * taken in stable descending share order) by the reference's 60-step bisection of the level, then
  * gives the leftover one block at a time to the request of the lowest (retained share, index).
  * rows <= 65535 (past 8192 requests the bisection keeps each request's state in the workspace),
- * width <= 262144 (requests up to 12288 blocks sort in LDS, wider ones through a device-wide
- * segmented radix sort whose storage the workspace includes, with rows x width below 2^31; the
- * level positions take 32 bits past 65535 blocks).  workspace:
+ * width <= 262144 (requests up to 12288 blocks sort in LDS, wider ones in global memory, in a
+ * second buffer the workspace includes; the level positions take 32 bits past 65535 blocks).
+ * workspace:
  * ekv_rank_maxmin_workspace(rows, width) bytes of device memory.
  */
 size_t ekv_rank_maxmin_workspace(int32_t rows, int32_t width);

@@ -21,10 +21,9 @@
 //
 // maxmin: raise the lowest retained share as far as the budget allows, then spend what is left on
 // the lowest request first (observe/allocation.py:126-166).  Per request: the pinned shares' NumPy
-// sum (base), its open blocks in stable descending share order (a block radix sort in LDS over the
-// same order-preserving keys, one workgroup per request; past 12288 blocks a device-wide segmented
-// sort), and their running float64 totals, added in that order as np.cumsum does by one lane per
-// request.  The 60-step bisection of the level: a request's count at a level is
+// sum (base), its open blocks in stable descending share order (a radix sort over the same
+// order-preserving keys, one workgroup per request, in LDS; past 12288 blocks in global memory), and
+// their running float64 totals, added in that order as np.cumsum does.  The 60-step bisection of the level: a request's count at a level is
 // min(1 + lower_bound(totals + 2 r, level - base - 1e-12 + 2 r), open), the shifted-by-2r comparison
 // NumPy's single search makes.  Its first 20 steps are walks over counts that two kernels sum over
 // every CU at the levels they can reach; the rest run in one workgroup, every request keeping the
@@ -37,7 +36,6 @@
 
 #include <algorithm>
 
-#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "ekv_common.hpp"
 #include "ekv_pairwise.hpp"
@@ -446,12 +444,8 @@ struct MaxminParams {
   // bracket, counts there and at the step's mid, and its count and retained share, in memory
   int32_t *b_lo, *b_hi, *b_flo, *b_fhi, *b_fmid, *b_pmid, *b_count;
   double *b_retained;
-  // requests wider than a sort in LDS (width > kMaxWidth): the device-wide segmented sort's inputs
-  unsigned long long *keys_in;  // [rows][width]
-  int32_t *vals_in;             // [rows][width]
-  int32_t *seg_begin, *seg_end; // [rows]
-  void *sort_temp;              // the segmented sort's temporary storage (host-side fields)
-  size_t sort_temp_bytes;
+  // requests wider than a sort in LDS (width > kMaxWidth): the sort's second buffer, [rows][width]
+  unsigned long long *keys_in;
 };
 
 // the bisection's first kLevelBits steps can only reach the levels j / 2^kLevelBits (0 < j < 2^kLevelBits,
@@ -541,20 +535,17 @@ struct SortLds {
   unsigned int count[kSortWaves][kDigitBins];  // per wave and digit; scratch between the passes
 };
 
-// One pass over bits [lo, lo + 8) of the ITEMS * kSortThreads elements in `elem`.
+// This wave's ranking of its ITEMS x 64 elements e (position order: i, then lane) by the digit at bit
+// lo: info[i] = digit (bits 16-23, descending as ascending) << 16 | the element's rank among the
+// wave's elements with that digit.  cnt (the wave's 256 counts in LDS) ends holding the wave's count
+// of each digit.  Every lane of the wave must take part.
 template <int ITEMS>
-__device__ __forceinline__ void radix_pass(unsigned long long *elem, unsigned int (*count)[kDigitBins], int lo) {
+__device__ __forceinline__ void rank_wave(const unsigned long long (&e)[ITEMS], int lo, unsigned int *cnt,
+                                          uint32_t (&info)[ITEMS]) {
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int run0 = wave * kWave * ITEMS;
-  unsigned long long e[ITEMS];
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) e[i] = elem[run0 + i * kWave + lane];
-  unsigned int *cnt = count[wave];
-  // cleared before this wave's atomics below: one wave's LDS accesses take effect in order
+  // cleared before the counting below: one wave's LDS accesses take effect in order
 #pragma unroll
   for (int j = 0; j < kDigitBins / kWave; ++j) cnt[j * kWave + lane] = 0u;
-  uint32_t info[ITEMS];  // the digit (bits 16-23, descending as ascending) and the rank in the wave
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const uint32_t d = 255u - (uint32_t)((e[i] >> lo) & 255u);
@@ -563,8 +554,8 @@ __device__ __forceinline__ void radix_pass(unsigned long long *elem, unsigned in
     uint32_t peer_lo = ~0u, peer_hi = ~0u;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      const uint64_t set = __ballot((d >> b) & 1u);
-      const uint32_t f = (uint32_t)__builtin_amdgcn_sbfe((int)~d, b, 1);
+      const uint32_t f = (uint32_t)__builtin_amdgcn_sbfe((int)~d, b, 1);  // all ones where d lacks the bit
+      const uint64_t set = __ballot(f == 0u);
       peer_lo = __builtin_amdgcn_bitop3_b32(peer_lo, (uint32_t)set, f, 0x60);  // peer & (set ^ f)
       peer_hi = __builtin_amdgcn_bitop3_b32(peer_hi, (uint32_t)(set >> 32), f, 0x60);
     }
@@ -577,6 +568,19 @@ __device__ __forceinline__ void radix_pass(unsigned long long *elem, unsigned in
     // to the moves after the scan instead of this one word
     asm volatile("" : "+v"(info[i]));
   }
+}
+
+// One pass over bits [lo, lo + 8) of the ITEMS * kSortThreads elements in `elem`.
+template <int ITEMS>
+__device__ __forceinline__ void radix_pass(unsigned long long *elem, unsigned int (*count)[kDigitBins], int lo) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int run0 = wave * kWave * ITEMS;
+  unsigned long long e[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) e[i] = elem[run0 + i * kWave + lane];
+  uint32_t info[ITEMS];
+  rank_wave<ITEMS>(e, lo, count[wave], info);
   __syncthreads();  // every wave's counts are final and every element is in registers
   {
     // the counts in (digit, wave) order: thread t takes digit t / 4 and waves 4 (t % 4) .. + 3; the
@@ -782,35 +786,197 @@ void mm_sort_kernel(const MaxminParams m) {
     sort_request<MAX_ITEMS>(m, st, r, lds);
 }
 
-// Requests wider than a sort in LDS go through a device-wide segmented radix sort (rocPRIM's, stable,
-// descending) instead: this kernel writes every request's keys and block indices (the keys of
-// sort_request) and its segment, one workgroup per request ...
-__global__ __launch_bounds__(kThreads) void mm_wide_keys_kernel(const MaxminParams m) {
-  const Params &p = m.p;
-  const int r = blockIdx.x;
-  const RowStat st = p.row_stat[r];
-  const int64_t row0 = (int64_t)r * p.width;
-  for (int pos = threadIdx.x; pos < st.n; pos += kThreads) {
-    const bool pinned = pinned_at(p, r, pos, st.n);
-    m.keys_in[row0 + pos] = pinned ? 0ull : gain_key(share_value(st, p.scores[(int64_t)r * p.scores_stride + pos]));
-    m.vals_in[row0 + pos] = pos;
+// Requests wider than a sort in LDS: the same radix sort, one workgroup per request, its elements in
+// global memory (keys_in and the request's prefix row, in turn) and streamed through the workgroup a
+// tile of kWideTile at a time.  An element packs the key's bits 24-63 above an 18-bit index.  A pass
+// counts the digit over the request, scans the counts into each digit's first position, then ranks
+// the tiles in order as the LDS sort ranks its elements and moves each element to its digit's next
+// position, which advances by the tile's count.  The runs that tie in the top bits are sorted again,
+// as in the LDS sort, on (~run, bits 0-23, index) over six passes.
+constexpr int kWideItems = 8;
+constexpr int kWideTile = kWideItems * kSortThreads;
+constexpr int kWideIndexBits = 18;
+static_assert(kMaxMaxminWidth <= (1 << kWideIndexBits), "a block index fits the wide element");
+
+struct WideSortLds {
+  unsigned int count[kSortWaves][kDigitBins];
+  unsigned int next[kDigitBins];  // each digit's next position in the destination
+  int scan[kSortWaves];
+  unsigned long long last[kSortThreads];  // the check: each thread's last key in the tile
+  unsigned long long carry;               // the previous tile's last key
+  int run_carry;                          // runs numbered before this tile
+  unsigned int resort;
+};
+
+// one pass over bits [lo, lo + 8) of the n elements of src, into dst
+__device__ __forceinline__ void wide_radix_pass(const unsigned long long *src, unsigned long long *dst, int n, int lo,
+                                                WideSortLds &lds) {
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const int run0 = wave * kWave * kWideItems;
+  // the digit's count over the request (in the waves' counts, summed below)
+#pragma unroll
+  for (int j = 0; j < kDigitBins / kWave; ++j) lds.count[wave][j * kWave + lane] = 0u;
+  __syncthreads();
+  for (int t0 = 0; t0 < n; t0 += kWideTile) {
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = t0 + run0 + i * kWave + lane;
+      if (pos < n) atomicAdd(&lds.count[wave][255u - (uint32_t)((src[pos] >> lo) & 255u)], 1u);
+    }
   }
-  if (threadIdx.x == 0) {
-    m.seg_begin[r] = (int32_t)row0;
-    m.seg_end[r] = (int32_t)(row0 + st.n);
+  __syncthreads();
+  {
+    int total = 0;
+    if (tid < kDigitBins)
+      for (int w = 0; w < kSortWaves; ++w) total += (int)lds.count[w][tid];
+    int all;
+    const int at = block_exclusive_scan<kSortThreads>(total, lds.scan, all);
+    if (tid < kDigitBins) lds.next[tid] = (unsigned int)at;
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < n; t0 += kWideTile) {
+    unsigned long long e[kWideItems];
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = t0 + run0 + i * kWave + lane;
+      e[i] = pos < n ? src[pos] : 0ull;  // past n: ranked after every element of the tile, never moved
+    }
+    uint32_t info[kWideItems];
+    rank_wave<kWideItems>(e, lo, lds.count[wave], info);
+    __syncthreads();
+    if (tid < kDigitBins) {  // digit tid: the waves' first positions, and the digit's next after the tile
+      unsigned int at = lds.next[tid];
+      for (int w = 0; w < kSortWaves; ++w) {
+        const unsigned int c = lds.count[w][tid];
+        lds.count[w][tid] = at;
+        at += c;
+      }
+      lds.next[tid] = at;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = t0 + run0 + i * kWave + lane;
+      if (pos < n) dst[lds.count[wave][info[i] >> 16] + (info[i] & 0xffffu)] = e[i];
+    }
+    __syncthreads();  // the counts are read before the next tile's ranking clears them
   }
 }
 
-// ... and this one turns the sorted keys, written over `prefix`, into the open shares in sorted order.
-__global__ __launch_bounds__(kThreads) void mm_wide_unpack_kernel(const MaxminParams m) {
+__global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const MaxminParams m) {
+  __shared__ WideSortLds lds;
+  constexpr unsigned long long kIndexMask = (1ull << kWideIndexBits) - 1ull;
+  constexpr unsigned long long kLow = (1ull << kSortLowBits) - 1ull;
   const Params &p = m.p;
   const int r = blockIdx.x;
-  const int open = p.row_stat[r].open;
-  double *row = m.prefix + (int64_t)r * p.width;
-  const unsigned long long *keys = reinterpret_cast<const unsigned long long *>(row);
-  for (int pos = threadIdx.x; pos < open; pos += kThreads) {
-    const unsigned long long k = keys[pos];
-    row[pos] = key_value(k);
+  const RowStat st = p.row_stat[r];
+  const int n = st.n, open = st.open;
+  if (n <= 0) return;
+  const int tid = threadIdx.x;
+  const int64_t row0 = (int64_t)r * p.width;
+  const double *srow = p.scores + (int64_t)r * p.scores_stride;
+  const bool masked = p.pinned != nullptr;
+  const uint8_t *prow = masked ? p.pinned + (int64_t)r * p.pinned_stride : reinterpret_cast<const uint8_t *>(srow);
+  auto key_of = [&](int b) {  // the full key of block b < n
+    return block_key(st, masked, b, srow[b], prow[b]);
+  };
+  unsigned long long *buf[2] = {m.keys_in + row0, reinterpret_cast<unsigned long long *>(m.prefix + row0)};
+  for (int pos = tid; pos < n; pos += kSortThreads)
+    buf[0][pos] = ((key_of(pos) >> kSortLowBits) << kWideIndexBits) | (unsigned long long)pos;
+  __syncthreads();
+  int cur = 0;
+#pragma unroll 1
+  for (int lo = kWideIndexBits; lo < kWideIndexBits + 64 - kSortLowBits; lo += 8, cur ^= 1)
+    wide_radix_pass(buf[cur], buf[cur ^ 1], n, lo, lds);
+  // Neighbours that tie in the top bits, tile by tile: each thread its kWideItems consecutive positions
+  if (tid == 0) {
+    lds.resort = 0u;
+    lds.carry = 0ull;
+  }
+  for (int t0 = 0; t0 < n; t0 += kWideTile) {
+    unsigned long long key[kWideItems];
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = t0 + tid * kWideItems + i;
+      key[i] = pos < n ? key_of((int)(buf[cur][pos] & kIndexMask)) : 0ull;
+    }
+    lds.last[tid] = key[kWideItems - 1];
+    __syncthreads();
+    const unsigned long long before = tid > 0 ? lds.last[tid - 1] : lds.carry;
+    bool unsorted = false;
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = t0 + tid * kWideItems + i;
+      const unsigned long long prev = i > 0 ? key[i - 1] : before;
+      unsorted |= pos > 0 && pos < n && (key[i] >> kSortLowBits) == (prev >> kSortLowBits) && (key[i] & kLow) > (prev & kLow);
+    }
+    if (unsorted) lds.resort = 1u;
+    __syncthreads();
+    if (tid == kSortThreads - 1) lds.carry = key[kWideItems - 1];
+  }
+  __syncthreads();
+  if (lds.resort != 0u) {
+    // runs of equal top bits numbered in order (a scan of their first positions, tile by tile), the
+    // elements packed as (~run, bits 0-23, index) into the other buffer, then six passes
+    if (tid == 0) {
+      lds.carry = 0ull;
+      lds.run_carry = 0;
+    }
+    __syncthreads();
+    for (int t0 = 0; t0 < n; t0 += kWideTile) {
+      unsigned long long key[kWideItems];
+      int idx[kWideItems];
+#pragma unroll
+      for (int i = 0; i < kWideItems; ++i) {
+        const int pos = t0 + tid * kWideItems + i;
+        idx[i] = pos < n ? (int)(buf[cur][pos] & kIndexMask) : 0;
+        key[i] = pos < n ? key_of(idx[i]) : 0ull;
+      }
+      lds.last[tid] = key[kWideItems - 1];
+      __syncthreads();
+      const unsigned long long before = tid > 0 ? lds.last[tid - 1] : lds.carry;
+      int starts = 0;
+#pragma unroll
+      for (int i = 0; i < kWideItems; ++i) {
+        const int pos = t0 + tid * kWideItems + i;
+        const unsigned long long prev = i > 0 ? key[i - 1] : before;
+        starts += (pos < n && (pos == 0 || (key[i] >> kSortLowBits) != (prev >> kSortLowBits))) ? 1 : 0;
+      }
+      int tile_runs;
+      int run = lds.run_carry + block_exclusive_scan<kSortThreads>(starts, lds.scan, tile_runs) - 1;
+#pragma unroll
+      for (int i = 0; i < kWideItems; ++i) {
+        const int pos = t0 + tid * kWideItems + i;
+        const unsigned long long prev = i > 0 ? key[i - 1] : before;
+        run += (pos < n && (pos == 0 || (key[i] >> kSortLowBits) != (prev >> kSortLowBits))) ? 1 : 0;
+        if (pos < n)
+          buf[cur ^ 1][pos] = ((~(unsigned long long)run & kIndexMask) << (kWideIndexBits + kSortLowBits)) |
+                              ((key[i] & kLow) << kWideIndexBits) | (unsigned long long)idx[i];
+      }
+      __syncthreads();
+      if (tid == kSortThreads - 1) {
+        lds.carry = key[kWideItems - 1];
+        lds.run_carry += tile_runs;
+      }
+      __syncthreads();
+    }
+    cur ^= 1;
+#pragma unroll 1
+    for (int lo = kWideIndexBits; lo < 2 * kWideIndexBits + kSortLowBits; lo += 8, cur ^= 1)
+      wide_radix_pass(buf[cur], buf[cur ^ 1], n, lo, lds);
+  }
+  // the outputs: each thread reads its positions before writing them (the final buffer may be the
+  // prefix row itself)
+  for (int pos0 = tid * kWideItems; pos0 < n; pos0 += kWideTile) {
+    int idx[kWideItems];
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) idx[i] = pos0 + i < n ? (int)(buf[cur][pos0 + i] & kIndexMask) : 0;
+#pragma unroll
+    for (int i = 0; i < kWideItems; ++i) {
+      const int pos = pos0 + i;
+      if (pos < n) m.vals_out[row0 + pos] = idx[i];
+      if (pos < open) m.prefix[row0 + pos] = key_value(key_of(idx[i]));
+    }
   }
 }
 
@@ -1762,19 +1928,8 @@ namespace {
 struct MaxminLayout {
   size_t state, row_stat, mrow, order, level_count, level_pos, level_count2, level_pos2, bisect, vals_out, prefix,
       total;
-  size_t keys_in, vals_in, seg_begin, seg_end, sort_temp, sort_temp_bytes;  // rows wider than kMaxWidth
+  size_t keys_in;  // rows wider than kMaxWidth: the sort's second buffer (0: none)
 };
-
-// Temporary storage of the segmented sort of rows x width keys (0 if the query fails).
-size_t wide_sort_bytes(int32_t rows, int32_t width) {
-  size_t bytes = 0;
-  unsigned long long *keys = nullptr;
-  int32_t *vals = nullptr, *offsets = nullptr;
-  const hipError_t e = rocprim::segmented_radix_sort_pairs_desc(
-      nullptr, bytes, keys, keys, vals, vals, (unsigned int)((size_t)rows * (size_t)width), (unsigned int)rows, offsets,
-      offsets, 0, 64, (hipStream_t)0);
-  return e == hipSuccess ? bytes : 0;
-}
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -1808,15 +1963,6 @@ MaxminLayout maxmin_layout(int32_t rows, int32_t width) {
   if (width > alloc::kMaxWidth) {
     l.keys_in = at;
     at = align256(at + cells * 8);
-    l.vals_in = at;
-    at = align256(at + cells * 4);
-    l.seg_begin = at;
-    at = align256(at + (size_t)rows * 4);
-    l.seg_end = at;
-    at = align256(at + (size_t)rows * 4);
-    l.sort_temp_bytes = wide_sort_bytes(rows, width);
-    l.sort_temp = at;
-    at = align256(at + l.sort_temp_bytes);
   }
   l.total = at + 256;  // + 256: the base may be realigned
   return l;
@@ -1851,14 +1997,7 @@ void set_maxmin_buffers(const MaxminLayout &l, uintptr_t base, alloc::MaxminPara
     take_ints(m.b_count);
     m.b_retained = (double *)at;
   }
-  if (l.sort_temp_bytes > 0) {
-    m.keys_in = (unsigned long long *)(base + l.keys_in);
-    m.vals_in = (int32_t *)(base + l.vals_in);
-    m.seg_begin = (int32_t *)(base + l.seg_begin);
-    m.seg_end = (int32_t *)(base + l.seg_end);
-    m.sort_temp = (void *)(base + l.sort_temp);
-    m.sort_temp_bytes = l.sort_temp_bytes;
-  }
+  if (m.p.width > alloc::kMaxWidth) m.keys_in = (unsigned long long *)(base + l.keys_in);
 }
 
 }  // namespace
@@ -1877,14 +2016,9 @@ extern "C" int ekv_rank_maxmin(const double *scores, int64_t scores_stride, cons
   if (rows < 0 || rows > alloc::kMaxMaxminRows || width < 1 || width > alloc::kMaxMaxminWidth)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: rows %d (max %d), width %d (max %d)", rows, alloc::kMaxMaxminRows,
                 width, alloc::kMaxMaxminWidth);
-  if (width > alloc::kMaxWidth && (int64_t)rows * width > INT_MAX)
-    return fail(EKV_EINVAL, "ekv_rank_maxmin: %d rows x %d blocks past the device-wide sort's 32-bit offsets", rows,
-                width);
   if (budget < 0) return fail(EKV_EINVAL, "ekv_rank_maxmin: the budget cannot be negative");
   if (rows == 0) return EKV_OK;
   const MaxminLayout l = maxmin_layout(rows, width);
-  if (width > alloc::kMaxWidth && l.sort_temp_bytes == 0)
-    return fail(EKV_ELAUNCH, "ekv_rank_maxmin: the segmented sort's storage query failed");
   if (workspace_bytes < l.total)
     return fail(EKV_EINVAL, "ekv_rank_maxmin: a workspace of %zu bytes is below the %zu needed", workspace_bytes,
                 l.total);
@@ -1922,16 +2056,7 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
   if (wide) {
-    // a device-wide segmented sort over the requests' keys, the sorted keys over `prefix`
-    hipLaunchKernelGGL(alloc::mm_wide_keys_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
-    size_t temp_bytes = m.sort_temp_bytes;
-    rc = check_hip(rocprim::segmented_radix_sort_pairs_desc(
-                       m.sort_temp, temp_bytes, m.keys_in, reinterpret_cast<unsigned long long *>(m.prefix),
-                       m.vals_in, m.vals_out, (unsigned int)((size_t)rows * (size_t)width), (unsigned int)rows,
-                       m.seg_begin, m.seg_end, 0, 64, s),
-                   "ekv_rank_maxmin segmented sort");
-    if (rc != EKV_OK) return rc;
-    hipLaunchKernelGGL(alloc::mm_wide_unpack_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, m);
+    hipLaunchKernelGGL(alloc::mm_wide_sort_kernel, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   } else if (width <= 4 * alloc::kSortThreads)
     hipLaunchKernelGGL(alloc::mm_sort_kernel<4>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   else if (width <= 8 * alloc::kSortThreads)
@@ -2031,9 +2156,6 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
   if (rows < 0 || rows > max_rows || width < 1 || width > max_width)
     return fail(EKV_EINVAL, "ekv_controller_keep: rows %d (max %d), width %d (max %d)", rows, max_rows, width,
                 max_width);
-  if (objective == EKV_OBJ_MAXMIN && width > alloc::kMaxWidth && (int64_t)rows * width > INT_MAX)
-    return fail(EKV_EINVAL, "ekv_controller_keep: %d rows x %d blocks past the device-wide sort's 32-bit offsets",
-                rows, width);
   if (recent_blocks < 0 || cap_above_blocks < 0)
     return fail(EKV_EINVAL, "ekv_controller_keep: recent_blocks %d, cap_above_blocks %d", recent_blocks,
                 cap_above_blocks);
@@ -2095,8 +2217,6 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
     rc = alloc::launch_sum(p, s);
   } else {
     const MaxminLayout ml = maxmin_layout(rows, width);
-    if (width > alloc::kMaxWidth && ml.sort_temp_bytes == 0)
-      return fail(EKV_ELAUNCH, "ekv_controller_keep: the segmented sort's storage query failed");
     alloc::MaxminParams m{};
     m.p = p;
     set_maxmin_buffers(ml, inner, m);

@@ -74,13 +74,15 @@ def test_shape_limits_are_refused_on_the_host():
                      P, wide, P, 0, 0)
     with pytest.raises(ValueError, match="block size"):
         ekv_hip.call("ekv_rank_uniform_view", P, 64, P, 0, 0, 0, 4, 64, 0.5, -1, P, 64, 0, P, 64, P, 0, P, 64, P, 0, 0)
-    # sum and maxmin: rows past 262144 blocks; maxmin past 12288 blocks: rows x width under 2^31
+    # sum and maxmin: rows past 262144 blocks
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_rank_sum", P, wide, P, 0, 0, 0, 4, wide, 10, P, wide, 0, P, 1 << 20, 0)
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_rank_maxmin", P, wide, P, 0, 0, 4, wide, 10, P, wide, 0, P, 1 << 20, 0)
-    with pytest.raises(ValueError, match="32-bit offsets"):
-        ekv_hip.call("ekv_rank_maxmin", P, 262144, P, 0, 0, 8192, 262144, 10, P, 262144, 0, P, 1 << 20, 0)
+    # maxmin: a workspace below the size the call reports (no 32-bit limit on rows x width)
+    need = int(ekv_hip.load().ekv_rank_maxmin_workspace(8192, 262144))
+    with pytest.raises(ValueError, match="workspace"):
+        ekv_hip.call("ekv_rank_maxmin", P, 262144, P, 0, 0, 8192, 262144, 10, P, 262144, 0, P, need - 4096, 0)
     # maxmin: more than 65535 requests
     with pytest.raises(ValueError, match="rows"):
         ekv_hip.call("ekv_rank_maxmin", P, 8, P, 0, 0, 65536, 8, 10, P, 8, 0, P, 1 << 30, 0)

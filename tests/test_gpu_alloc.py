@@ -198,7 +198,7 @@ def test_maxmin_leftover_over_plateaus_and_ties(rows):
 @pytest.mark.parametrize("sizes", [(12289, 300, 5000), (20000, 16384, 17, 9000), (65535, 40000, 12288),
                                    (65536, 100000, 7), (262144, 70000)])
 def test_maxmin_rows_wider_than_a_sort_in_lds(sizes):
-    # requests past 12288 blocks go through the device-wide segmented sort and search their running
+    # requests past 12288 blocks sort in global memory and search their running
     # totals in memory; ties (integer scores), explicit pins and a zero tail
     rng = np.random.default_rng(sum(sizes))
     scores = [rng.integers(0, 6, size=n).astype(float) * rng.choice([1e-3, 1.0]) for n in sizes]

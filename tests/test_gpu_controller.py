@@ -144,7 +144,7 @@ def test_sum_rows_wider_than_a_register_row():
 
 @pytest.mark.parametrize("width", [30000, 70000])
 def test_maxmin_rows_wider_than_a_sort_in_lds(width):
-    # the maxmin rule on rows past 12288 blocks (the device-wide segmented sort), and past 65535
+    # the maxmin rule on rows past 12288 blocks (the sort in global memory), and past 65535
     # (level positions in 32 bits)
     rng = np.random.default_rng(22)
     rows = 4
