@@ -372,8 +372,10 @@ int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_
  * the blocks of all rows.  keep[r][b] is 1 or 0, and 1 past the row's blocks.  summary (int64[6],
  * may be NULL): budget, blocks of all rows, pinned blocks, status (1: the budget is below the
  * pinned blocks -- the reference raises ValueError -- and every block is kept), requests, free.
- * workspace: ekv_rank_sum_workspace(rows) bytes of device memory the call may overwrite.
- * rows at most 65535, width at most 262144 (every pass streams the rows from memory).
+ * workspace: ekv_rank_sum_workspace(rows) bytes of device memory the call may overwrite (16 KB a
+ * row of it lists the blocks left after the select's first digit).  rows at most 65535, width at most
+ * 262144 (the first two passes stream the rows from memory; the later ones read the list, or the
+ * rows again when it outgrows its room).
  */
 size_t ekv_rank_sum_workspace(int32_t rows);
 int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blocks, const double *weights,

@@ -85,6 +85,11 @@ struct Params {
   int64_t *summary;
   State *state;
   RowStat *row_stat;
+  // sum: the open blocks whose gain key matched the first pass's digit, as (gain key, tie key) pairs,
+  // listed by the second pass so that the later passes read them alone: each workgroup of the passes
+  // lists its rows' blocks in its own region of `cand` (cand_region) and their number in cand_count
+  unsigned long long *cand;
+  unsigned int *cand_count;  // [workgroups of the passes]
   // the controller's rule (ekv_controller_keep): budget < 0 takes max(pinned, ceil(fraction * blocks))
   // over every block of the measured rows, from `ctl`, which also holds the request count
   double fraction;
@@ -324,56 +329,111 @@ __device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_p
 // one once, with device-scope atomics; once they have completed it counts its arrival, and the
 // pass's last workgroup picks the digit (pick_digit), so no second kernel runs per pass.
 // last_gain_pass: 1 on the last gain pass, 0 on the others, -1 on tie passes.
-template <bool TIE>
+// CAND_MODE: 1 (the second gain pass) also lists the blocks it counts, every one matching the first
+// pass's digit, in p.cand; 2 (the later passes) reads that list instead of the rows, unless it
+// outgrew its capacity.
+constexpr int kCandPerRow = 1024;  // the list's room per request row
+
+// Workgroup w of a pass takes rows w, w + grid, ...: its region of the list holds kCandPerRow pairs
+// for each of them, after the regions of the workgroups before it.
+__device__ __forceinline__ void cand_region(int rows, int w, int grid, long long &first, int &room) {
+  const int per = rows / grid, extra = rows % grid;
+  first = (long long)kCandPerRow * ((long long)w * per + min(w, extra));
+  room = kCandPerRow * (per + (w < extra ? 1 : 0));
+}
+
+template <bool TIE, int CAND_MODE>
 __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits, int last_gain_pass) {
+  constexpr int cand_mode = CAND_MODE;
   __shared__ unsigned int s_hist[kBins];
   __shared__ int s_last;
+  __shared__ unsigned int s_listed;
   State *s = p.state;
   if (s->mode != kSelect || s->error || s->done) return;
   for (int i = threadIdx.x; i < kBins; i += kThreads) s_hist[i] = 0u;
+  if (threadIdx.x == 0) s_listed = 0u;
   __syncthreads();
+  long long region;
+  int room;
+  cand_region(p.rows, blockIdx.x, gridDim.x, region, room);
   const unsigned int digit_mask = (1u << bits) - 1u;
   const unsigned long long prefix = s->prefix, mask = s->mask, threshold = s->threshold;
-  for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
-    const RowStat st = p.row_stat[r];
-    const double weight = weight_of(p, r);
-    for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < st.n; b0 += kThreads * kRun) {
-      BlockRun<kRun> run;
-      run.load(p, r, b0, st.n);
+  const int lane = lane_id();
+  // one key per lane of the wave, every lane taking part: when every counting lane has one digit
+  // (the first passes), one add for all
+  auto count = [&](bool counted, unsigned int digit) {
+    const uint64_t active = __ballot(counted);
+    if (active == 0) return;
+    const unsigned int lead = (unsigned int)__builtin_amdgcn_readlane((int)digit, __ffsll((long long)active) - 1);
+    const bool same = __ballot(counted && digit == lead) == active;
+    if (counted) {
+      if (same) {
+        if (lane == __ffsll((long long)active) - 1) atomicAdd(&s_hist[lead], (unsigned int)__popcll(active));
+      } else {
+        atomicAdd(&s_hist[digit], 1u);
+      }
+    }
+  };
+  // which of a key's gain and tie key is ranked, and its digit when it matches the prefix
+  auto consider = [&](unsigned long long k, unsigned long long tk, unsigned int &digit) {
+    unsigned long long key = k;
+    bool take = true;
+    if constexpr (TIE) {
+      take = k == threshold;
+      key = tk;
+    }
+    const bool counted = take && (key & mask) == prefix;
+    digit = (unsigned int)(key >> shift) & digit_mask;
+    return counted;
+  };
+  const unsigned int listed = cand_mode == 2 ? p.cand_count[blockIdx.x] : 0u;
+  if (cand_mode == 2 && listed <= (unsigned int)room) {  // this workgroup's list (else its rows again)
+    const unsigned long long *list = p.cand + 2 * region;
+    for (int c0 = 0; c0 < (int)listed; c0 += kThreads) {
+      const int c = c0 + threadIdx.x;
+      unsigned int digit = 0u;
+      const bool counted = c < (int)listed && consider(list[2 * c], list[2 * c + 1], digit);
+      count(counted, digit);
+    }
+  } else {
+    for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
+      const RowStat st = p.row_stat[r];
+      const double weight = weight_of(p, r);
+      for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < st.n; b0 += kThreads * kRun) {
+        BlockRun<kRun> run;
+        run.load(p, r, b0, st.n);
 #pragma unroll
-      for (int u = 0; u < kRun; ++u) {
-        const int b = b0 + u * kThreads;
-        bool counted = false;
-        unsigned int digit = 0u;
-        if (((run.inside & ~run.pinned) >> u) & 1u) {
-          const unsigned long long k = gain_key(weight * share_value(st, run.score[u]));
-          unsigned long long key = k;
-          bool take = true;
-          if constexpr (TIE) {
-            take = k == threshold;
-            key = tie_key(r, b);
+        for (int u = 0; u < kRun; ++u) {
+          const int b = b0 + u * kThreads;
+          bool counted = false;
+          unsigned int digit = 0u;
+          unsigned long long k = 0ull;
+          if (((run.inside & ~run.pinned) >> u) & 1u) {
+            k = gain_key(weight * share_value(st, run.score[u]));
+            counted = consider(k, tie_key(r, b), digit);
           }
-          if (take && (key & mask) == prefix) {
-            counted = true;
-            digit = (unsigned int)(key >> shift) & digit_mask;
-          }
-        }
-        // when every counting lane of the wave has one digit (the first passes), one add for all
-        const uint64_t active = __ballot(counted);
-        if (active == 0) continue;
-        const unsigned int lead = (unsigned int)__builtin_amdgcn_readlane((int)digit, __ffsll((long long)active) - 1);
-        const bool same = __ballot(counted && digit == lead) == active;
-        if (counted) {
-          if (same) {
-            if (lane_id() == __ffsll((long long)active) - 1) atomicAdd(&s_hist[lead], (unsigned int)__popcll(active));
-          } else {
-            atomicAdd(&s_hist[digit], 1u);
+          count(counted, digit);
+          if constexpr (cand_mode == 1) {  // list the counted blocks: one slot reservation (in LDS) per wave
+            const uint64_t active = __ballot(counted);
+            if (active != 0) {
+              const int first = __ffsll((long long)active) - 1;
+              unsigned int at = 0u;
+              if (lane == first) at = atomicAdd(&s_listed, (unsigned int)__popcll(active));
+              at = (unsigned int)__shfl((int)at, first) +
+                   __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0u));
+              if (counted && at < (unsigned int)room) {
+                p.cand[2 * (region + at)] = k;
+                p.cand[2 * (region + at) + 1] = tie_key(r, b);
+              }
+            }
           }
         }
       }
     }
   }
   __syncthreads();
+  if constexpr (cand_mode == 1)
+    if (threadIdx.x == 0) p.cand_count[blockIdx.x] = s_listed;  // may pass the room
   for (int i = threadIdx.x; i < kBins; i += kThreads) {
     const unsigned int c = s_hist[i];
     if (c) __hip_atomic_fetch_add(&s->hist[i], (unsigned long long)c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1858,8 +1918,26 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s);
 
 using namespace ekv;
 
+namespace {
+// The sum workspace from its 256-aligned base: the state, the row statistics, the passes' workgroups'
+// list lengths (one per row at most), then the list of the second pass (kCandPerRow pairs per row),
+// each right after the last (8-byte aligned).
+static_assert(sizeof(alloc::State) % 8 == 0 && sizeof(alloc::RowStat) % 8 == 0, "the list is 8-byte aligned");
+size_t sum_cand_offset(int32_t rows) {
+  const size_t r = (size_t)(rows > 0 ? rows : 0);
+  return sizeof(alloc::State) + r * sizeof(alloc::RowStat) + ((r * sizeof(unsigned int) + 7) & ~(size_t)7);
+}
+void set_sum_buffers(uintptr_t base, int32_t rows, alloc::Params &p) {
+  p.state = (alloc::State *)base;
+  p.row_stat = (alloc::RowStat *)(base + sizeof(alloc::State));
+  p.cand_count = (unsigned int *)(base + sizeof(alloc::State) + (size_t)(rows > 0 ? rows : 0) * sizeof(alloc::RowStat));
+  p.cand = (unsigned long long *)(base + sum_cand_offset(rows));
+}
+}  // namespace
+
 extern "C" size_t ekv_rank_sum_workspace(int32_t rows) {
-  return sizeof(alloc::State) + (size_t)(rows > 0 ? rows : 0) * sizeof(alloc::RowStat) + 256;
+  const size_t r = (size_t)(rows > 0 ? rows : 0);
+  return sum_cand_offset(rows) + r * alloc::kCandPerRow * 2 * sizeof(unsigned long long) + 256;
 }
 
 extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blocks,
@@ -1890,8 +1968,7 @@ extern "C" int ekv_rank_sum(const double *scores, int64_t scores_stride, const i
   p.keep_stride = keep_stride;
   p.summary = summary;
   const uintptr_t base = ((uintptr_t)workspace + 255) & ~(uintptr_t)255;
-  p.state = (alloc::State *)base;
-  p.row_stat = (alloc::RowStat *)(base + sizeof(alloc::State));
+  set_sum_buffers(base, rows, p);
   return alloc::launch_sum(p, (hipStream_t)stream);
 }
 
@@ -1905,16 +1982,23 @@ int launch_sum(Params p, hipStream_t s) {
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
   // the gain threshold, kDigitBits at a time from the top of the 64-bit key
-  for (int top = 64; top > 0; top -= alloc::kDigitBits) {
+  // (the second pass lists the blocks in the first pass's bucket; the later passes read that list)
+  int pass = 0;
+  for (int top = 64; top > 0; top -= alloc::kDigitBits, ++pass) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
-    hipLaunchKernelGGL(alloc::hist_kernel<false>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits,
-                       shift == 0 ? 1 : 0);
+    const int last = shift == 0 ? 1 : 0;
+    if (pass == 0)
+      hipLaunchKernelGGL((alloc::hist_kernel<false, 0>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
+    else if (pass == 1)
+      hipLaunchKernelGGL((alloc::hist_kernel<false, 1>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
+    else
+      hipLaunchKernelGGL((alloc::hist_kernel<false, 2>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
   }
   // among the blocks at the threshold: newer block, earlier request (the tie key)
   static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
   for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
-    hipLaunchKernelGGL(alloc::hist_kernel<true>, grid, dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
+    hipLaunchKernelGGL((alloc::hist_kernel<true, 2>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
   }
   hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
@@ -2212,8 +2296,7 @@ extern "C" int ekv_controller_keep(int32_t objective, const void *shares, int32_
   p.summary = summary;
   const uintptr_t inner = ((base + l.inner) + 255) & ~(uintptr_t)255;
   if (objective == EKV_OBJ_SUM) {
-    p.state = (alloc::State *)inner;
-    p.row_stat = (alloc::RowStat *)(inner + sizeof(alloc::State));
+    set_sum_buffers(inner, rows, p);
     rc = alloc::launch_sum(p, s);
   } else {
     const MaxminLayout ml = maxmin_layout(rows, width);
