@@ -54,7 +54,7 @@ constexpr int kSplitThreads = 256;  // a (row, layer group) per workgroup
 constexpr int kBatch = 8;  // quads (or cells) of each plane in flight per lane
 constexpr int kMaxCells = 64;
 constexpr int kMaxStats = 8000;  // layers * padded cells: 2 floats each in LDS (64 KB)
-constexpr int kWaveLayers = 8;   // the wave form: one layer per wave, 8 waves per workgroup
+constexpr int kWaveLayers = 8;   // the wave form: one layer per wave, 8 or 16 waves per workgroup
 constexpr int kMaxArrivalRows = 65536;  // rows whose arrival counters the workspace holds
 constexpr size_t kHeaderBytes = 256;    // the workspace's status word, then padding
 constexpr size_t kArrivalBytes = (size_t)kMaxArrivalRows * sizeof(int32_t);
@@ -601,10 +601,11 @@ __device__ __forceinline__ uint32_t landed(const uint32_t *at, uint32_t first, i
 // LDS and are added in layer order.  A row of several groups writes each group's partial to the
 // workspace; the last of the row's workgroups to finish (counted in arrivals[row], which it
 // resets) adds them in group order and writes the row, so no second kernel runs.
-template <int S>
-__global__ __launch_bounds__(kWaveLayers *kWave) __attribute__((amdgpu_waves_per_eu(4)))
+template <int S, int NW>
+__global__ __launch_bounds__(NW *kWave) __attribute__((amdgpu_waves_per_eu(4)))
 void shares_wave_kernel(const Params p) {
-  constexpr int NW = kWaveLayers, NT = NW * kWave, kSlots = S * kWave;
+  constexpr int NT = NW * kWave, kSlots = S * kWave;
+  static_assert(kSlots <= NT, "a thread per block in the layer sums");
   __shared__ float s_part[NW][kSlots];
   __shared__ int s_count[NW];
   __shared__ float s_red[NW];
@@ -938,16 +939,23 @@ int launch(Params p, int nrows, void *workspace, size_t workspace_bytes, void *s
   p.lanes_per_layer = std::max(lpl, std::max(cp / 4, 1));
   hipStream_t s = (hipStream_t)stream;
   if (split && vec && !p.from_u && p.cells == 4 && p.width <= kWaveLayers * kWave && nrows <= kMaxArrivalRows) {
-    // the wave form: one layer per wave, the row's last workgroup combines
-    p.groups = (p.layers + kWaveLayers - 1) / kWaveLayers;
+    // the wave form: one layer per wave, 8 waves a workgroup up to 8 layers, else 16 (fewer layer
+    // groups to combine: none up to 16 layers); the row's last workgroup combines
+    const int nw = p.layers <= kWaveLayers ? kWaveLayers : 2 * kWaveLayers;
+    p.groups = (p.layers + nw - 1) / nw;
     const size_t parts = (size_t)nrows * p.groups * p.width * sizeof(float);
     p.part_count = (int32_t *)((char *)p.part + ((parts + 255) / 256) * 256);
     const unsigned grid = (unsigned)nrows * (unsigned)p.groups;
-    const dim3 block(kWaveLayers * kWave);
-    if (p.width <= kWave) hipLaunchKernelGGL(shares_wave_kernel<1>, dim3(grid), block, 0, s, p);
-    else if (p.width <= 2 * kWave) hipLaunchKernelGGL(shares_wave_kernel<2>, dim3(grid), block, 0, s, p);
-    else if (p.width <= 4 * kWave) hipLaunchKernelGGL(shares_wave_kernel<4>, dim3(grid), block, 0, s, p);
-    else hipLaunchKernelGGL(shares_wave_kernel<8>, dim3(grid), block, 0, s, p);
+    const dim3 block(nw * kWave);
+    auto launch = [&](auto nw_tag) {
+      constexpr int NW = decltype(nw_tag)::value;
+      if (p.width <= kWave) hipLaunchKernelGGL((shares_wave_kernel<1, NW>), dim3(grid), block, 0, s, p);
+      else if (p.width <= 2 * kWave) hipLaunchKernelGGL((shares_wave_kernel<2, NW>), dim3(grid), block, 0, s, p);
+      else if (p.width <= 4 * kWave) hipLaunchKernelGGL((shares_wave_kernel<4, NW>), dim3(grid), block, 0, s, p);
+      else hipLaunchKernelGGL((shares_wave_kernel<8, NW>), dim3(grid), block, 0, s, p);
+    };
+    if (nw == kWaveLayers) launch(std::integral_constant<int, kWaveLayers>());
+    else launch(std::integral_constant<int, 2 * kWaveLayers>());
     return check_hip(hipGetLastError(), "tile shares launch");
   }
   if (split && vec && p.cells == 4 && p.width <= 4 * kSplitThreads) {
