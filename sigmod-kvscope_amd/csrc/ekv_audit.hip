@@ -651,13 +651,16 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_cu_kernel(const Params p)
 // change.  So the work list the self-contained kernel rebuilds in every launch -- the tiles of
 // each selected row, their scan, each tile's row and block ids -- is built once per step (by one
 // kernel up to 4096 rows, two small kernels past that) into a plan buffer that holds, for each
-// workgroup of the audit grid, the count of its tiles and their descriptors, contiguous.  A planned launch then starts with one load of
-// the wave's first descriptor before its first key requests, and reads its later descriptors
-// one tile ahead, as the self-contained kernel reads them from LDS.
+// workgroup of the audit grid, the count of its tiles and their descriptors, contiguous.  A planned
+// launch then starts with one load of the wave's first descriptor before its first key requests,
+// and reads its later descriptors one tile ahead, as the self-contained kernel reads them from LDS.
+// Each row's tiles are padded to a multiple of kPlanRun, and each workgroup's list puts its whole
+// runs of kPlanRun tiles first (plan_split_head), so that a launch can give a wave a run whose
+// records fill whole cache lines.
 //
-// Plan buffer (PlanLayout): wg[kMaxGrid] int2 = (tiles, first row), first[kMaxGrid + 1] = the
-// split points of the flat tile list over the grid, row_off[rows + 1] = each row's first tile,
-// desc[grid][cap] = the tiles of each workgroup in flat order.
+// Plan buffer (PlanLayout): wg[kMaxGrid] int4 = (tiles, first row, whole runs, 0), first[kMaxGrid + 1]
+// = the split points of the padded tile list over the grid, row_off[rows + 1] = each row's first
+// padded tile, desc[grid][cap] = the tiles of each workgroup (its whole runs, then the rest).
 // ---------------------------------------------------------------------------------------
 constexpr int kSplitThreads = 1024;
 constexpr int kFillThreads = 256;
@@ -670,19 +673,21 @@ struct PlanLayout {
 
 inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
+// The padded tiles of at most rows x width (plan_split_head).
 inline int64_t plan_max_tiles(int rows, int width) {
-  return (int64_t)rows * ((width + kTileBlocks - 1) / kTileBlocks);
+  const int64_t tiles = (width + kTileBlocks - 1) / kTileBlocks;
+  return (int64_t)rows * ((tiles + kPlanRun - 1) / kPlanRun * kPlanRun);
 }
 
 // The layout of a plan for batches of at most rows x width on a grid of `grid` workgroups.  The
-// split gives workgroup b the tiles [T b / grid, T (b + 1) / grid) of the T live tiles, at most
+// split gives workgroup b the tiles [T b / grid, T (b + 1) / grid) of the T padded tiles, at most
 // ceil(T / grid) of them.
 inline PlanLayout plan_layout(int rows, int width, int grid) {
   PlanLayout L;
   const int64_t max_tiles = plan_max_tiles(rows, width);
   L.cap = (int32_t)std::max<int64_t>(1, (max_tiles + grid - 1) / grid);
   L.wg = 0;
-  L.first = align_up(L.wg + (int64_t)sizeof(int2) * kMaxGrid, 256);
+  L.first = align_up(L.wg + (int64_t)sizeof(int4) * kMaxGrid, 256);
   L.row_off = align_up(L.first + 4 * (int64_t)(kMaxGrid + 1), 256);
   L.desc = align_up(L.row_off + 4 * ((int64_t)rows + 1), 256);
   L.bytes = align_up(L.desc + (int64_t)grid * L.cap * (int64_t)sizeof(TileDesc), 256);
@@ -697,7 +702,7 @@ struct PlanArgs {
   const uint8_t *select;
   const uint32_t *flag;
   int32_t rows, width, block_size, grid, cap;
-  int2 *wg;
+  int4 *wg;
   int32_t *first;
   int32_t *row_off;
   TileDesc *desc;
@@ -708,6 +713,30 @@ __device__ __forceinline__ int plan_row_tiles(const PlanArgs &a, int r) {
   if (a.select[r] == 0) return 0;
   const int len = min(max(a.lens[r], 0), a.width * a.block_size);
   return (len + tile_tokens - 1) / tile_tokens;  // runtime/audit_kernel.py:65-69
+}
+__device__ __forceinline__ int plan_padded(int tiles) { return (tiles + kPlanRun - 1) / kPlanRun * kPlanRun; }
+// split point b of T padded tiles over G workgroups
+__device__ __forceinline__ int plan_first(int64_t T, int64_t G, int64_t b) { return (int)(T * b / G); }
+// split b's entry: (tiles, first row, whole runs listed first, 0)
+__device__ __forceinline__ int4 plan_entry(int f, int cnt, int row) {
+  return make_int4(cnt, row, plan_split_runs(f, cnt), 0);
+}
+// tile k of a row with `real` tiles: its descriptor (past `real`: a padding tile without tokens,
+// whose block ids are the row's last, so that nothing reads past the row)
+__device__ __forceinline__ TileDesc plan_desc(const PlanArgs &a, int row, int k, int real, int len, int qtok) {
+  const int tile_tokens = kTileBlocks * a.block_size;
+  const int nb = (len + a.block_size - 1) / a.block_size;
+  const int32_t *trow = a.table + (int64_t)row * a.table_stride;
+  const int kk = min(k, real - 1);
+  TileDesc d;
+  d.row = row;
+  d.k = k;
+  d.valid = k < real ? min(len - k * tile_tokens, tile_tokens) : 0;
+  d.qtok = qtok;
+  d.id0 = trow[kTileBlocks * kk];
+  d.id1 = kTileBlocks * kk + 1 < nb ? trow[kTileBlocks * kk + 1] : d.id0;  // past the row: stands in
+  d.pad0 = d.pad1 = 0;
+  return d;
 }
 
 // One workgroup: the live tiles of every row (none with the flag off), their exclusive scan,
@@ -720,20 +749,20 @@ __global__ __launch_bounds__(kSplitThreads) void plan_split_kernel(const PlanArg
   const int r1 = min(r0 + per, a.rows);
   int local = 0;
   if (on)
-    for (int r = r0; r < r1; ++r) local += plan_row_tiles(a, r);
+    for (int r = r0; r < r1; ++r) local += plan_padded(plan_row_tiles(a, r));
   int total = 0;
   int base = block_exclusive_scan<kSplitThreads>(local, s_scan, total);
   for (int r = r0; r < r1; ++r) {
     a.row_off[r] = base;
-    if (on) base += plan_row_tiles(a, r);
+    if (on) base += plan_padded(plan_row_tiles(a, r));
   }
   if (threadIdx.x == 0) a.row_off[a.rows] = total;
   for (int b = threadIdx.x; b <= kMaxGrid; b += kSplitThreads) {
-    const int f = b <= a.grid ? (int)((int64_t)total * b / a.grid) : total;
+    const int f = b <= a.grid ? plan_first(total, a.grid, b) : total;
     a.first[b] = f;
     if (b < kMaxGrid) {
-      const int next = b + 1 <= a.grid ? (int)((int64_t)total * (b + 1) / a.grid) : total;
-      a.wg[b] = make_int2(next - f, 0);
+      const int next = b + 1 <= a.grid ? plan_first(total, a.grid, b + 1) : total;
+      a.wg[b] = plan_entry(f, next - f, 0);
     }
   }
 }
@@ -744,15 +773,13 @@ __global__ __launch_bounds__(kFillThreads) void plan_fill_kernel(const PlanArgs 
   __shared__ int s_first[kMaxGrid + 1];
   for (int b = threadIdx.x; b <= a.grid; b += kFillThreads) s_first[b] = a.first[b];
   __syncthreads();
-  const int tile_tokens = kTileBlocks * a.block_size;
   for (int row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const int off = a.row_off[row];
-    const int tiles = a.row_off[row + 1] - off;
+    const int tiles = a.row_off[row + 1] - off;  // padded
     if (tiles <= 0) continue;
+    const int real = plan_row_tiles(a, row);
     const int len = min(max(a.lens[row], 0), a.width * a.block_size);
-    const int nb = (len + a.block_size - 1) / a.block_size;
     const int qtok = a.qrow[row];
-    const int32_t *trow = a.table + (int64_t)row * a.table_stride;
     for (int k = threadIdx.x; k < tiles; k += kFillThreads) {
       const int t = off + k;
       int lo = 0, hi = a.grid;  // the workgroup b with first[b] <= t < first[b + 1]
@@ -760,24 +787,18 @@ __global__ __launch_bounds__(kFillThreads) void plan_fill_kernel(const PlanArgs 
         const int mid = (lo + hi) >> 1;
         if (s_first[mid] <= t) lo = mid; else hi = mid;
       }
-      TileDesc d;
-      d.row = row;
-      d.k = k;
-      d.valid = min(len - k * tile_tokens, tile_tokens);
-      d.qtok = qtok;
-      d.id0 = trow[kTileBlocks * k];
-      d.id1 = kTileBlocks * k + 1 < nb ? trow[kTileBlocks * k + 1] : d.id0;  // past the row: stands in
-      d.pad0 = d.pad1 = 0;
-      a.desc[(int64_t)lo * a.cap + (t - s_first[lo])] = d;
-      if (t == s_first[lo]) a.wg[lo].y = row;
+      const int f = s_first[lo], cnt = s_first[lo + 1] - f;
+      const int pos = plan_split_pos(t - f, plan_split_head(f, cnt), plan_split_runs(f, cnt));
+      a.desc[(int64_t)lo * a.cap + pos] = plan_desc(a, row, k, real, len, qtok);
+      if (t == f) a.wg[lo].y = row;
     }
   }
 }
 
 // The plan in one launch, for batches of at most kPlanRowsLds rows: every workgroup scans all rows'
-// live tiles itself (a few hundred rows: one block scan) into LDS, so its rows' first tiles and the
-// grid's split need no kernel before it, and the workgroup of tile t comes from arithmetic on the
-// split (b = floor(((t + 1) G - 1) / T) is the last b with floor(T b / G) <= t).  The workgroups
+// padded tiles itself (a few hundred rows: one block scan) into LDS, so its rows' first tiles and
+// the grid's split need no kernel before it, and the workgroup of tile t comes from arithmetic on
+// the split (b = floor(((t + 1) G - 1) / T) is the last b with floor(T b / G) <= t).  The workgroups
 // take rows blockIdx.x, blockIdx.x + gridDim.x, ...; the owner of a workgroup's first tile writes
 // its (count, first row), and workgroup 0 writes the empty workgroups' zero counts.
 constexpr int kPlanThreads = 256;
@@ -792,45 +813,36 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const PlanArgs a) {
   const int r1 = min(r0 + per, a.rows);
   int local = 0;
   if (on)
-    for (int r = r0; r < r1; ++r) local += plan_row_tiles(a, r);
+    for (int r = r0; r < r1; ++r) local += plan_padded(plan_row_tiles(a, r));
   int total = 0;
   int base = block_exclusive_scan<kPlanThreads>(local, s_scan, total);
   for (int r = r0; r < r1; ++r) {
     s_off[r] = base;
-    if (on) base += plan_row_tiles(a, r);
+    if (on) base += plan_padded(plan_row_tiles(a, r));
   }
   if (threadIdx.x == 0) s_off[a.rows] = total;
   const int64_t T = total, G = a.grid;
-  auto first = [&](int64_t b) { return (int)(T * b / G); };
+  auto first = [&](int64_t b) { return plan_first(T, G, b); };
   if (blockIdx.x == 0) {
     for (int b = threadIdx.x; b < kMaxGrid; b += kPlanThreads)
-      if (b >= a.grid || first(b + 1) == first(b)) a.wg[b] = make_int2(0, 0);
+      if (b >= a.grid || first(b + 1) == first(b)) a.wg[b] = make_int4(0, 0, 0, 0);
   }
   __syncthreads();
   if (T == 0) return;
-  const int tile_tokens = kTileBlocks * a.block_size;
   for (int row = blockIdx.x; row < a.rows; row += gridDim.x) {
     const int off = s_off[row];
-    const int tiles = s_off[row + 1] - off;
+    const int tiles = s_off[row + 1] - off;  // padded
     if (tiles <= 0) continue;
+    const int real = plan_row_tiles(a, row);
     const int len = min(max(a.lens[row], 0), a.width * a.block_size);
-    const int nb = (len + a.block_size - 1) / a.block_size;
     const int qtok = a.qrow[row];
-    const int32_t *trow = a.table + (int64_t)row * a.table_stride;
     for (int k = threadIdx.x; k < tiles; k += kPlanThreads) {
       const int t = off + k;
       const int b = (int)(((int64_t)(t + 1) * G - 1) / T);
-      const int fb = first(b);
-      TileDesc d;
-      d.row = row;
-      d.k = k;
-      d.valid = min(len - k * tile_tokens, tile_tokens);
-      d.qtok = qtok;
-      d.id0 = trow[kTileBlocks * k];
-      d.id1 = kTileBlocks * k + 1 < nb ? trow[kTileBlocks * k + 1] : d.id0;  // past the row: stands in
-      d.pad0 = d.pad1 = 0;
-      a.desc[(int64_t)b * a.cap + (t - fb)] = d;
-      if (t == fb) a.wg[b] = make_int2(first(b + 1) - fb, row);
+      const int fb = first(b), cnt = first(b + 1) - fb;
+      const int pos = plan_split_pos(t - fb, plan_split_head(fb, cnt), plan_split_runs(fb, cnt));
+      a.desc[(int64_t)b * a.cap + pos] = plan_desc(a, row, k, real, len, qtok);
+      if (t == fb) a.wg[b] = plan_entry(fb, cnt, row);
     }
   }
 }
@@ -841,18 +853,31 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const PlanArgs a) {
 // that over the layers every workgroup's share of tiles differs from another's by at most one
 // tile (the split gives the first T mod grid splits one tile more), and its splits are adjacent
 // in the list (their rows follow one another).  Items run layer by layer; an item is
-// (tile, audited head), tile-major.  Wave w starts at item w and the waves then take items from an
-// LDS counter, one ahead.
-template <int MODE, int HEAD_DIM, int MT>
+// (tile, audited head), tile-major.  The waves take runs of items from an LDS counter (wave w
+// starts at run w), reading each item's descriptor one item ahead: a run is the tiles whose records
+// share cache lines (record_run_tiles) times the audited heads, and its records are stored together
+// when it ends.  The runs come from the whole runs each split lists first (plan_split_head), layer
+// by layer; the last NW runs' worth of them and then the splits' other tiles are taken one at a
+// time, so that the waves run out of work together (a launch of one layer takes most of its items
+// so).
+template <int MODE, int HEAD_DIM, int MT, bool RUNS>
 __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Params p, const PlanView plan,
                                                                     const LayerSet ls) {
   using S = MfmaShape<MODE, HEAD_DIM>;
   using C = CuShape<MODE, HEAD_DIM, MT>;
   constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
   constexpr int NW = C::kWaves;
+  // items of a run whose records are held in registers (fewer where the shape's registers are taken)
+  constexpr int kRecords = HEAD_DIM >= 256 ? 1 : (HEAD_DIM >= 128 ? 4 : 8);
+  static_assert(sizeof(u32x4) * C::kStash >= 256 * sizeof(float), "the records pass through the chunk staging");
 
-  __shared__ int s_next;
-  __shared__ int s_pref[kMaxLaunchLayers + 1];  // items before each layer of the launch
+  __shared__ int s_next;    // the next untaken run
+  __shared__ int s_single;  // past s_switch: the next untaken single item
+  __shared__ int s_switch;  // the items from here on are taken one at a time
+  // the launch's items in 2 nl segments: segment j < nl holds layer j's whole runs (its split's first
+  // tiles), segment nl + j the rest of layer j's split; s_pref[k] items come before segment k
+  __shared__ int s_pref[2 * kMaxLaunchLayers + 1];
+  __shared__ int s_whole[kMaxLaunchLayers];  // tiles in layer j's whole runs
   __shared__ u32x4 s_tr[NW][C::kStash];
   __shared__ unsigned long long s_cycles[kCycleSlots];
 
@@ -862,18 +887,26 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   const int grid = gridDim.x;
   const int nl = ls.n;
   auto split_of = [&](int j) { return (int)((blockIdx.x + (unsigned)j) % (unsigned)grid); };
+  const int run_tiles = record_run_tiles(p.cells, groups);
+  // items a wave takes at a time (RUNS: the form for launches of several layers; a launch of one
+  // layer takes them one at a time, its waves having a few items each)
+  const int run = RUNS ? run_tiles * groups : 1;
   // the flag, the first split's count and first row, the layers' counts and the wave's first
   // descriptor: one latency (a relaxed load: a volatile one is completed before the next is issued)
   uint32_t flag = __hip_atomic_load(p.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  int2 wg = plan.wg[blockIdx.x];
-  int cnt = 0;  // wave 0: lane j holds layer j's split count
-  if (wave == 0 && lane < nl) cnt = plan.wg[split_of(lane)].x;
-  u32x4 d_lo, d_hi;
-  load_desc(plan.desc + (int64_t)blockIdx.x * plan.cap + min(groups == 1 ? wave : wave / groups, plan.cap - 1), d_lo,
-            d_hi);
+  int4 wg = plan.wg[blockIdx.x];
+  int cnt = 0, whole_runs = 0;  // wave 0: lane j holds layer j's split count and whole runs
+  if (wave == 0 && lane < nl) {
+    const int4 e = plan.wg[split_of(lane)];
+    cnt = e.x;
+    whole_runs = e.z;
+  }
+  u32x4 d_lo;
+  u32x2 d_hi;
+  load_desc(plan.desc + (int64_t)blockIdx.x * plan.cap + min(wave * run / groups, plan.cap - 1), d_lo, d_hi);
   // all are waited for here, together: otherwise the compiler tests the flag before it issues the
   // other loads, a second memory latency before the first key request
-  asm volatile("" : "+v"(flag), "+v"(wg.x), "+v"(wg.y), "+v"(cnt) : "v"(d_lo), "v"(d_hi));
+  asm volatile("" : "+v"(flag), "+v"(wg.y), "+v"(cnt), "+v"(whole_runs) : "v"(d_lo), "v"(d_hi));
   // the first layer's parameters and the shared strides, read with the others (a scalar-cache miss
   // after the barrier would be one more latency)
   const char *keys0 = ls.l[0].keys, *q0 = ls.l[0].q;
@@ -882,20 +915,31 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   asm volatile("" : "+s"(keys0), "+s"(q0), "+s"(k_block), "+s"(k_pos), "+s"(k_head), "+s"(q_tok), "+s"(q_head));
   if (flag == 0u) return;  // runtime/audit_kernel.py:64
   if (wave == 0) {
-    // items before each layer: an inclusive scan of the clipped counts over wave 0's lanes
-    const int items_j = min(cnt, plan.cap) * groups;
-    const int inc = wave_inclusive_scan(items_j);
-    if (lane < nl) s_pref[lane + 1] = inc;
+    // items before each segment: an inclusive scan over wave 0's lanes (lane j < nl: layer j's whole
+    // runs, lane nl + j: the rest of its split)
+    const int tiles_j = min(cnt, plan.cap);
+    const int whole_j = min(whole_runs * kPlanRun, tiles_j);
+    const int rest_j = __shfl((tiles_j - whole_j) * groups, (lane - nl) & (kWave - 1), kWave);
+    const int inc = wave_inclusive_scan(lane < nl ? whole_j * groups : (lane < 2 * nl ? rest_j : 0));
+    if (lane < 2 * nl) s_pref[lane + 1] = inc;
+    if (lane < nl) s_whole[lane] = whole_j;
+    const int in_runs = nl > 0 ? __builtin_amdgcn_readlane(inc, nl - 1) : 0;
     if (lane == 0) {
+      // every wave starts with a run (wave w with items w run ..), and runs are taken while every
+      // wave has at least one more ahead of it; the last NW runs' worth of them and the tiles
+      // outside whole runs go one at a time, so that the waves run out of work together
       s_pref[0] = 0;
-      s_next = NW;
+      s_switch = max(NW * run, max(0, in_runs - NW * run) / run * run);
+      s_next = NW * run;
+      s_single = 0;
     }
   }
   if (p.cycles != nullptr)
     for (int k = threadIdx.x; k < kCycleSlots; k += kCuThreads) s_cycles[k] = 0ull;
   const int row0 = __builtin_amdgcn_readfirstlane(wg.y);  // the first split's first row: the timer slots' base
   __syncthreads();  // s_next, the layer offsets and the timer slots are set before any take
-  const int items = __builtin_amdgcn_readfirstlane(s_pref[nl]);
+  const int items = __builtin_amdgcn_readfirstlane(s_pref[2 * nl]);
+  const int switch_at = __builtin_amdgcn_readfirstlane(s_switch);
 
   const int n = lane & 15;  // A: token of the M-tile; B / C: query row
   const int c = lane >> 4;  // dim piece within a k-step; C: token quad
@@ -910,20 +954,23 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
 #pragma unroll
   for (int j = 0; j < NLD; ++j) voff[j] = (uint32_t)((j * S::kTPI + row_in) * k_pos + piece * 16);
 
-  // A wave's position in the launch's items: the layer of its latest taken item and that layer's
-  // item range.  Items a wave takes only grow, so the walk moves forward.
+  // A wave's position in the launch's items: the segment of its latest taken item, that segment's
+  // item range, its layer and the place of its first item in the layer's split.  Items a wave takes
+  // only grow, so the walk moves forward.
   struct Walk {
-    int j, lo, hi;
+    int k, lo, hi, j, base;
   };
   auto walk_to = [&](Walk &w, int item) {
     while (item >= w.hi) {
-      ++w.j;
+      ++w.k;
       w.lo = w.hi;
-      w.hi = __builtin_amdgcn_readfirstlane(s_pref[w.j + 1]);
+      w.hi = __builtin_amdgcn_readfirstlane(s_pref[w.k + 1]);
+      w.j = w.k < nl ? w.k : w.k - nl;
+      w.base = w.k < nl ? 0 : __builtin_amdgcn_readfirstlane(s_whole[w.j]);
     }
   };
   auto desc_of = [&](const Walk &w, int item) {
-    return plan.desc + (int64_t)split_of(w.j) * plan.cap + (item - w.lo) / groups;
+    return plan.desc + (int64_t)split_of(w.j) * plan.cap + w.base + (item - w.lo) / groups;
   };
 
   struct Layer {
@@ -947,7 +994,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   struct Tile {
     int row, h, k, valid, id0, id1, qtok, j;
   };
-  auto describe = [&](const u32x4 &lo, const u32x4 &hi, const Walk &w, int item) -> Tile {
+  auto describe = [&](const u32x4 &lo, const u32x2 &hi, const Walk &w, int item) -> Tile {
     Tile t;
     t.row = __builtin_amdgcn_readfirstlane((int)lo[0]);
     t.k = __builtin_amdgcn_readfirstlane((int)lo[1]);
@@ -956,14 +1003,19 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
     t.id0 = __builtin_amdgcn_readfirstlane((int)hi[0]);
     t.id1 = __builtin_amdgcn_readfirstlane((int)hi[1]);
     t.h = groups == 1 ? 0 : (item - w.lo) % groups;
-    t.j = w.j;
+    t.j = w.j;  // the layer
     return t;
   };
   auto take = [&]() -> int {
     int v = 0;
-    if (lane == 0) v = atomicAdd(&s_next, 1);
+    if (lane == 0) {
+      v = atomicAdd(&s_next, run);
+      if (v >= switch_at) v = switch_at + atomicAdd(&s_single, 1);
+    }
     return __builtin_amdgcn_readfirstlane(v);
   };
+  // the item after item i: the next of its run, or the first of a new run (or a single item)
+  auto after = [&](int i) -> int { return i + 1 < switch_at && (i + 1) % run != 0 ? i + 1 : take(); };
   auto load_chunk = [&](u32x4 (&D)[MT * NLD], const Tile &T, const Layer &L, int sub) {
     const int64_t head_off = (int64_t)(L.group_first + T.h) * k_head;
 #pragma unroll
@@ -975,7 +1027,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
       for (int j = 0; j < NLD; ++j) {
         uint32_t o = voff[j];
         asm volatile("" : "+v"(o));
-        D[mt * NLD + j] = __builtin_nontemporal_load((const u32x4 *)(src + o));
+        D[mt * NLD + j] = __builtin_nontemporal_load(as_global((const u32x4 *)(src + o)));
       }
     }
   };
@@ -986,7 +1038,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int dim = S::kFp8 ? 16 * (4 * (s / 2) + c) + 8 * (s % 2) : 8 * (4 * s + c);
-      Q[s] = n < G ? *(const u32x4 *)(qrow + dim * 2) : (u32x4){0u, 0u, 0u, 0u};
+      Q[s] = n < G ? *as_global((const u32x4 *)(qrow + dim * 2)) : (u32x4){0u, 0u, 0u, 0u};
     }
   };
   auto stash_chunk = [&](const u32x4 (&L)[MT * NLD]) {
@@ -1031,7 +1083,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   // the chunk's tile max and sum, folded into the tile's running (m, l); at the tile's last chunk
   // its record goes into each of its blocks the row reaches (runtime/audit_kernel.py:97-109)
   auto reduce_chunk = [&](const f32x4_t (&acc)[MT], const Tile &T, const Layer &L, int sub, float &m_run,
-                          float &l_run) {
+                          float &l_run, RunRecords<kRecords> &rec) {
     const int tok0 = sub * CH;  // within the tile
     float sc[4 * MT];
     if (tok0 + CH <= T.valid) {
@@ -1067,65 +1119,84 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
     }
     if (sub == nsub - 1) {
       const int blk = kTileBlocks * T.k + c;
-      if (c < kTileBlocks && n < G && c * bs < T.valid) {
-        float *cell = L.lse + (int64_t)T.row * p.row_stride + T.h * G + (int64_t)blk * p.cells + n;
-        cell[0] = m_run * kLn2;
-        cell[p.plane_stride] = l_run;
+      int off = -1;
+      if (c < kTileBlocks && n < G && c * bs < T.valid) off = T.h * G + blk * p.cells + n;
+      float *row_base = L.lse + (int64_t)T.row * p.row_stride;
+      if constexpr (RUNS) {
+        rec.push(row_base, off, m_run * kLn2, l_run, p.plane_stride, (float *)tr);
+      } else if (off >= 0) {
+        as_global(row_base)[off] = m_run * kLn2;
+        as_global(row_base)[off + p.plane_stride] = l_run;
       }
       m_run = -INFINITY;
       l_run = 0.0f;
     }
   };
 
-  if (wave < items) {
-    Walk w{0, 0, __builtin_amdgcn_readfirstlane(s_pref[1])};
-    if (wave >= w.hi) {  // a first layer with fewer items than waves: the wave's first item is later
-      walk_to(w, wave);
-      load_desc(desc_of(w, wave), d_lo, d_hi);
+  const int first_item = wave * run;
+  if (first_item < items) {
+    Walk w{0, 0, __builtin_amdgcn_readfirstlane(s_pref[1]), 0, 0};
+    // the descriptor loaded first is tile wave x run_tiles of the first layer's split: past the first
+    // layer's whole runs the wave's first item is another, loaded now
+    if (first_item >= w.hi) {
+      walk_to(w, first_item);
+      load_desc(desc_of(w, first_item), d_lo, d_hi);
     }
-    Tile T = describe(d_lo, d_hi, w, wave);
+    Tile T = describe(d_lo, d_hi, w, first_item);
     Layer cur = T.j == 0 ? Layer{q0, keys0, ls.l[0].lse, ls.l[0].scale2, ls.l[0].group_first, ls.l[0].q_head0}
                          : layer_of(T.j);
-    int ahead = take();  // the wave's next item, its descriptor read a tile early
+    int ahead = after(first_item);  // the wave's next item, its descriptor read a tile early
     if (ahead < items) {
       walk_to(w, ahead);
       load_desc(desc_of(w, ahead), d_lo, d_hi);
     }
     float m_run = -INFINITY, l_run = 0.0f;
+    RunRecords<kRecords> rec;
+    rec.init();
     f32x4_t acc[MT];
     // one chunk in flight per wave: it goes to LDS when it arrives and the next is requested at once
     u32x4 A[MT * NLD], qb[KS], qn[KS];
     load_query(qb, T, cur);
-    load_chunk(A, T, cur, 0);
+    if (T.valid > 0) load_chunk(A, T, cur, 0);
     int sub = 0;
     uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
     while (true) {
       Tile N = T;
       Layer next = cur;
       int nsub_next = sub + 1;
-      bool more = true, new_query = false;
+      bool more = true, new_query = false, run_ends = false;
       if (nsub_next == nsub) {
         more = ahead < items;
         if (more) {
+          run_ends = ahead >= switch_at || ahead % run == 0;  // N starts a new run or is a single item
           N = describe(d_lo, d_hi, w, ahead);
           if (N.j != T.j) next = layer_of(N.j);
           nsub_next = 0;
-          ahead = take();
-          if (ahead < items) {
-            walk_to(w, ahead);
-            load_desc(desc_of(w, ahead), d_lo, d_hi);
-          }
           new_query = N.row != T.row || N.h != T.h || N.j != T.j;
         }
       }
       stash_chunk(A);  // waits for the chunk
       if (more) {
-        load_chunk(A, N, next, nsub_next);
+        if (N.valid > 0) load_chunk(A, N, next, nsub_next);  // a padding tile has no keys
         if (new_query) load_query(qn, N, next);
+        if (nsub_next == 0) {
+          // the descriptor of the item after N, requested after N's keys: the wait for a chunk
+          // counts every load issued before the wait, so a descriptor requested ahead of the keys
+          // would hold the keys back by its own latency
+          asm volatile("" ::: "memory");
+          ahead = after(ahead);
+          if (ahead < items) {
+            walk_to(w, ahead);
+            load_desc(desc_of(w, ahead), d_lo, d_hi);
+          }
+        }
       }
       mma_stashed(qb, acc);
-      reduce_chunk(acc, T, cur, sub, m_run, l_run);
+      reduce_chunk(acc, T, cur, sub, m_run, l_run, rec);
       if (timed && sub == nsub - 1 && (!more || new_query)) time_tile(T, mark);
+      if constexpr (RUNS) {
+        if (!more || run_ends) rec.flush(p.plane_stride, (float *)tr);
+      }
       if (!more) break;
       if (new_query) {
 #pragma unroll
@@ -1297,33 +1368,36 @@ namespace audit {
 
 using PlannedFn = void (*)(const Params, const PlanView, const LayerSet);
 
-template <int MODE, int HD>
+template <int MODE, int HD, bool RUNS>
 PlannedFn pick_planned_mt(bool wide) {
   constexpr int kRowBytes = MfmaShape<MODE, HD>::kRowBytes;
   if constexpr (kRowBytes <= 128) {
-    if (wide) return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, true)>;
+    if (wide) return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, true), RUNS>;
   }
-  return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, false)>;
+  return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, false), RUNS>;
 }
 
-template <int MODE>
+template <int MODE, bool RUNS>
 PlannedFn pick_planned_hd(int hd, bool wide) {
   switch (hd) {
     case 32:
-      if constexpr (MODE != kModeFp8Bf16) return pick_planned_mt<MODE, 32>(wide);
+      if constexpr (MODE != kModeFp8Bf16) return pick_planned_mt<MODE, 32, RUNS>(wide);
       return nullptr;
-    case 64: return pick_planned_mt<MODE, 64>(wide);
-    case 128: return pick_planned_mt<MODE, 128>(wide);
-    case 256: return pick_planned_mt<MODE, 256>(wide);
+    case 64: return pick_planned_mt<MODE, 64, RUNS>(wide);
+    case 128: return pick_planned_mt<MODE, 128, RUNS>(wide);
+    case 256: return pick_planned_mt<MODE, 256, RUNS>(wide);
   }
   return nullptr;
 }
 
-PlannedFn pick_planned(int mode, int hd, bool wide) {
+// the planned kernel of a shape; `runs`: the form for launches of several layers
+PlannedFn pick_planned(int mode, int hd, bool wide, bool runs) {
   switch (mode) {
-    case kModeF16: return pick_planned_hd<kModeF16>(hd, wide);
-    case kModeBF16: return pick_planned_hd<kModeBF16>(hd, wide);
-    case kModeFp8Bf16: return pick_planned_hd<kModeFp8Bf16>(hd, wide);
+    case kModeF16: return runs ? pick_planned_hd<kModeF16, true>(hd, wide) : pick_planned_hd<kModeF16, false>(hd, wide);
+    case kModeBF16:
+      return runs ? pick_planned_hd<kModeBF16, true>(hd, wide) : pick_planned_hd<kModeBF16, false>(hd, wide);
+    case kModeFp8Bf16:
+      return runs ? pick_planned_hd<kModeFp8Bf16, true>(hd, wide) : pick_planned_hd<kModeFp8Bf16, false>(hd, wide);
   }
   return nullptr;
 }
@@ -1331,7 +1405,8 @@ PlannedFn pick_planned(int mode, int hd, bool wide) {
 // The kernel choice and launch shape of one audit call.
 struct Launch {
   KernelFn fn = nullptr;        // the self-contained kernel (none for some VALU shapes)
-  PlannedFn planned = nullptr;  // the planned form, for the MFMA shapes
+  PlannedFn planned = nullptr;       // the planned form, for the MFMA shapes
+  PlannedFn planned_runs = nullptr;  // its form for launches of several layers
   bool valu_planned = false;    // the planned form on the VALU (ekv_audit_valu.hip), for the others
   int mode = 0, head_dim = 0;
   int threads = kThreads;
@@ -1393,7 +1468,8 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
   if (use_mfma) {
     const bool wide = tile_tokens % 64 == 0;
     L.fn = pick_mfma(mode, head_dim, wide);
-    L.planned = pick_planned(mode, head_dim, wide);
+    L.planned = pick_planned(mode, head_dim, wide, false);
+    L.planned_runs = pick_planned(mode, head_dim, wide, true);
     nsub = tile_tokens / (16 * chunk_mtiles(row_bytes, wide));  // chunks of up to 8 KB of keys
     L.threads = kCuThreads;
   } else if (planned) {
@@ -1512,12 +1588,13 @@ int launch_planned(const Launch &L, const Params &p, const LayerSet &ls, const v
   const int grid = plan_grid();
   const PlanLayout Lp = plan_layout(plan_rows, plan_width, grid);
   PlanView v;
-  v.wg = (const int2 *)((const char *)plan + Lp.wg);
+  v.wg = (const int4 *)((const char *)plan + Lp.wg);
   v.desc = (const TileDesc *)((const char *)plan + Lp.desc);
   v.cap = Lp.cap;
   if (L.planned == nullptr)
     return launch_valu_layers(L.mode, L.head_dim, p.block_size, p.group_rows, p, v, ls, grid, (hipStream_t)stream, what);
-  hipLaunchKernelGGL(L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v, ls);
+  hipLaunchKernelGGL(ls.n > 1 ? L.planned_runs : L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p,
+                     v, ls);
   return check_hip(hipGetLastError(), what);
 }
 
@@ -1578,7 +1655,7 @@ extern "C" int ekv_audit_plan(const int32_t *table, int64_t table_stride, const 
   a.block_size = block_size;
   a.grid = grid;
   a.cap = Lp.cap;
-  a.wg = (int2 *)(base + Lp.wg);
+  a.wg = (int4 *)(base + Lp.wg);
   a.first = (int32_t *)(base + Lp.first);
   a.row_off = (int32_t *)(base + Lp.row_off);
   a.desc = (TileDesc *)(base + Lp.desc);

@@ -21,6 +21,7 @@ constexpr int kCycleSlots = 64;  // per-row cycle accumulators of a round in til
 enum Mode : int { kModeF32 = 0, kModeF16 = 1, kModeBF16 = 2, kModeFp8Bf16 = 3 };
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
@@ -150,23 +151,136 @@ constexpr int kMaxGrid = 1024;  // the largest grid a plan splits its tiles over
 struct TileDesc {
   int32_t row, k, valid, qtok, id0, id1, pad0, pad1;  // valid: tokens of the tile the row reaches
 };
-static_assert(sizeof(TileDesc) == 32, "a descriptor is two 16-byte loads");
+static_assert(sizeof(TileDesc) == 32, "a descriptor is 32 bytes, 16-byte aligned");
 
 struct PlanView {
-  const int2 *wg;
+  const int4 *wg;  // per split: (tiles, first row, whole runs listed first, 0)
   const TileDesc *desc;
   int32_t cap;
 };
 
 // A descriptor into VGPRs with a vector load (the offset register keeps it one: a scalar load
 // would be waited for with the wave's LDS traffic, both being counted by lgkmcnt).
-__device__ __forceinline__ void load_desc(const TileDesc *d, u32x4 &lo, u32x4 &hi) {
+// The descriptor's first 24 bytes (the padding is not read: a load into registers the kernel
+// does not use still writes them, and the next write to such a register would wait for it)
+__device__ __forceinline__ void load_desc(const TileDesc *d, u32x4 &lo, u32x2 &hi) {
   uint32_t o = 0;
   asm volatile("" : "+v"(o));
   const char *src = reinterpret_cast<const char *>(d) + o;
-  lo = *reinterpret_cast<const u32x4 *>(src);
-  hi = *reinterpret_cast<const u32x4 *>(src + 16);
+  lo = *as_global(reinterpret_cast<const u32x4 *>(src));
+  hi = *as_global(reinterpret_cast<const u32x2 *>(src + 16));
 }
+
+// The tiles whose records share 128-byte lines: a tile records 2 blocks x `cells` floats in each
+// plane, so 16 / cells consecutive tiles of a row fill a line.  A planned launch hands its waves runs
+// of that many tiles times the audited heads (at most 8 items; a power of two of tiles, at most
+// kPlanRun, since a plan's rows and splits fall on multiples of kPlanRun), so that one wave writes
+// each line whole, at once.
+constexpr int kPlanRun = 4;
+__host__ __device__ inline int record_run_tiles(int cells, int groups) {
+  int tiles = 1;
+  while (tiles < kPlanRun && 2 * tiles * cells <= 16 && 2 * tiles * groups <= 8) tiles *= 2;
+  return tiles;
+}
+
+// A plan pads each row's tiles to a multiple of kPlanRun (padding tiles have no tokens), so that the
+// padded list's multiples of kPlanRun start runs of one row.  A split of `cnt` tiles from padded tile
+// f lists its whole runs first, then the `head` tiles before its first multiple of kPlanRun, then the
+// tail, so that a launch can hand out the runs as runs and the rest one tile at a time.
+__host__ __device__ inline int plan_split_head(int f, int cnt) {
+  const int h = (kPlanRun - f % kPlanRun) % kPlanRun;
+  return h < cnt ? h : cnt;
+}
+__host__ __device__ inline int plan_split_runs(int f, int cnt) { return (cnt - plan_split_head(f, cnt)) / kPlanRun; }
+// the place of the split's tile t (counted from f) in its list
+__host__ __device__ inline int plan_split_pos(int t, int head, int runs) {
+  const int whole = runs * kPlanRun;
+  return t < head ? whole + t : (t < head + whole ? t - head : t);
+}
+
+// The records of a wave's current run (one row's consecutive tiles of one layer, record_run_tiles),
+// held in registers until the run ends.  Records are ~1% of a launch's bytes but cost far more:
+// under the streaming key reads, every record cache line that reaches memory costs about as much as
+// several lines read, and a line stored in pieces by ordinary stores is no cheaper than one stored
+// whole.  A whole, aligned line written with a non-temporal store costs least (at the Llama-3-8B
+// decode shape the records took ~14% of the launch with a store per tile, ~10% as whole lines).
+//
+// Slot s holds the run's s-th item: in lane c * 16 + n, the tile max and sum of query n for the
+// tile's block c, and the cell's offset in floats from the row's record base (-1 where the lane has
+// no record).  When the run ends its records go out as whole lines if they are: the F records per
+// plane (F a multiple of 32, at most 128) fill the F floats from the first one's cell, which is
+// 128-byte aligned.  They then pass through the wave's LDS staging buffer into float order, and one
+// non-temporal store per plane and 64 floats writes them.  Otherwise (a row's last run, which
+// reaches past the row; a plane with more cells than the audited heads) each record is stored on its
+// own.
+template <int K>
+struct RunRecords {
+  float m[K], l[K];
+  int off[K];
+  int n;
+  float *row;  // the record base of the run's row in its layer's max plane
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int i = 0; i < K; ++i) off[i] = -1;
+    n = 0;
+  }
+  // `stage`: 256 floats of the wave's LDS (its chunk staging buffer, free between the chunk's dots
+  // and the next chunk's arrival)
+  __device__ __forceinline__ void flush(int64_t plane, float *stage) {
+    const int lane = lane_id();
+    const int off0 = __builtin_amdgcn_readlane(off[0], 0);  // slot 0, block 0, query 0
+    int F = 0;  // the records held (their cells are distinct: each is one block, head and query)
+#pragma unroll
+    for (int i = 0; i < K; ++i) F += __builtin_popcountll(__builtin_amdgcn_ballot_w64(off[i] >= 0));
+    // F distinct cells inside [off0, off0 + F) fill it
+    bool inside = true;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (off[i] >= 0 && (off[i] < off0 || off[i] - off0 >= F)) inside = false;
+    const bool lines = off0 >= 0 && F % 32 == 0 && F <= 128 && ((uintptr_t)(row + off0) & 127) == 0 &&
+                       __builtin_amdgcn_ballot_w64(!inside) == 0;
+    if (lines) {
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+        if (off[i] >= 0) {
+          stage[off[i] - off0] = m[i];
+          stage[128 + off[i] - off0] = l[i];
+        }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int f = lane + 64 * half;
+        if (f < F) {
+          __builtin_nontemporal_store(stage[f], as_global(row + off0 + f));
+          __builtin_nontemporal_store(stage[128 + f], as_global(row + plane + off0 + f));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < K; ++i)
+        if (off[i] >= 0) {
+          as_global(row)[off[i]] = m[i];
+          as_global(row)[off[i] + plane] = l[i];
+        }
+    }
+    init();
+  }
+  // the item's records; the batch is stored first if it holds another row's (a run taken where the
+  // plan has no whole runs can cross rows and layers), and after it when it holds K items (a run of
+  // more than K items: more than 8 audited heads)
+  __device__ __forceinline__ void push(float *row_base, int cell_off, float mv, float lv, int64_t plane,
+                                       float *stage) {
+    if (n > 0 && row_base != row) flush(plane, stage);
+    row = row_base;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (i == n) {
+        m[i] = mv;
+        l[i] = lv;
+        off[i] = cell_off;
+      }
+    if (++n == K) flush(plane, stage);
+  }
+};
 
 // The layers of one planned launch.  A decode step's audit launches differ only in the layer:
 // its queries, its key cache, its records and its scale.  One launch can take up to

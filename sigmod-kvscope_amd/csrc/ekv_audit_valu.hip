@@ -127,10 +127,11 @@ __global__ __launch_bounds__(kValuThreads) void tile_lse_valu_layers_kernel(cons
   const int nl = ls.n;
   auto split_of = [&](int j) { return (int)((blockIdx.x + (unsigned)j) % (unsigned)grid); };
   const uint32_t flag = __hip_atomic_load(p.flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int2 wg = plan.wg[blockIdx.x];
+  const int4 wg = plan.wg[blockIdx.x];
   int cnt = 0;  // wave 0: lane j holds layer j's split count
   if (wave == 0 && lane < nl) cnt = plan.wg[split_of(lane)].x;
-  u32x4 d_lo, d_hi;
+  u32x4 d_lo;
+  u32x2 d_hi;
   load_desc(plan.desc + (int64_t)blockIdx.x * plan.cap + min(groups == 1 ? wave : wave / groups, plan.cap - 1), d_lo,
             d_hi);
   if (flag == 0u) return;  // runtime/audit_kernel.py:64
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kValuThreads) void tile_lse_valu_layers_kernel(cons
   struct Tile {
     int row, h, k, valid, id0, id1, qtok, j;
   };
-  auto describe = [&](const u32x4 &lo, const u32x4 &hi, const Walk &w, int item) -> Tile {
+  auto describe = [&](const u32x4 &lo, const u32x2 &hi, const Walk &w, int item) -> Tile {
     Tile t;
     t.row = __builtin_amdgcn_readfirstlane((int)lo[0]);
     t.k = __builtin_amdgcn_readfirstlane((int)lo[1]);
@@ -327,7 +328,7 @@ __global__ __launch_bounds__(kValuThreads) void tile_lse_valu_layers_kernel(cons
     uint32_t qb[GP][OW], qn[GP][OW];
     load_query(qb, T, cur);
     LT A[NL], B[NL];
-    load_chunk(A, T, cur, 0);
+    if (T.valid > 0) load_chunk(A, T, cur, 0);
     int sub = 0;
     uint64_t mark = timed ? __builtin_amdgcn_s_memtime() : 0;
     // reduce the chunk in X after requesting the next one into Y; false after the wave's last chunk
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(kValuThreads) void tile_lse_valu_layers_kernel(cons
         }
       }
       if (more) {
-        load_chunk(Y, N, next, nsub_next);
+        if (N.valid > 0) load_chunk(Y, N, next, nsub_next);  // a padding tile of the plan has no keys
         if (new_query) load_query(qn, N, next);
       }
       reduce_chunk(X, qb, T, cur, sub, m_run, l_run);

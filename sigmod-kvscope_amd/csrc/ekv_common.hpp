@@ -28,6 +28,20 @@ int cu_count();
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// A pointer read out of memory (a field of an argument struct indexed at run time, a table of
+// pointers) is generic to the compiler, and its accesses become FLAT instructions.  A FLAT access
+// counts against the LDS wait counter as well as the vector-memory one, so every later wait for
+// an LDS result also waits for it: a key load issued before the LDS work of the previous chunk
+// would be waited for by that work.  These casts state that the memory is global.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T *as_global(const T *p) {
+  return (const __attribute__((address_space(1))) T *)p;
+}
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *as_global(T *p) {
+  return (__attribute__((address_space(1))) T *)p;
+}
+
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, kWave);

@@ -51,6 +51,9 @@ SHAPES = [
     (torch.bfloat16, 64, 32, 4, 8, 30, 12, 6, False, True),
     (torch.float8_e4m3fn, 128, 32, 8, 4, 40, 20, 9, False, True),
     (torch.bfloat16, 128, 16, 4, 4, 24, 20, 3, True, True),
+    # every one of 8 KV heads: runs of 8 items, held 4 (d = 128) or 8 (d = 64) at a time
+    (torch.bfloat16, 128, 16, 8, 4, 24, 20, 3, True, False),
+    (torch.float16, 64, 16, 8, 4, 20, 16, 4, True, False),
     (torch.bfloat16, 128, 16, 2, 4, 12, 10, 40, False, False),  # 40 layers: two launches of 32 and 8
 ]
 
