@@ -848,6 +848,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(const PlanArgs a) {
 }
 
 
+constexpr int kLdsBytes = 160 * 1024;  // a compute unit's LDS
+constexpr int kLayersLdsFixed = 2048;   // tile_lse_layers_kernel's LDS besides its staging and held lines
+
 // The planned form of tile_lse_cu_kernel over one or more layers: the same chunks, dots, records
 // and timer.  For layer j of the launch, workgroup b takes the plan's split (b + j) mod grid, so
 // that over the layers every workgroup's share of tiles differs from another's by at most one
@@ -879,6 +882,13 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   __shared__ int s_pref[2 * kMaxLaunchLayers + 1];
   __shared__ int s_whole[kMaxLaunchLayers];  // tiles in layer j's whole runs
   __shared__ u32x4 s_tr[NW][C::kStash];
+  // Whole record lines (32 floats per plane) of each wave's first runs, held until the wave's items
+  // are done: the lines then reach memory when few reads are left.  Each slot: the max plane's 32
+  // floats, the sum plane's 32, and the line's address; the LDS the chunk staging leaves.
+  constexpr int kHoldBytes = 64 * 4 + 8;
+  constexpr int kHold = RUNS ? (int)((kLdsBytes - kLayersLdsFixed - sizeof(u32x4) * NW * C::kStash) / (NW * kHoldBytes)) : 0;
+  __shared__ float s_hold[NW][kHold > 0 ? kHold : 1][64];
+  __shared__ float *s_hold_at[NW][kHold > 0 ? kHold : 1];
   __shared__ unsigned long long s_cycles[kCycleSlots];
 
   const int lane = lane_id();
@@ -1082,6 +1092,18 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   };
   // the chunk's tile max and sum, folded into the tile's running (m, l); at the tile's last chunk
   // its record goes into each of its blocks the row reaches (runtime/audit_kernel.py:97-109)
+  int held = 0;  // lines in this wave's hold slots
+  auto hold_line = [&](int F, float *line, const float *stage) -> bool {
+    if constexpr (kHold == 0) {
+      return false;
+    } else {
+      if (F != 32 || held >= kHold) return false;
+      s_hold[wave][held][lane] = lane < 32 ? stage[lane] : stage[128 + lane - 32];
+      if (lane == 0) s_hold_at[wave][held] = line;
+      ++held;
+      return true;
+    }
+  };
   auto reduce_chunk = [&](const f32x4_t (&acc)[MT], const Tile &T, const Layer &L, int sub, float &m_run,
                           float &l_run, RunRecords<kRecords> &rec) {
     const int tok0 = sub * CH;  // within the tile
@@ -1123,7 +1145,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
       if (c < kTileBlocks && n < G && c * bs < T.valid) off = T.h * G + blk * p.cells + n;
       float *row_base = L.lse + (int64_t)T.row * p.row_stride;
       if constexpr (RUNS) {
-        rec.push(row_base, off, m_run * kLn2, l_run, p.plane_stride, (float *)tr);
+        rec.push(row_base, off, m_run * kLn2, l_run, p.plane_stride, (float *)tr, hold_line);
       } else if (off >= 0) {
         as_global(row_base)[off] = m_run * kLn2;
         as_global(row_base)[off + p.plane_stride] = l_run;
@@ -1195,7 +1217,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
       reduce_chunk(acc, T, cur, sub, m_run, l_run, rec);
       if (timed && sub == nsub - 1 && (!more || new_query)) time_tile(T, mark);
       if constexpr (RUNS) {
-        if (!more || run_ends) rec.flush(p.plane_stride, (float *)tr);
+        if (!more || run_ends) rec.flush(p.plane_stride, (float *)tr, hold_line);
       }
       if (!more) break;
       if (new_query) {
@@ -1205,6 +1227,14 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
       T = N;
       cur = next;
       sub = nsub_next;
+    }
+  }
+  if constexpr (kHold > 0) {
+    // the held lines: lanes 0-31 the max plane's, lanes 32-63 the sum plane's
+    for (int k = 0; k < held; ++k) {
+      float *line = s_hold_at[wave][k];
+      const float v = s_hold[wave][k][lane];
+      __builtin_nontemporal_store(v, as_global(lane < 32 ? line + lane : line + p.plane_stride + (lane - 32)));
     }
   }
   if (p.cycles != nullptr) {

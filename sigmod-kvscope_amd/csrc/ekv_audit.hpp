@@ -210,7 +210,8 @@ __host__ __device__ inline int plan_split_pos(int t, int head, int runs) {
 // no record).  When the run ends its records go out as whole lines if they are: the F records per
 // plane (F a multiple of 32, at most 128) fill the F floats from the first one's cell, which is
 // 128-byte aligned.  They then pass through the wave's LDS staging buffer into float order, and one
-// non-temporal store per plane and 64 floats writes them.  Otherwise (a row's last run, which
+// non-temporal store per plane and 64 floats writes them, unless `hold` keeps them (the caller's
+// store for lines written when the launch's reads are over).  Otherwise (a row's last run, which
 // reaches past the row; a plane with more cells than the audited heads) each record is stored on its
 // own.
 template <int K>
@@ -226,7 +227,10 @@ struct RunRecords {
   }
   // `stage`: 256 floats of the wave's LDS (its chunk staging buffer, free between the chunk's dots
   // and the next chunk's arrival)
-  __device__ __forceinline__ void flush(int64_t plane, float *stage) {
+  // hold(F, line, stage): true if it keeps the F floats per plane from `line` (stage[f] the max plane's
+  // float f, stage[128 + f] the sum plane's)
+  template <class Hold>
+  __device__ __forceinline__ void flush(int64_t plane, float *stage, Hold &&hold) {
     const int lane = lane_id();
     const int off0 = __builtin_amdgcn_readlane(off[0], 0);  // slot 0, block 0, query 0
     int F = 0;  // the records held (their cells are distinct: each is one block, head and query)
@@ -246,12 +250,14 @@ struct RunRecords {
           stage[off[i] - off0] = m[i];
           stage[128 + off[i] - off0] = l[i];
         }
+      if (!hold(F, row + off0, stage)) {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int f = lane + 64 * half;
-        if (f < F) {
-          __builtin_nontemporal_store(stage[f], as_global(row + off0 + f));
-          __builtin_nontemporal_store(stage[128 + f], as_global(row + plane + off0 + f));
+        for (int half = 0; half < 2; ++half) {
+          const int f = lane + 64 * half;
+          if (f < F) {
+            __builtin_nontemporal_store(stage[f], as_global(row + off0 + f));
+            __builtin_nontemporal_store(stage[128 + f], as_global(row + plane + off0 + f));
+          }
         }
       }
     } else {
@@ -267,9 +273,10 @@ struct RunRecords {
   // the item's records; the batch is stored first if it holds another row's (a run taken where the
   // plan has no whole runs can cross rows and layers), and after it when it holds K items (a run of
   // more than K items: more than 8 audited heads)
+  template <class Hold>
   __device__ __forceinline__ void push(float *row_base, int cell_off, float mv, float lv, int64_t plane,
-                                       float *stage) {
-    if (n > 0 && row_base != row) flush(plane, stage);
+                                       float *stage, Hold &&hold) {
+    if (n > 0 && row_base != row) flush(plane, stage, hold);
     row = row_base;
 #pragma unroll
     for (int i = 0; i < K; ++i)
@@ -278,7 +285,7 @@ struct RunRecords {
         l[i] = lv;
         off[i] = cell_off;
       }
-    if (++n == K) flush(plane, stage);
+    if (++n == K) flush(plane, stage, hold);
   }
 };
 
