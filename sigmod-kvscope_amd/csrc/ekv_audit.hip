@@ -863,15 +863,16 @@ constexpr int kLayersLdsFixed = 2048;   // tile_lse_layers_kernel's LDS besides 
 // by layer; the last NW runs' worth of them and then the splits' other tiles are taken one at a
 // time, so that the waves run out of work together (a launch of one layer takes most of its items
 // so).
-template <int MODE, int HEAD_DIM, int MT, bool RUNS>
+template <int MODE, int HEAD_DIM, int MT, int MT_REF, bool RUNS>
 __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Params p, const PlanView plan,
                                                                     const LayerSet ls) {
+  static_assert(MT_REF == MT || MT_REF == 2 * MT, "a reduction chunk is one or two chunks");
   using S = MfmaShape<MODE, HEAD_DIM>;
   using C = CuShape<MODE, HEAD_DIM, MT>;
   constexpr int KS = S::kSteps, NLD = S::kLoads, CH = C::kChunk;
   constexpr int NW = C::kWaves;
   // items of a run whose records are held in registers (fewer where the shape's registers are taken)
-  constexpr int kRecords = HEAD_DIM >= 256 ? 1 : (HEAD_DIM >= 128 ? 4 : 8);
+  constexpr int kRecords = HEAD_DIM >= 256 ? 1 : 8;
   static_assert(sizeof(u32x4) * C::kStash >= 256 * sizeof(float), "the records pass through the chunk staging");
 
   __shared__ int s_next;    // the next untaken run
@@ -1093,6 +1094,7 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   // the chunk's tile max and sum, folded into the tile's running (m, l); at the tile's last chunk
   // its record goes into each of its blocks the row reaches (runtime/audit_kernel.py:97-109)
   int held = 0;  // lines in this wave's hold slots
+  float held_sc[4 * MT];  // PAIRS = 2: the scores of a reduction chunk's first half
   auto hold_line = [&](int F, float *line, const float *stage) -> bool {
     if constexpr (kHold == 0) {
       return false;
@@ -1122,14 +1124,31 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
           sc[4 * mt + e] = tok < T.valid ? acc[mt][e] * L.scale2 : -INFINITY;
         }
     }
-    float mx = sc[0];
+    // the max and sum over a reduction chunk of MT_REF M-tiles: this chunk, or with PAIRS = 2 the
+    // previous one (held in `held_sc`) and this one, in the order a chunk of MT_REF M-tiles takes
+    // them, so that the records are the same bits as the launches of one layer write
+    constexpr int PAIRS = MT_REF / MT;
+    if constexpr (PAIRS == 2) {
+      if ((sub & 1) == 0) {
 #pragma unroll
-    for (int e = 1; e < 4 * MT; ++e) mx = fmaxf(mx, sc[e]);
+        for (int e = 0; e < 4 * MT; ++e) held_sc[e] = sc[e];
+        return;
+      }
+    }
+    float all[4 * MT_REF];
+#pragma unroll
+    for (int e = 0; e < 4 * MT; ++e) {
+      if constexpr (PAIRS == 2) all[e] = held_sc[e];
+      all[4 * MT_REF - 4 * MT + e] = sc[e];
+    }
+    float mx = all[0];
+#pragma unroll
+    for (int e = 1; e < 4 * MT_REF; ++e) mx = fmaxf(mx, all[e]);
     mx = rows_max(mx);
     float sum = 0.0f;
     if (mx != -INFINITY) {
 #pragma unroll
-      for (int e = 0; e < 4 * MT; ++e) sum += __builtin_amdgcn_exp2f(sc[e] - mx);
+      for (int e = 0; e < 4 * MT_REF; ++e) sum += __builtin_amdgcn_exp2f(all[e] - mx);
     }
     sum = rows_sum(sum);
     const float M = fmaxf(m_run, mx);
@@ -1312,6 +1331,12 @@ KernelFn pick_hd(int hd, int nl, int gp) {
 
 // M-tiles per chunk: 8 KB of keys, within one tile (`wide`: a tile holds at least 64 tokens)
 constexpr int chunk_mtiles(int row_bytes, bool wide) { return row_bytes > 256 ? 1 : (row_bytes > 128 || !wide ? 2 : 4); }
+// The run form's chunks: 4 KB of keys where a chunk of 8 KB has two M-tiles or more.  A probe of the
+// launch's access pattern streams as fast with 4 KB in flight per wave (12 waves a compute unit) as
+// with 8 KB, and the LDS the smaller staging leaves holds more record lines until the reads are done.
+constexpr int runs_mtiles(int row_bytes, bool wide) {
+  return chunk_mtiles(row_bytes, wide) > 1 ? chunk_mtiles(row_bytes, wide) / 2 : 1;
+}
 
 template <int MODE, int HD>
 KernelFn pick_mfma_mt(bool wide) {
@@ -1398,13 +1423,16 @@ namespace audit {
 
 using PlannedFn = void (*)(const Params, const PlanView, const LayerSet);
 
+// (the run form's chunks, runs_mtiles, are reduced in pairs where they are half of chunk_mtiles)
 template <int MODE, int HD, bool RUNS>
 PlannedFn pick_planned_mt(bool wide) {
   constexpr int kRowBytes = MfmaShape<MODE, HD>::kRowBytes;
+  constexpr auto mtiles = RUNS ? runs_mtiles : chunk_mtiles;
   if constexpr (kRowBytes <= 128) {
-    if (wide) return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, true), RUNS>;
+    if (wide)
+      return tile_lse_layers_kernel<MODE, HD, mtiles(kRowBytes, true), chunk_mtiles(kRowBytes, true), RUNS>;
   }
-  return tile_lse_layers_kernel<MODE, HD, chunk_mtiles(kRowBytes, false), RUNS>;
+  return tile_lse_layers_kernel<MODE, HD, mtiles(kRowBytes, false), chunk_mtiles(kRowBytes, false), RUNS>;
 }
 
 template <int MODE, bool RUNS>
@@ -1437,6 +1465,7 @@ struct Launch {
   KernelFn fn = nullptr;        // the self-contained kernel (none for some VALU shapes)
   PlannedFn planned = nullptr;       // the planned form, for the MFMA shapes
   PlannedFn planned_runs = nullptr;  // its form for launches of several layers
+  int nsub_runs = 0;                 // that form's chunks per tile
   bool valu_planned = false;    // the planned form on the VALU (ekv_audit_valu.hip), for the others
   int mode = 0, head_dim = 0;
   int threads = kThreads;
@@ -1501,6 +1530,7 @@ int audit_setup(const void *q, int q_dtype, int64_t q_stride_token, int64_t q_st
     L.planned = pick_planned(mode, head_dim, wide, false);
     L.planned_runs = pick_planned(mode, head_dim, wide, true);
     nsub = tile_tokens / (16 * chunk_mtiles(row_bytes, wide));  // chunks of up to 8 KB of keys
+    L.nsub_runs = tile_tokens / (16 * runs_mtiles(row_bytes, wide));
     L.threads = kCuThreads;
   } else if (planned) {
     // the planned VALU form: lanes of 16, 8 or 4 bytes, so that a load instruction sits in a block
@@ -1623,8 +1653,13 @@ int launch_planned(const Launch &L, const Params &p, const LayerSet &ls, const v
   v.cap = Lp.cap;
   if (L.planned == nullptr)
     return launch_valu_layers(L.mode, L.head_dim, p.block_size, p.group_rows, p, v, ls, grid, (hipStream_t)stream, what);
-  hipLaunchKernelGGL(ls.n > 1 ? L.planned_runs : L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p,
-                     v, ls);
+  if (ls.n > 1) {
+    Params q = p;
+    q.nsub = L.nsub_runs;
+    hipLaunchKernelGGL(L.planned_runs, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, q, v, ls);
+  } else {
+    hipLaunchKernelGGL(L.planned, dim3(grid), dim3(kCuThreads), 0, (hipStream_t)stream, p, v, ls);
+  }
   return check_hip(hipGetLastError(), what);
 }
 
