@@ -883,12 +883,14 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
   __shared__ int s_pref[2 * kMaxLaunchLayers + 1];
   __shared__ int s_whole[kMaxLaunchLayers];  // tiles in layer j's whole runs
   __shared__ u32x4 s_tr[NW][C::kStash];
-  // Whole record lines (32 floats per plane) of each wave's first runs, held until the wave's items
-  // are done: the lines then reach memory when few reads are left.  Each slot: the max plane's 32
-  // floats, the sum plane's 32, and the line's address; the LDS the chunk staging leaves.
-  constexpr int kHoldBytes = 64 * 4 + 8;
+  // Whole record lines (32 floats per plane) of each wave's runs, held until the wave's items are
+  // done: the lines then reach memory when few reads are left.  A line's blocks pair up into tiles
+  // whose two blocks hold the same record (the line starts at a tile), so a slot keeps each pair
+  // once: 16 floats of the max plane, 16 of the sum plane, and the line's address, in the LDS the
+  // chunk staging leaves (at the Llama-3-8B shape 69 slots a wave, more than a wave has runs).
+  constexpr int kHoldBytes = 32 * 4 + 8;
   constexpr int kHold = RUNS ? (int)((kLdsBytes - kLayersLdsFixed - sizeof(u32x4) * NW * C::kStash) / (NW * kHoldBytes)) : 0;
-  __shared__ float s_hold[NW][kHold > 0 ? kHold : 1][64];
+  __shared__ float s_hold[NW][kHold > 0 ? kHold : 1][32];
   __shared__ float *s_hold_at[NW][kHold > 0 ? kHold : 1];
   __shared__ unsigned long long s_cycles[kCycleSlots];
 
@@ -1099,8 +1101,11 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
     if constexpr (kHold == 0) {
       return false;
     } else {
-      if (F != 32 || held >= kHold) return false;
-      s_hold[wave][held][lane] = lane < 32 ? stage[lane] : stage[128 + lane - 32];
+      // (cells <= 16: a line holds whole tiles, two blocks each; a line of 32 cells is one block)
+      if (F != 32 || p.cells > 16 || held >= kHold) return false;
+      // lane u < 16 keeps the max plane's float of pair u (its first block's), lane 16 + u the sum's
+      const int u = lane & 15, f = (u / p.cells) * 2 * p.cells + u % p.cells;
+      if (lane < 32) s_hold[wave][held][lane] = stage[(lane < 16 ? 0 : 128) + f];
       if (lane == 0) s_hold_at[wave][held] = line;
       ++held;
       return true;
@@ -1249,11 +1254,14 @@ __global__ __launch_bounds__(kCuThreads) void tile_lse_layers_kernel(const Param
     }
   }
   if constexpr (kHold > 0) {
-    // the held lines: lanes 0-31 the max plane's, lanes 32-63 the sum plane's
+    // the held lines: lanes 0-31 the max plane's, lanes 32-63 the sum plane's, float f of a line
+    // from its block pair's slot
+    const int f = lane & 31;
+    const int u = (f / p.cells / 2) * p.cells + f % p.cells + (lane < 32 ? 0 : 16);
     for (int k = 0; k < held; ++k) {
       float *line = s_hold_at[wave][k];
-      const float v = s_hold[wave][k][lane];
-      __builtin_nontemporal_store(v, as_global(lane < 32 ? line + lane : line + p.plane_stride + (lane - 32)));
+      const float v = s_hold[wave][k][u];
+      __builtin_nontemporal_store(v, as_global(lane < 32 ? line + f : line + p.plane_stride + f));
     }
   }
   if (p.cycles != nullptr) {
