@@ -63,7 +63,8 @@ struct State {
   // key with that prefix is kept and the later passes have nothing to rank (done_tie: in a pass
   // over the tie key, among the blocks at the gain threshold)
   int done, done_tie;
-  int arrivals, pad;  // a pass's workgroups that have flushed their histogram (0 between passes)
+  int arrivals;  // a pass's workgroups that have flushed their histogram (0 between passes)
+  int done_first;  // the select ended at the first pass: the second did not run (nor write its keeps)
 };
 
 struct RowStat {
@@ -136,27 +137,34 @@ __device__ __forceinline__ double share_of(const Params &p, const RowStat &st, i
   return share_value(st, p.scores[(int64_t)r * p.scores_stride + b]);
 }
 
-// A row's blocks b0 + kThreads u (u < U) for one thread: the scores and pinned flags loaded
-// together before any is used (one memory latency per U blocks, not per block).
-template <int U>
+// A row's blocks b0 + NT u (u < U) for one thread of NT: the scores and pinned flags loaded
+// together before any is used (one memory latency per U blocks, not per block).  PIN: the pinned
+// flags come from the caller's mask (p.pinned), else they are the row's first and last block.
+template <int U, int NT, bool PIN>
 struct BlockRun {
   double score[U];
   uint32_t pinned = 0, inside = 0;
   __device__ __forceinline__ void load(const Params &p, int r, int b0, int n) {
     const double *srow = p.scores + (int64_t)r * p.scores_stride;
-    const uint8_t *prow = p.pinned != nullptr ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
+    const uint8_t *prow = PIN ? p.pinned + (int64_t)r * p.pinned_stride : nullptr;
     uint8_t pin[U];
+    // every load issued, the blocks past the row reading its block 0 (a row holds `width` >= 1
+    // blocks): a load under a condition is followed by a wait for every load before it
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int b = b0 + u * kThreads;
-      score[u] = b < n ? srow[b] : 0.0;
-      pin[u] = (prow != nullptr && b < n) ? prow[b] : 0;
+      const int b = b0 + u * NT;
+      const int at = b < n ? b : 0;
+      const double x = srow[at];
+      score[u] = b < n ? x : 0.0;
+      if constexpr (PIN) pin[u] = prow[at];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int b = b0 + u * kThreads;
+      const int b = b0 + u * NT;
       inside |= b < n ? (1u << u) : 0u;
-      const bool pn = prow != nullptr ? pin[u] != 0 : (b == 0 || b == n - 1);
+      bool pn;
+      if constexpr (PIN) pn = pin[u] != 0;
+      else pn = b == 0 || b == n - 1;
       pinned |= (b < n && pn) ? (1u << u) : 0u;
     }
   }
@@ -165,19 +173,30 @@ constexpr int kRun = 8;  // blocks per thread per step of the per-row loops
 
 __device__ __forceinline__ double weight_of(const Params &p, int r) { return p.weights != nullptr ? p.weights[r] : 1.0; }
 
-// one wave per request: its total, its pinned and open blocks
-__global__ __launch_bounds__(kWave) void prepare_kernel(const Params p) {
-  __shared__ int s_start[kMaxLeaves], s_len[kMaxLeaves];
-  __shared__ double s_leaf[kMaxLeaves];
+// one workgroup per request: its total, its pinned and open blocks
+constexpr int kPrepThreads = 256;
+__global__ __launch_bounds__(kPrepThreads) void prepare_kernel(const Params p) {
+  __shared__ PairwiseLds s_sum;
+  __shared__ int s_red[kPrepThreads / kWave];
   const int r = blockIdx.x;
-  const int lane = lane_id();
   const int n = row_blocks(p, r);
   const double *srow = p.scores + (int64_t)r * p.scores_stride;
-  const double total = numpy_sum([&](int i) { return clamp0(srow[i]); }, n, s_start, s_len, s_leaf);
+  const double total = block_numpy_sum<kPrepThreads>([&](int i) { return clamp0(srow[i]); }, n, s_sum);
   int pinned = 0;
-  for (int b = lane; b < n; b += kWave) pinned += pinned_at(p, r, b, n) ? 1 : 0;
-  pinned = wave_sum_int(pinned);
-  if (lane == 0) {
+  if (p.pinned == nullptr) {
+    pinned = threadIdx.x == 0 ? min(n, 2) : 0;  // the first and the last block
+  } else {
+    const uint8_t *prow = p.pinned + (int64_t)r * p.pinned_stride;
+    for (int b0 = threadIdx.x; b0 < n; b0 += 8 * kPrepThreads) {
+      uint8_t f[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) f[u] = b0 + u * kPrepThreads < n ? prow[b0 + u * kPrepThreads] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pinned += f[u] != 0 ? 1 : 0;
+    }
+  }
+  pinned = block_sum<kPrepThreads>(pinned, s_red);
+  if (threadIdx.x == 0) {
     RowStat st;
     st.total = total;
     st.n = n;
@@ -263,12 +282,13 @@ __device__ __forceinline__ unsigned long long tie_key(int r, int b) {
 inline int tie_bits(int width) { return width <= (1 << 14) ? 30 : 34; }
 
 // The digit where the k_rem-th largest key lies, and the next pass's prefix, from the pass's
-// histogram: thread t holds the kBins / kThreads digits below kBins - (kBins / kThreads) t, in
-// descending order.  The histogram is read with device-coherent loads (the pass's workgroups added
+// histogram: thread t holds the kBins / NT digits below kBins - (kBins / NT) t, in
+// descending order (NT threads).  The histogram is read with device-coherent loads (the pass's workgroups added
 // into it with device-scope atomics from every XCD) and cleared for the next pass.
-__device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_pass) {
-  constexpr int kPer = kBins / kThreads;
-  __shared__ long long s_scan[kThreads / kWave];
+template <int NT>
+__device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_pass, bool first_pass) {
+  constexpr int kPer = kBins / NT;
+  __shared__ long long s_scan[NT / kWave];
   __shared__ int s_whole;
   State *s = p.state;
   const int t = threadIdx.x;
@@ -314,6 +334,7 @@ __device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_p
     s->mask |= ((1ull << bits) - 1ull) << shift;
     if (s_whole) {
       s->done = 1;
+      s->done_first = first_pass ? 1 : 0;
       s->done_tie = last_gain_pass < 0 ? 1 : 0;
     } else if (last_gain_pass > 0) {  // the gain threshold is complete: the tie passes start
       s->threshold = s->prefix;
@@ -333,6 +354,10 @@ __device__ void pick_digit(const Params &p, int shift, int bits, int last_gain_p
 // pass's digit, in p.cand; 2 (the later passes) reads that list instead of the rows, unless it
 // outgrew its capacity.
 constexpr int kCandPerRow = 1024;  // the list's room per request row
+// The passes run one workgroup of kHistThreads per CU at most (rows w, w + grid, ... each): a pass's
+// workgroups each add their histogram into the global one, and the adds to one digit from every
+// workgroup are serialised in memory, so fewer, larger workgroups end the pass sooner.
+constexpr int kHistThreads = 1024;
 
 // Workgroup w of a pass takes rows w, w + grid, ...: its region of the list holds kCandPerRow pairs
 // for each of them, after the regions of the workgroups before it.
@@ -342,15 +367,17 @@ __device__ __forceinline__ void cand_region(int rows, int w, int grid, long long
   room = kCandPerRow * (per + (w < extra ? 1 : 0));
 }
 
-template <bool TIE, int CAND_MODE>
-__global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shift, int bits, int last_gain_pass) {
+constexpr int kHistRows = 2;  // rows whose blocks a pass's workgroup loads together
+
+template <bool TIE, int CAND_MODE, bool PIN>
+__global__ __launch_bounds__(kHistThreads) void hist_kernel(const Params p, int shift, int bits, int last_gain_pass) {
   constexpr int cand_mode = CAND_MODE;
   __shared__ unsigned int s_hist[kBins];
   __shared__ int s_last;
   __shared__ unsigned int s_listed;
   State *s = p.state;
   if (s->mode != kSelect || s->error || s->done) return;
-  for (int i = threadIdx.x; i < kBins; i += kThreads) s_hist[i] = 0u;
+  for (int i = threadIdx.x; i < kBins; i += kHistThreads) s_hist[i] = 0u;
   if (threadIdx.x == 0) s_listed = 0u;
   __syncthreads();
   long long region;
@@ -389,41 +416,67 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   const unsigned int listed = cand_mode == 2 ? p.cand_count[blockIdx.x] : 0u;
   if (cand_mode == 2 && listed <= (unsigned int)room) {  // this workgroup's list (else its rows again)
     const unsigned long long *list = p.cand + 2 * region;
-    for (int c0 = 0; c0 < (int)listed; c0 += kThreads) {
+    for (int c0 = 0; c0 < (int)listed; c0 += kHistThreads) {
       const int c = c0 + threadIdx.x;
       unsigned int digit = 0u;
       const bool counted = c < (int)listed && consider(list[2 * c], list[2 * c + 1], digit);
       count(counted, digit);
     }
   } else {
-    for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
-      const RowStat st = p.row_stat[r];
-      const double weight = weight_of(p, r);
-      for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < st.n; b0 += kThreads * kRun) {
-        BlockRun<kRun> run;
-        run.load(p, r, b0, st.n);
+    // rows w, w + G, ... kHistRows at a time: every row's blocks of a step loaded before any is
+    // counted (a step's list stores then wait for no load of the same step).  The second pass also
+    // writes the keep of every block the first digit decides (pinned and past-the-row blocks 1, an
+    // open block 1 or 0 as its digit is above or below the threshold's), across the whole width, and
+    // leaves the blocks it lists to the keep kernel.
+    const int G = gridDim.x;
+    for (int r0 = blockIdx.x; r0 < p.rows; r0 += kHistRows * G) {
+      int rr[kHistRows], nmax = 0;
+      RowStat st[kHistRows];
+      double weight[kHistRows];
 #pragma unroll
-        for (int u = 0; u < kRun; ++u) {
-          const int b = b0 + u * kThreads;
-          bool counted = false;
-          unsigned int digit = 0u;
-          unsigned long long k = 0ull;
-          if (((run.inside & ~run.pinned) >> u) & 1u) {
-            k = gain_key(weight * share_value(st, run.score[u]));
-            counted = consider(k, tie_key(r, b), digit);
-          }
-          count(counted, digit);
-          if constexpr (cand_mode == 1) {  // list the counted blocks: one slot reservation (in LDS) per wave
-            const uint64_t active = __ballot(counted);
-            if (active != 0) {
-              const int first = __ffsll((long long)active) - 1;
-              unsigned int at = 0u;
-              if (lane == first) at = atomicAdd(&s_listed, (unsigned int)__popcll(active));
-              at = (unsigned int)__shfl((int)at, first) +
-                   __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0u));
-              if (counted && at < (unsigned int)room) {
-                p.cand[2 * (region + at)] = k;
-                p.cand[2 * (region + at) + 1] = tie_key(r, b);
+      for (int i = 0; i < kHistRows; ++i) {
+        const bool real = r0 + i * G < p.rows;
+        rr[i] = real ? r0 + i * G : r0;  // a row past the last reads row r0's first block, counts nothing
+        st[i] = p.row_stat[rr[i]];
+        if (!real) st[i].n = 0;
+        weight[i] = weight_of(p, rr[i]);
+        nmax = max(nmax, st[i].n);
+      }
+      const int steps_to = cand_mode == 1 ? p.width : nmax;
+      for (int c0 = 0; c0 < steps_to; c0 += kHistThreads * kRun) {
+        BlockRun<kRun, kHistThreads, PIN> run[kHistRows];
+#pragma unroll
+        for (int i = 0; i < kHistRows; ++i) run[i].load(p, rr[i], c0 + threadIdx.x, st[i].n);
+#pragma unroll
+        for (int i = 0; i < kHistRows; ++i) {
+#pragma unroll
+          for (int u = 0; u < kRun; ++u) {
+            const int b = c0 + threadIdx.x + u * kHistThreads;
+            bool counted = false;
+            unsigned int digit = 0u;
+            unsigned long long k = 0ull;
+            if (((run[i].inside & ~run[i].pinned) >> u) & 1u) {
+              k = gain_key(weight[i] * share_value(st[i], run[i].score[u]));
+              counted = consider(k, tie_key(rr[i], b), digit);
+            }
+            count(counted, digit);
+            if constexpr (cand_mode == 1) {  // list the counted blocks: one slot reservation (in LDS) per wave
+              const uint64_t active = __ballot(counted);
+              if (active != 0) {
+                const int first = __ffsll((long long)active) - 1;
+                unsigned int at = 0u;
+                if (lane == first) at = atomicAdd(&s_listed, (unsigned int)__popcll(active));
+                at = (unsigned int)__shfl((int)at, first) +
+                     __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0u));
+                if (counted && at < (unsigned int)room) {
+                  p.cand[2 * (region + at)] = k;
+                  p.cand[2 * (region + at) + 1] = tie_key(rr[i], b);
+                }
+              }
+              if (b < p.width && !counted && rr[i] == r0 + i * G) {
+                const bool open = ((run[i].inside & ~run[i].pinned) >> u) & 1u;
+                const uint8_t kv = !open || (k & mask) > prefix ? 1 : 0;
+                p.keep[(int64_t)rr[i] * p.keep_stride + b] = kv;
               }
             }
           }
@@ -434,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   __syncthreads();
   if constexpr (cand_mode == 1)
     if (threadIdx.x == 0) p.cand_count[blockIdx.x] = s_listed;  // may pass the room
-  for (int i = threadIdx.x; i < kBins; i += kThreads) {
+  for (int i = threadIdx.x; i < kBins; i += kHistThreads) {
     const unsigned int c = s_hist[i];
     if (c) __hip_atomic_fetch_add(&s->hist[i], (unsigned long long)c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -445,36 +498,56 @@ __global__ __launch_bounds__(kThreads) void hist_kernel(const Params p, int shif
   __syncthreads();
   if (!s_last) return;
   if (threadIdx.x == 0) s->arrivals = 0;
-  pick_digit(p, shift, bits, last_gain_pass);
+  pick_digit<kHistThreads>(p, shift, bits, last_gain_pass, cand_mode == 0);
 }
 
-__global__ __launch_bounds__(kThreads) void sum_keep_kernel(const Params p) {
-  const int r = blockIdx.x;
+// The keep, on the passes' grid.  When the second pass ran, it has written every keep but those of
+// the blocks it listed, and a workgroup writes its list's; otherwise (another mode, an error, a
+// select that ended at the first pass) or when its list outgrew its room, the workgroup writes every
+// block of its rows.
+template <bool PIN>
+__global__ __launch_bounds__(kHistThreads) void sum_keep_kernel(const Params p) {
   const State *s = p.state;
-  const RowStat st = p.row_stat[r];
   const int mode = s->mode;
   const bool error = s->error != 0;
   const unsigned long long threshold = s->threshold, prefix = s->prefix, mask = s->mask;
   const bool done_gain = s->done && !s->done_tie;
-  const double weight = weight_of(p, r);
-  uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
-  for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < p.width; b0 += kThreads * kRun) {
-    BlockRun<kRun> run;
-    run.load(p, r, b0, st.n);
+  auto selected = [&](unsigned long long key, unsigned long long tk) -> uint8_t {
+    if (done_gain) return (key & mask) >= prefix ? 1 : 0;  // every key from the last bucket on
+    return (key > threshold || (key == threshold && (tk & mask) >= prefix)) ? 1 : 0;
+  };
+  long long region;
+  int room;
+  cand_region(p.rows, blockIdx.x, gridDim.x, region, room);
+  const bool second_ran = mode == kSelect && !error && !s->done_first;
+  const unsigned int listed = second_ran ? p.cand_count[blockIdx.x] : 0u;
+  if (second_ran && listed <= (unsigned int)room) {
+    const unsigned long long *list = p.cand + 2 * region;
+    for (int c = threadIdx.x; c < (int)listed; c += kHistThreads) {
+      const unsigned long long key = list[2 * c], tk = list[2 * c + 1];
+      const int r = 0xFFFF - (int)(tk & 0xFFFFull), b = (int)(tk >> 16);
+      p.keep[(int64_t)r * p.keep_stride + b] = selected(key, tk);
+    }
+    return;
+  }
+  for (int r = blockIdx.x; r < p.rows; r += gridDim.x) {
+    const RowStat st = p.row_stat[r];
+    const double weight = weight_of(p, r);
+    uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
+    for (int b0 = threadIdx.x; b0 - (int)threadIdx.x < p.width; b0 += kHistThreads * kRun) {
+      BlockRun<kRun, kHistThreads, PIN> run;
+      run.load(p, r, b0, st.n);
 #pragma unroll
-    for (int u = 0; u < kRun; ++u) {
-      const int b = b0 + u * kThreads;
-      if (b >= p.width) continue;
-      uint8_t k;
-      if (error || b >= st.n || mode == kKeepAll || ((run.pinned >> u) & 1u)) k = 1;
-      else if (mode == kKeepOpen) k = 1;
-      else if (mode == kPinnedOnly) k = 0;
-      else {
-        const unsigned long long key = gain_key(weight * share_value(st, run.score[u]));
-        if (done_gain) k = (key & mask) >= prefix ? 1 : 0;  // every key from the last bucket on
-        else k = (key > threshold || (key == threshold && (tie_key(r, b) & mask) >= prefix)) ? 1 : 0;
+      for (int u = 0; u < kRun; ++u) {
+        const int b = b0 + u * kHistThreads;
+        if (b >= p.width) continue;
+        uint8_t k;
+        if (error || b >= st.n || mode == kKeepAll || ((run.pinned >> u) & 1u)) k = 1;
+        else if (mode == kKeepOpen) k = 1;
+        else if (mode == kPinnedOnly) k = 0;
+        else k = selected(gain_key(weight * share_value(st, run.score[u])), tie_key(r, b));
+        krow[b] = k;
       }
-      krow[b] = k;
     }
   }
 }
@@ -1978,29 +2051,33 @@ namespace alloc {
 // The `sum` pipeline on prepared parameters (state and row statistics in place).
 int launch_sum(Params p, hipStream_t s) {
   const int rows = p.rows;
-  hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(alloc::kPrepThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
-  const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 4));
+  const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count()));
   // the gain threshold, kDigitBits at a time from the top of the 64-bit key
   // (the second pass lists the blocks in the first pass's bucket; the later passes read that list)
+  // the kernels for the caller's pins: a mask, or each row's first and last block
+  const bool pin = p.pinned != nullptr;
+  using Pass = void (*)(alloc::Params, int, int, int);
+  const Pass first = pin ? alloc::hist_kernel<false, 0, true> : alloc::hist_kernel<false, 0, false>;
+  const Pass second = pin ? alloc::hist_kernel<false, 1, true> : alloc::hist_kernel<false, 1, false>;
+  const Pass listed = pin ? alloc::hist_kernel<false, 2, true> : alloc::hist_kernel<false, 2, false>;
+  const Pass tied = pin ? alloc::hist_kernel<true, 2, true> : alloc::hist_kernel<true, 2, false>;
   int pass = 0;
   for (int top = 64; top > 0; top -= alloc::kDigitBits, ++pass) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
     const int last = shift == 0 ? 1 : 0;
-    if (pass == 0)
-      hipLaunchKernelGGL((alloc::hist_kernel<false, 0>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
-    else if (pass == 1)
-      hipLaunchKernelGGL((alloc::hist_kernel<false, 1>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
-    else
-      hipLaunchKernelGGL((alloc::hist_kernel<false, 2>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, last);
+    const Pass kernel = pass == 0 ? first : pass == 1 ? second : listed;
+    hipLaunchKernelGGL(kernel, grid, dim3(alloc::kHistThreads), 0, s, p, shift, bits, last);
   }
   // among the blocks at the threshold: newer block, earlier request (the tie key)
   static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
   for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
-    hipLaunchKernelGGL((alloc::hist_kernel<true, 2>), grid, dim3(alloc::kThreads), 0, s, p, shift, bits, -1);
+    hipLaunchKernelGGL(tied, grid, dim3(alloc::kHistThreads), 0, s, p, shift, bits, -1);
   }
-  hipLaunchKernelGGL(alloc::sum_keep_kernel, dim3(rows), dim3(alloc::kThreads), 0, s, p);
+  hipLaunchKernelGGL(pin ? alloc::sum_keep_kernel<true> : alloc::sum_keep_kernel<false>, grid,
+                     dim3(alloc::kHistThreads), 0, s, p);
   return check_hip(hipGetLastError(), "ekv_rank_sum launch");
 }
 
@@ -2131,7 +2208,7 @@ namespace alloc {
 // The `maxmin` pipeline on prepared parameters (every workspace pointer in place).
 int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   Params &p = m.p;
-  hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(kWave), 0, s, p);
+  hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(alloc::kPrepThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const bool wide = width > alloc::kMaxWidth;
   if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);

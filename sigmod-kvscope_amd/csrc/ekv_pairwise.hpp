@@ -107,4 +107,122 @@ __device__ double numpy_sum(Get get, int n, int *s_start, int *s_len, double *s_
   return __shfl(total, 0, kWave);
 }
 
+// ---- NumPy's sum of n values get(i), by a workgroup of NT threads; every thread returns it -----
+// The same runs, leaves and combination as numpy_sum, evaluated in parallel over the recursion's
+// tree.  The tree has at most kPairDepth + 1 levels, so its nodes fit a heap of 255 entries (node v's
+// halves are 2v and 2v + 1); thread v - 1 finds node v by walking from the run down the bits of v,
+// and it is a leaf when its length is at most 128 (or it lies at the last level), absent when an
+// ancestor is a leaf.  Eight consecutive threads take a leaf of at least 8 values, thread k adding
+// values k, k + 8, ... of its first len - len % 8 in order (NumPy's eight accumulators); the
+// accumulators then combine as ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)) over lane exchanges
+// (IEEE addition commutes, so lanes k and k ^ 1 hold the same bits of a pair's sum), and thread 0 of
+// the eight adds the leaf's last len % 8 values in order (all of a leaf shorter than 8, from 0.0).
+// The inner nodes then add their halves' sums, a level at a time from the deepest.  Each thread
+// loads the values of two leaves' accumulators before it adds any, so with NT = 256 a run of 8192
+// values costs one memory latency.  get(i) is also called for i = 0 when n is 0.  Contains barriers:
+// every thread of the workgroup calls it.
+constexpr int kPairNodes = 1 << (kPairDepth + 1);  // heap slots 1 .. 255
+struct PairwiseLds {
+  int start[kMaxLeaves], len[kMaxLeaves], node_of[kMaxLeaves];
+  double node[kPairNodes];
+  int scan[16];
+};
+
+template <int NT, class Get>
+__device__ double block_numpy_sum(Get get, int n, PairwiseLds &lds) {
+  static_assert(NT % kWave == 0 && NT >= kPairNodes && NT <= 1024, "whole waves, a thread per tree node");
+  constexpr int kPer = 16;  // values per accumulator in a leaf of at most 128
+  const int t = threadIdx.x, k = t & 7;
+  const int v = t + 1;  // this thread's tree node (heap numbering), when v < kPairNodes
+  const int depth = v < kPairNodes ? 31 - __clz(v) : 0;
+  double total = 0.0;
+  for (int c0 = 0; c0 < max(n, 1); c0 += kChunk) {
+    const int run = n > 0 ? min(n - c0, kChunk) : 0;
+    // node v of this run's tree: its values [vs, vs + vlen), and whether it is a leaf or an inner node
+    int vs = c0, vlen = run;
+    bool exists = v < kPairNodes;
+    for (int i = depth - 1; i >= 0 && exists; --i) {
+      if (vlen <= 128) {
+        exists = false;  // an ancestor is a leaf
+      } else {
+        const int n2 = (vlen / 2) & ~7;
+        if ((v >> i) & 1) {
+          vs += n2;
+          vlen -= n2;
+        } else {
+          vlen = n2;
+        }
+      }
+    }
+    const bool leaf = exists && (vlen <= 128 || depth == kPairDepth);
+    const bool inner = exists && !leaf;
+    int leaves;
+    const int li = block_exclusive_scan<NT, true>(leaf ? 1 : 0, lds.scan, leaves);
+    if (leaf) {
+      lds.start[li] = vs;
+      lds.len[li] = vlen;
+      lds.node_of[li] = v;
+    }
+    lds_barrier();
+    const int chains = 8 * leaves;  // a multiple of 8: the eight threads of a leaf go together
+    for (int c = t; c < chains; c += 2 * NT) {
+      double x[2][kPer], tail[2][7];
+      int m[2], rest[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // chains c and c + NT: every load issued before any add
+        const int cc = c + h * NT;
+        const int j = cc < chains ? cc >> 3 : 0;
+        const int s = lds.start[j], len = cc < chains ? lds.len[j] : 0;
+        m[h] = len >> 3;
+        rest[h] = len - 8 * m[h];
+        // every load issued, the unused ones reading value c0 (a load under a condition is followed
+        // by a wait for every load before it)
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const double y = get(i < m[h] ? s + k + 8 * i : c0);
+          x[h][i] = i < m[h] ? y : 0.0;
+        }
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+          const bool used = k == 0 && i < rest[h];
+          const double y = get(used ? s + 8 * m[h] + i : c0);
+          tail[h][i] = used ? y : 0.0;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int cc = c + h * NT;
+        if (cc >= chains) continue;  // uniform over the eight threads of a leaf
+        double res = 0.0;
+        if (m[h] > 0) {
+          double r = x[h][0];
+#pragma unroll
+          for (int i = 1; i < kPer; ++i)
+            if (i < m[h]) r += x[h][i];
+          r = r + __shfl_xor(r, 1, kWave);
+          r = r + __shfl_xor(r, 2, kWave);
+          r = r + __shfl_xor(r, 4, kWave);
+          res = r;
+        }
+        if (k == 0) {
+#pragma unroll
+          for (int i = 0; i < 7; ++i)
+            if (i < rest[h]) res += tail[h][i];
+          lds.node[lds.node_of[cc >> 3]] = res;
+        }
+      }
+    }
+    // the inner nodes, deepest first: left half + right half, as the recursion returns them
+#pragma unroll
+    for (int d = kPairDepth - 1; d >= 0; --d) {
+      lds_barrier();
+      if (inner && depth == d) lds.node[v] = lds.node[2 * v] + lds.node[2 * v + 1];
+    }
+    lds_barrier();
+    total += lds.node[1];  // every thread adds the runs in order
+    lds_barrier();         // node 1 is read before the next run writes it
+  }
+  return total;
+}
+
 }  // namespace ekv

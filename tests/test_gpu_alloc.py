@@ -126,6 +126,25 @@ def test_sum_view_build_configuration():
         bad = sum(int((got[r, : sizes[r]].astype(bool) != want[r]).sum()) for r in range(len(sizes)))
         print(f"sum at {frac}: budget {budget}, kept {sum(int(w.sum()) for w in want)}, mismatched {bad}", flush=True)
         assert bad == 0 and int(summary[0]) == budget and int(summary[3]) == 0
+        assert all(got[r, sizes[r]:].all() for r in range(len(sizes))), "a position past a row is kept"
+
+
+def test_sum_select_ending_at_the_first_digit():
+    # the free blocks are exactly the open blocks of the top bucket of the first digit (shares near 1/k
+    # against shares 1e-10 times smaller, 33 binades apart): the select ends at the first pass, so the
+    # keep kernel writes every block itself; a budget one block larger ends it in a later pass
+    rng = np.random.default_rng(5)
+    scores, pinned = [], []
+    for n in (40, 300, 3000, 9000):
+        big = int(rng.integers(5, n - 5))
+        x = np.concatenate([1.0 + rng.random(big), 1e-10 * (1.0 + rng.random(n - big))])
+        scores.append(rng.permutation(x))
+        pinned.append(oa.default_pins(n))
+    must = sum(int(p.sum()) for p in pinned)
+    top = sum(int(((x >= 1.0) & ~p).sum()) for x, p in zip(scores, pinned))
+    for budget in (must + top, must + top + 1, must + top - 1):
+        reqs = [allocation.Request(scores=x) for x in scores]
+        assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, [1.0] * 4, budget)), budget
 
 
 def test_sum_summary_flags_a_budget_below_the_pins():
