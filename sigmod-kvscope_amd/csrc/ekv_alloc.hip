@@ -637,6 +637,24 @@ __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
   }
 }
 
+// The base with the default pins (the first and the last block): NumPy sums fewer than 8 values in
+// order from 0.0 and adds that to its 0.0 identity, so 0 + ((0 + share(0)) + share(n - 1)) for
+// n >= 2 and 0 + (0 + share(0)) for n = 1.  One thread per request.
+__global__ __launch_bounds__(kThreads) void mm_base_default_kernel(const MaxminParams m) {
+  const Params &p = m.p;
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= p.rows) return;
+  const RowStat st = p.row_stat[r];
+  double pinned = 0.0;
+  if (st.n >= 1) pinned += share_of(p, st, r, 0);
+  if (st.n >= 2) pinned += share_of(p, st, r, st.n - 1);
+  MaxminRow mr;
+  mr.base = 0.0 + pinned;
+  mr.open = st.open;
+  mr.counts = 0;
+  m.mrow[r] = mr;
+}
+
 // per request, one workgroup: its n blocks in stable descending order of their gain keys (the
 // pinned blocks keyed 0, after every open block, in block order), written as the sorted block
 // indices (vals_out) and the open blocks' shares in that order (prefix, for the totals).
@@ -1838,20 +1856,47 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const Max
   for (int r = tid; r < rows; r += kBisectThreads) m.mrow[r].counts = m.b_count[r];
 }
 
+// The keep: the first `counts` blocks of the request's sorted order marked in an LDS bitmap (rows
+// up to kKeepBits blocks; wider rows are written, then the kept blocks set, in two sweeps), then every
+// byte of the row written once.
+constexpr int kKeepBits = 1 << 16;
 __global__ __launch_bounds__(kThreads) void mm_keep_kernel(const MaxminParams m) {
+  __shared__ uint32_t s_kept[kKeepBits / 32];
   const Params &p = m.p;
   const int r = blockIdx.x;
   const State *s = p.state;
   const RowStat st = p.row_stat[r];
   const bool all = s->error != 0 || s->mode == kKeepAll || s->mode == kKeepOpen;
   uint8_t *krow = p.keep + (int64_t)r * p.keep_stride;
-  for (int b = threadIdx.x; b < p.width; b += kThreads)
-    krow[b] = (all || b >= st.n || pinned_at(p, r, b, st.n)) ? 1 : 0;
-  if (all) return;
-  __syncthreads();
-  const int counts = s->mode == kSelect ? m.mrow[r].counts : 0;
+  const int counts = (!all && s->mode == kSelect) ? m.mrow[r].counts : 0;
   const int64_t row0 = (int64_t)r * p.width;
-  for (int i = threadIdx.x; i < counts; i += kThreads) krow[m.vals_out[row0 + i]] = 1;
+  if (p.width > kKeepBits) {
+    for (int b = threadIdx.x; b < p.width; b += kThreads)
+      krow[b] = (all || b >= st.n || pinned_at(p, r, b, st.n)) ? 1 : 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < counts; i += kThreads) krow[m.vals_out[row0 + i]] = 1;
+    return;
+  }
+  const int words = (p.width + 31) / 32;
+  for (int w = threadIdx.x; w < words; w += kThreads) s_kept[w] = 0u;
+  __syncthreads();
+  for (int i0 = threadIdx.x; i0 < counts; i0 += 8 * kThreads) {  // eight loads in flight per thread
+    int b[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kThreads;
+      const int v = m.vals_out[row0 + min(i, counts - 1)];  // every load issued, none under a condition
+      b[u] = i < counts ? v : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (b[u] >= 0) atomicOr(&s_kept[b[u] >> 5], 1u << (b[u] & 31));
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < p.width; b += kThreads) {
+    const bool kept = (s_kept[b >> 5] >> (b & 31)) & 1u;
+    krow[b] = (all || b >= st.n || kept || pinned_at(p, r, b, st.n)) ? 1 : 0;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -2211,7 +2256,10 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(alloc::kPrepThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const bool wide = width > alloc::kMaxWidth;
-  if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);
+  if (p.pinned == nullptr)
+    hipLaunchKernelGGL(alloc::mm_base_default_kernel, dim3((rows + alloc::kThreads - 1) / alloc::kThreads),
+                       dim3(alloc::kThreads), 0, s, m);
+  else if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);
   else hipLaunchKernelGGL(alloc::mm_base_kernel<false>, dim3(rows), dim3(kWave), 0, s, m);
   hipLaunchKernelGGL(alloc::mm_order_kernel, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
