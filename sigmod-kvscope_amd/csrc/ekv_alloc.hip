@@ -1139,18 +1139,41 @@ __global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const Maxmin
 // + q] (the requests longest first, so a wave's chains have about the same length), each lane's loads
 // and stores being those of one instruction for all its chains.  The wave stages a chunk of each
 // request in LDS with coalesced loads (the next chunk's loads in flight meanwhile); a chain lane reads
-// two shares per 16-byte LDS read, a batch ahead of adding them, and stores two totals at a time.
+// two shares per 16-byte LDS read, a batch ahead of adding them, stores two totals at a time, and
+// leaves each batch's last total in LDS.
+//
+// A level wave per chain places the levels j / kLevels (0 < j < kLevels) of the bisection's first
+// steps in each chunk's totals while the chain wave adds the next chunk: a request's count at a
+// level is its position among its totals shifted by 2r (np.searchsorted's left side, NaN above every
+// level), so the levels are placed in increasing order, those a chunk holds being those at or below
+// its last shifted total.  A lane takes a level: a binary search of the batches' last totals finds its batch,
+// whose totals the lane adds again from the batch before (the same float64 adds in the same order, so
+// the same bits) to find the position.  (A total per element in LDS would cost the chain lanes a
+// store per two elements, which slowed them by 15%; one level wave for both chains held them back at
+// the chunks that hold most levels.)  A level wave stores each position (level_pos) and adds the count
+// into the workgroup's counts in LDS, added into level_count once at the end, so the first walk of
+// the bisection needs no pass of its own.
 constexpr int kTotalsChunk = 1024;  // values per chunk and request: 16 per lane
 constexpr int kChainBatch = 16;     // values a chain lane reads from LDS a batch ahead of adding them
 constexpr int kChainsPerWave = 2;
 constexpr int kChunkPad = kTotalsChunk + 2;  // the requests' chunks a bank apart
+constexpr int kTotalsThreads = (1 + kChainsPerWave) * kWave;  // the chain wave, then a level wave per chain
+constexpr int kBatchEnds = kTotalsChunk / kChainBatch;  // last totals of a chunk's batches
 
-__global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) {
+__global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminParams m) {
   static_assert(kTotalsChunk % kWave == 0 && kTotalsChunk % (2 * kChainBatch) == 0, "whole steps per chunk");
   constexpr int kPer = kTotalsChunk / kWave;
   constexpr int Q = kChainsPerWave;
-  __shared__ __align__(16) double s_chunk[Q * kChunkPad];
+  // by chunk parity (the level wave reads one while the chain wave fills the other): a chunk's
+  // shares, and its batches' last totals
+  __shared__ __align__(16) double s_chunk[2][Q * kChunkPad];
+  __shared__ double s_ends[2][Q * kBatchEnds];
+  __shared__ int s_count[kLevels];  // the level wave's counts of the workgroup's requests
   const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const bool chain_wave = wave == 0;
+  for (int j = threadIdx.x; j < kLevels; j += kTotalsThreads) s_count[j] = 0;
+  __syncthreads();
   int req[Q], open[Q];
   int longest = 0;
 #pragma unroll
@@ -1160,141 +1183,178 @@ __global__ __launch_bounds__(kWave) void mm_totals_kernel(const MaxminParams m) 
     open[q] = req[q] >= 0 ? m.p.row_stat[req[q]].open : 0;
     longest = max(longest, open[q]);
   }
+  const int chunks = (longest + kTotalsChunk - 1) / kTotalsChunk;
   const double *row[Q];
 #pragma unroll
   for (int q = 0; q < Q; ++q) row[q] = m.prefix + (int64_t)max(req[q], 0) * m.p.width;
-  // this lane's chain (lanes below Q): its request's row and length
+  // the chain wave: this lane's chain (lanes below Q), its request's row and length, and the chunk
+  // in registers
   const int my_open = lane < Q ? open[min(lane, Q - 1)] : 0;
   double *my_row = m.prefix + (int64_t)max(lane < Q ? req[min(lane, Q - 1)] : 0, 0) * m.p.width;
   double v[Q][kPer];
-#pragma unroll
-  for (int q = 0; q < Q; ++q)
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = j * kWave + lane;
-      v[q][j] = i < open[q] ? row[q][i] : 0.0;
-    }
-  // -0.0 + x is x for every x, so the first total is the first share itself, as in np.cumsum
-  double acc = -0.0;
-  for (int c0 = 0; c0 < longest; c0 += kTotalsChunk) {
+  if (chain_wave) {
 #pragma unroll
     for (int q = 0; q < Q; ++q)
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) s_chunk[q * kChunkPad + j * kWave + lane] = v[q][j];
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {  // the next chunk
-        const int i = c0 + kTotalsChunk + j * kWave + lane;
+      for (int j = 0; j < kPer; ++j) {
+        const int i = j * kWave + lane;
         v[q][j] = i < open[q] ? row[q][i] : 0.0;
       }
-    const int steps = min(longest - c0, kTotalsChunk);  // positions every chain lane walks
-    // positions below `whole` are inside every chain of the wave (an absent request, in the last wave,
-    // has none): their totals are stored without a test
-    int shortest = kTotalsChunk;
+  }
+  // the level wave: per request, the next level to place, the total before the chunk, and the
+  // request's shift and base
+  int next[Q];
+  double shift[Q], base[Q], before[Q];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) shortest = min(shortest, open[q] - c0);
-    const int whole = max(shortest, 0) / (2 * kChainBatch) * (2 * kChainBatch);
-    if (lane < Q) {
-      // past the lane's own length the chain adds zeros (its total stays) and stores nothing
-      const int len = min(my_open - c0, kTotalsChunk);
-      const double2 *pair = reinterpret_cast<const double2 *>(s_chunk + lane * kChunkPad);
-      double2 *out = reinterpret_cast<double2 *>(my_row + c0);
-      constexpr int kPairs = kChainBatch / 2;
-      auto read = [&](double2 (&x)[kPairs], int first) {  // a batch from `first`, or a dummy past the chunk
-        const int at = first < kTotalsChunk ? first / 2 : 0;
+  for (int q = 0; q < Q; ++q) {
+    next[q] = 1;
+    before[q] = -0.0;
+    shift[q] = 2.0 * (double)max(req[q], 0);
+    base[q] = (!chain_wave && req[q] >= 0) ? m.mrow[req[q]].base : 0.0;
+  }
+  // -0.0 + x is x for every x, so the first total is the first share itself, as in np.cumsum
+  double acc = -0.0;
+  for (int it = 0; it <= chunks; ++it) {
+    if (chain_wave && it < chunks) {
+      const int c0 = it * kTotalsChunk;
+      double *buf = s_chunk[it & 1];
 #pragma unroll
-        for (int k = 0; k < kPairs; ++k) x[k] = pair[at + k];
-      };
-      auto add = [&](double2 (&x)[kPairs], int first, bool test) {
+      for (int q = 0; q < Q; ++q)
 #pragma unroll
-        for (int k = 0; k < kPairs; ++k) {
-          acc += x[k].x;
-          x[k].x = acc;
-          acc += x[k].y;
-          x[k].y = acc;
+        for (int j = 0; j < kPer; ++j) buf[q * kChunkPad + j * kWave + lane] = v[q][j];
+      // the chain lanes read what every lane of the wave wrote
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {  // the next chunk
+          const int i = c0 + kTotalsChunk + j * kWave + lane;
+          v[q][j] = i < open[q] ? row[q][i] : 0.0;
         }
+      const int steps = min(longest - c0, kTotalsChunk);  // positions every chain lane walks
+      // positions below `whole` are inside every chain of the wave (an absent request, in the last
+      // wave, has none): their totals are stored without a test
+      int shortest = kTotalsChunk;
 #pragma unroll
-        for (int k = 0; k < kPairs; ++k) {
-          const int i = first + 2 * k;
-          if (!test) {
-            out[i / 2] = x[k];
-          } else {
-            if (i < len) my_row[c0 + i] = x[k].x;
-            if (i + 1 < len) my_row[c0 + i + 1] = x[k].y;
+      for (int q = 0; q < Q; ++q) shortest = min(shortest, open[q] - c0);
+      const int whole = max(shortest, 0) / (2 * kChainBatch) * (2 * kChainBatch);
+      if (lane < Q) {
+        // past the lane's own length the chain adds zeros (its total stays) and stores nothing to memory
+        const int len = min(my_open - c0, kTotalsChunk);
+        const double2 *pair = reinterpret_cast<const double2 *>(buf + lane * kChunkPad);
+        double *ends = s_ends[it & 1] + lane * kBatchEnds;
+        double2 *out = reinterpret_cast<double2 *>(my_row + c0);
+        constexpr int kPairs = kChainBatch / 2;
+        auto read = [&](double2 (&x)[kPairs], int first) {  // a batch from `first`, or a dummy past the chunk
+          const int at = first < kTotalsChunk ? first / 2 : 0;
+#pragma unroll
+          for (int k = 0; k < kPairs; ++k) x[k] = pair[at + k];
+        };
+        auto add = [&](double2 (&x)[kPairs], int first, bool test) {
+#pragma unroll
+          for (int k = 0; k < kPairs; ++k) {
+            acc += x[k].x;
+            x[k].x = acc;
+            acc += x[k].y;
+            x[k].y = acc;
           }
+          ends[first / kChainBatch] = acc;
+#pragma unroll
+          for (int k = 0; k < kPairs; ++k) {
+            const int i = first + 2 * k;
+            if (!test) {
+              out[i / 2] = x[k];
+            } else {
+              if (i < len) my_row[c0 + i] = x[k].x;
+              if (i + 1 < len) my_row[c0 + i + 1] = x[k].y;
+            }
+          }
+        };
+        double2 xa[kPairs], xb[kPairs];
+        read(xa, 0);
+        int i = 0;
+        for (; i < whole; i += 2 * kChainBatch) {
+          read(xb, i + kChainBatch);
+          add(xa, i, false);
+          read(xa, i + 2 * kChainBatch);
+          add(xb, i + kChainBatch, false);
         }
-      };
-      double2 xa[kPairs], xb[kPairs];
-      read(xa, 0);
-      int i = 0;
-      for (; i < whole; i += 2 * kChainBatch) {
-        read(xb, i + kChainBatch);
-        add(xa, i, false);
-        read(xa, i + 2 * kChainBatch);
-        add(xb, i + kChainBatch, false);
+        for (; i < steps; i += 2 * kChainBatch) {
+          read(xb, i + kChainBatch);
+          add(xa, i, true);
+          read(xa, i + 2 * kChainBatch);
+          add(xb, i + kChainBatch, true);
+        }
       }
-      for (; i < steps; i += 2 * kChainBatch) {
-        read(xb, i + kChainBatch);
-        add(xa, i, true);
-        read(xa, i + 2 * kChainBatch);
-        add(xb, i + kChainBatch, true);
+    } else if (!chain_wave && it >= 1) {
+      // the previous chunk's totals: place every level at or below its last shifted total
+      const int c0 = (it - 1) * kTotalsChunk;
+      const double *buf = s_chunk[(it - 1) & 1];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int len = min(open[q] - c0, kTotalsChunk);
+        if (q != wave - 1 || req[q] < 0 || len <= 0) continue;  // level wave q + 1 takes chain q
+        const double *share = buf + q * kChunkPad;
+        const double *ends = s_ends[(it - 1) & 1] + q * kBatchEnds;
+        const int nb = (len + kChainBatch - 1) / kChainBatch;  // past len a chain adds zeros: the last
+        const double last = ends[nb - 1] + shift[q];          // batch ends on the total at len - 1
+        while (next[q] < kLevels) {
+          const int j = next[q] + lane;
+          const double need = (double)j / kLevels - base[q];
+          const double target = (need - 1e-12) + shift[q];
+          const bool here = j < kLevels && !(last < target);  // the lanes that hold one: a prefix of the wave
+          if (here) {
+            int lo = 0, hi = nb - 1;  // the first batch whose last shifted total is not below the target
+            while (lo < hi) {
+              const int mid = (lo + hi) >> 1;
+              if (ends[mid] + shift[q] < target) lo = mid + 1;
+              else hi = mid;
+            }
+            // the batch's totals again, from the total before it: the first not below the target
+            double t = lo > 0 ? ends[lo - 1] : before[q];
+            int pos = kChainBatch - 1;
+            bool found = false;
+#pragma unroll
+            for (int k = 0; k < kChainBatch; ++k) {
+              t += share[lo * kChainBatch + k];
+              if (!found && !(t + shift[q] < target)) {
+                pos = k;
+                found = true;
+              }
+            }
+            pos += c0 + lo * kChainBatch;
+            set_pos(m, m.level_pos, req[q], j, pos);
+            const int count = need <= 1e-12 ? 0 : min(pos + 1, open[q]);
+            if (count > 0) atomicAdd(&s_count[j], count);
+          }
+          const int placed = __popcll(__ballot(here));
+          next[q] += placed;
+          if (placed < kWave) break;
+        }
+        before[q] = ends[kBatchEnds - 1];  // the total before the next chunk (this one was whole if it has one)
       }
     }
-    __syncthreads();  // the chain lanes' reads of the chunk are done before it is refilled
+    lds_barrier();  // a parity's totals are read before the chain wave refills it
   }
-}
-
-// per request, one workgroup: its position and count at every level j / kLevels, the counts added
-// into level_count.  A count is the bisection's (its position among the request's shifted totals,
-// found on the totals staged in LDS), so the first kLevelBits steps of the bisection become a walk
-// over the summed counts, with every CU searching here rather than the bisection's one workgroup, and
-// the positions give the brackets that those steps leave.
-constexpr int kLevelThreads = 256;
-
-template <int CAP>  // CAP 0: the totals are searched in memory (requests wider than LDS holds)
-__global__ __launch_bounds__(kLevelThreads) void mm_levels_kernel(const MaxminParams m) {
-  constexpr int kMine = (kLevels + kLevelThreads - 1) / kLevelThreads;  // levels per thread
-  __shared__ double s_lds[CAP > 0 ? CAP : 1];  // the request's running totals
-  // a workgroup takes requests blockIdx.x, + gridDim.x, ... and adds its counts once per level
-  int mine[kMine];
+  if (!chain_wave) {  // the levels above every total: position `open`, count `open`
 #pragma unroll
-  for (int i = 0; i < kMine; ++i) mine[i] = 0;
-  for (int r = blockIdx.x; r < m.p.rows; r += gridDim.x) {
-  __syncthreads();  // the previous request's searches are done before its totals are replaced
-  const MaxminRow mr = m.mrow[r];
-  const int open = mr.open;
-  const double *pre = m.prefix + (int64_t)r * m.p.width;
-  if constexpr (CAP > 0) {
-    for (int i = threadIdx.x; i < open; i += kLevelThreads) s_lds[i] = pre[i];
+    for (int q = 0; q < Q; ++q) {
+      if (q != wave - 1 || req[q] < 0) continue;
+      for (int j = next[q] + lane; j < kLevels; j += kWave) {
+        set_pos(m, m.level_pos, req[q], j, open[q]);
+        const double need = (double)j / kLevels - base[q];
+        const int count = need <= 1e-12 ? 0 : open[q];
+        if (count > 0) atomicAdd(&s_count[j], count);
+      }
+    }
   }
-  const double *s_tot = CAP > 0 ? s_lds : pre;
   __syncthreads();
-  const double shift = 2.0 * (double)r;
-
-#pragma unroll
-  for (int i = 0; i < kMine; ++i) {
-    const int j = i * kLevelThreads + threadIdx.x;
-    if (j < 1 || j >= kLevels) continue;
-    const double level = (double)j / kLevels;
-    const double need = level - mr.base;
-    const double q = (need - 1e-12) + shift;
-    int a = 0, b = open;
-    while (a < b) {  // first position whose shifted total is >= q
-      const int c = (a + b) >> 1;
-      if (s_tot[c] + shift < q) a = c + 1; else b = c;
-    }
-    set_pos(m, m.level_pos, r, j, a);
-    mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
-  }
-  }
-#pragma unroll
-  for (int i = 0; i < kMine; ++i) {  // integer sums: the order does not matter
-    const int j = i * kLevelThreads + threadIdx.x;
-    if (j >= 1 && j < kLevels && mine[i] > 0) atomicAdd(&m.level_count[j], mine[i]);
-  }
+  for (int j = threadIdx.x; j < kLevels; j += kTotalsThreads)
+    if (s_count[j] > 0) atomicAdd(&m.level_count[j], s_count[j]);
 }
+
+constexpr int kLevelThreads = 256;  // the second level-count pass's workgroups
 
 // The first kLevelBits steps of the bisection over counts summed at kLevels levels: [jl, jh] of
 // those levels, jh = jl + 1 (the same decisions: a level rises when its count fits the free blocks).
@@ -1311,10 +1371,15 @@ __device__ __forceinline__ void walk_levels(const int *s_level, long long free_b
 // first walk (the summed counts staged in LDS), then counts each of its requests at the levels
 // low + j / kLevels^2 (0 < j < kLevels) inside the walk's bracket [low, high] -- exactly the mids
 // the bisection's next steps visit -- searching only between the request's positions at low and
-// high from the first pass.
+// high from the first pass.  That range of the request's totals is staged in LDS first with coalesced
+// loads (up to kStaged of them; a wider range is searched in memory), so a search waits on one load
+// rather than on each of its steps.
+constexpr int kStaged = 6144;  // totals of a request's bracket staged in LDS (48 KB)
+
 __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminParams m) {
   constexpr int kMine = (kLevels + kLevelThreads - 1) / kLevelThreads;
   __shared__ int s_level[kLevels];
+  __shared__ double s_tot[kStaged];
   const Params &p = m.p;
   const State *s = p.state;
   if (s->mode != kSelect || s->error) return;
@@ -1334,6 +1399,20 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
     const int hi0 = jh < kLevels ? pos_at(m, m.level_pos, r, jh) : open;
     const double *pre = m.prefix + (int64_t)r * p.width;
     const double shift = 2.0 * (double)r;
+    const int span = hi0 - lo0;
+    const bool staged = span <= kStaged;
+    __syncthreads();  // the previous request's searches are done with s_tot
+    if (staged) {
+      for (int i0 = threadIdx.x; i0 < span; i0 += 8 * kLevelThreads) {
+        double x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = pre[lo0 + min(i0 + u * kLevelThreads, span - 1)];  // no load under a condition
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i0 + u * kLevelThreads < span) s_tot[i0 + u * kLevelThreads] = x[u];
+      }
+    }
+    __syncthreads();
 
 #pragma unroll
     for (int i = 0; i < kMine; ++i) {
@@ -1343,9 +1422,16 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
       const double need = level - mr.base;
       const double q = (need - 1e-12) + shift;
       int a = lo0, b = hi0;
-      while (a < b) {  // first position whose shifted total is >= q
-        const int c = (a + b) >> 1;
-        if (pre[c] + shift < q) a = c + 1; else b = c;
+      if (staged) {
+        while (a < b) {  // first position whose shifted total is >= q
+          const int c = (a + b) >> 1;
+          if (s_tot[c - lo0] + shift < q) a = c + 1; else b = c;
+        }
+      } else {
+        while (a < b) {
+          const int c = (a + b) >> 1;
+          if (pre[c] + shift < q) a = c + 1; else b = c;
+        }
       }
       set_pos(m, m.level_pos2, r, j, a);
       mine[i] += need <= 1e-12 ? 0 : min(a + 1, open);
@@ -2275,17 +2361,8 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
   hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3((rows + alloc::kChainsPerWave - 1) / alloc::kChainsPerWave),
-                     dim3(kWave), 0, s, m);
+                     dim3(alloc::kTotalsThreads), 0, s, m);
   const dim3 level_grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 2));
-  if (wide)
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<0>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
-  else if (width <= 4096)
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<4096>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
-  else if (width <= 8192)
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<8192>, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
-  else
-    hipLaunchKernelGGL(alloc::mm_levels_kernel<alloc::kMaxWidth>, level_grid, dim3(alloc::kLevelThreads), 0, s,
-                       m);
   hipLaunchKernelGGL(alloc::mm_levels2_kernel, level_grid, dim3(alloc::kLevelThreads), 0, s, m);
   if (rows > alloc::kMaxMaxminRegRows)
     hipLaunchKernelGGL(alloc::mm_bisect_mem_kernel, dim3(1), dim3(alloc::kBisectThreads), 0, s, m);
