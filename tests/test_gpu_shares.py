@@ -125,7 +125,7 @@ def test_device_share_source_reads_only_live_rows(tmp_path, monkeypatch):
 
 @pytest.mark.parametrize("aggregate", ["mean", "max"])
 @pytest.mark.parametrize("layers,cells,width", [(1, 4, 300), (5, 4, 300), (32, 4, 300), (32, 4, 200), (9, 4, 700),
-                                                (3, 4, 1000), (7, 5, 300), (4, 4, 1100)])
+                                                (3, 4, 1000), (7, 5, 300), (4, 4, 1100), (12, 4, 400), (32, 4, 512)])
 def test_split_form_matches_the_whole_row_form_and_the_oracle(layers, cells, width, aggregate):
     # ekv_tile_shares_ws spreads a row's layers over several workgroups and combines their partial
     # sums (in registers for quads of 4 cells up to 1024 blocks, re-reading the records otherwise);
