@@ -1139,8 +1139,11 @@ __global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const Maxmin
 // + q] (the requests longest first, so a wave's chains have about the same length), each lane's loads
 // and stores being those of one instruction for all its chains.  The wave stages a chunk of each
 // request in LDS with coalesced loads (the next chunk's loads in flight meanwhile); a chain lane reads
-// two shares per 16-byte LDS read, a batch ahead of adding them, stores two totals at a time, and
-// leaves each batch's last total in LDS.
+// two shares per 16-byte LDS read, a batch ahead of adding them, and leaves only each batch's last
+// total in LDS.  A level wave per chain (below) adds each batch of the chunk again from the total
+// before it (one lane a batch; the same float64 adds in the same order, so the same bits) and stores
+// the totals with whole-wave stores: a store per two elements from the chain lane had cost 19 µs of
+// its ~105.
 //
 // A level wave per chain places the levels j / kLevels (0 < j < kLevels) of the bisection's first
 // steps in each chunk's totals while the chain wave adds the next chunk: a request's count at a
@@ -1189,8 +1192,6 @@ __global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminP
   for (int q = 0; q < Q; ++q) row[q] = m.prefix + (int64_t)max(req[q], 0) * m.p.width;
   // the chain wave: this lane's chain (lanes below Q), its request's row and length, and the chunk
   // in registers
-  const int my_open = lane < Q ? open[min(lane, Q - 1)] : 0;
-  double *my_row = m.prefix + (int64_t)max(lane < Q ? req[min(lane, Q - 1)] : 0, 0) * m.p.width;
   double v[Q][kPer];
   if (chain_wave) {
 #pragma unroll
@@ -1233,58 +1234,31 @@ __global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminP
           v[q][j] = i < open[q] ? row[q][i] : 0.0;
         }
       const int steps = min(longest - c0, kTotalsChunk);  // positions every chain lane walks
-      // positions below `whole` are inside every chain of the wave (an absent request, in the last
-      // wave, has none): their totals are stored without a test
-      int shortest = kTotalsChunk;
-#pragma unroll
-      for (int q = 0; q < Q; ++q) shortest = min(shortest, open[q] - c0);
-      const int whole = max(shortest, 0) / (2 * kChainBatch) * (2 * kChainBatch);
       if (lane < Q) {
-        // past the lane's own length the chain adds zeros (its total stays) and stores nothing to memory
-        const int len = min(my_open - c0, kTotalsChunk);
+        // past the request's length the chain adds zeros (its total stays)
         const double2 *pair = reinterpret_cast<const double2 *>(buf + lane * kChunkPad);
         double *ends = s_ends[it & 1] + lane * kBatchEnds;
-        double2 *out = reinterpret_cast<double2 *>(my_row + c0);
         constexpr int kPairs = kChainBatch / 2;
         auto read = [&](double2 (&x)[kPairs], int first) {  // a batch from `first`, or a dummy past the chunk
           const int at = first < kTotalsChunk ? first / 2 : 0;
 #pragma unroll
           for (int k = 0; k < kPairs; ++k) x[k] = pair[at + k];
         };
-        auto add = [&](double2 (&x)[kPairs], int first, bool test) {
+        auto add = [&](const double2 (&x)[kPairs], int first) {
 #pragma unroll
           for (int k = 0; k < kPairs; ++k) {
             acc += x[k].x;
-            x[k].x = acc;
             acc += x[k].y;
-            x[k].y = acc;
           }
           ends[first / kChainBatch] = acc;
-#pragma unroll
-          for (int k = 0; k < kPairs; ++k) {
-            const int i = first + 2 * k;
-            if (!test) {
-              out[i / 2] = x[k];
-            } else {
-              if (i < len) my_row[c0 + i] = x[k].x;
-              if (i + 1 < len) my_row[c0 + i + 1] = x[k].y;
-            }
-          }
         };
         double2 xa[kPairs], xb[kPairs];
         read(xa, 0);
-        int i = 0;
-        for (; i < whole; i += 2 * kChainBatch) {
+        for (int i = 0; i < steps; i += 2 * kChainBatch) {
           read(xb, i + kChainBatch);
-          add(xa, i, false);
+          add(xa, i);
           read(xa, i + 2 * kChainBatch);
-          add(xb, i + kChainBatch, false);
-        }
-        for (; i < steps; i += 2 * kChainBatch) {
-          read(xb, i + kChainBatch);
-          add(xa, i, true);
-          read(xa, i + 2 * kChainBatch);
-          add(xb, i + kChainBatch, true);
+          add(xb, i + kChainBatch);
         }
       }
     } else if (!chain_wave && it >= 1) {
@@ -1299,6 +1273,27 @@ __global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminP
         const double *ends = s_ends[(it - 1) & 1] + q * kBatchEnds;
         const int nb = (len + kChainBatch - 1) / kChainBatch;  // past len a chain adds zeros: the last
         const double last = ends[nb - 1] + shift[q];          // batch ends on the total at len - 1
+        {  // the totals: lane b adds batch b again from the total before it and stores those inside len
+          static_assert(kBatchEnds == kWave, "a lane per batch of a chunk");
+          const int b = lane;
+          double t = b > 0 ? ends[b - 1] : before[q];
+          double tot[kChainBatch];
+#pragma unroll
+          for (int k = 0; k < kChainBatch; ++k) {
+            t += share[b * kChainBatch + k];
+            tot[k] = t;
+          }
+          double *dst = m.prefix + (int64_t)req[q] * m.p.width + c0 + b * kChainBatch;
+          if ((b + 1) * kChainBatch <= len) {
+#pragma unroll
+            for (int k = 0; k < kChainBatch; k += 2)
+              *reinterpret_cast<double2 *>(dst + k) = double2{tot[k], tot[k + 1]};
+          } else {
+#pragma unroll
+            for (int k = 0; k < kChainBatch; ++k)
+              if (b * kChainBatch + k < len) dst[k] = tot[k];
+          }
+        }
         while (next[q] < kLevels) {
           const int j = next[q] + lane;
           const double need = (double)j / kLevels - base[q];
