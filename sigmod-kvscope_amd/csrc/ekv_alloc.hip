@@ -210,14 +210,15 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_kernel(const Params p) {
 // the requests' pinned, existing and open blocks, summed over the rows' statistics by one
 // workgroup, then the budget's mode (allocation.py:57-76) and the select's start; the state
 // (histogram, flags, counters) is cleared first
-__global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
-  __shared__ long long s_red[3][kThreads / kWave];
+template <int NT>
+__device__ void decide(const Params &p) {
+  __shared__ long long s_red[3][NT / kWave];
   {
     unsigned long long *w = (unsigned long long *)p.state;
-    for (int i = threadIdx.x; i < (int)(sizeof(State) / 8); i += kThreads) w[i] = 0ull;
+    for (int i = threadIdx.x; i < (int)(sizeof(State) / 8); i += NT) w[i] = 0ull;
   }
   long long v[3] = {0, 0, 0};  // must, sizes, open_total
-  for (int r = threadIdx.x; r < p.rows; r += kThreads) {
+  for (int r = threadIdx.x; r < p.rows; r += NT) {
     const RowStat st = p.row_stat[r];
     v[0] += st.pinned;
     v[1] += st.n;
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
     v[k] = 0;
-    for (int w = 0; w < kThreads / kWave; ++w) v[k] += s_red[k][w];
+    for (int w = 0; w < NT / kWave; ++w) v[k] += s_red[k][w];
   }
   State *s = p.state;
   s->must = v[0];
@@ -270,6 +271,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) {
     p.summary[5] = free_blocks;
   }
 }
+__global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) { decide<kThreads>(p); }
 
 // the select's two keys of an open block
 __device__ __forceinline__ unsigned long long key_at(const Params &p, const RowStat &st, int r, int b) {
@@ -639,11 +641,9 @@ __global__ __launch_bounds__(kWave) void mm_base_kernel(const MaxminParams m) {
 
 // The base with the default pins (the first and the last block): NumPy sums fewer than 8 values in
 // order from 0.0 and adds that to its 0.0 identity, so 0 + ((0 + share(0)) + share(n - 1)) for
-// n >= 2 and 0 + (0 + share(0)) for n = 1.  One thread per request.
-__global__ __launch_bounds__(kThreads) void mm_base_default_kernel(const MaxminParams m) {
+// n >= 2 and 0 + (0 + share(0)) for n = 1.
+__device__ __forceinline__ void base_default(const MaxminParams &m, int r) {
   const Params &p = m.p;
-  const int r = blockIdx.x * kThreads + threadIdx.x;
-  if (r >= p.rows) return;
   const RowStat st = p.row_stat[r];
   double pinned = 0.0;
   if (st.n >= 1) pinned += share_of(p, st, r, 0);
@@ -892,7 +892,8 @@ __device__ __forceinline__ void sort_request(const MaxminParams &m, const RowSta
 constexpr int kOrderStep = 256;
 constexpr int kOrderClasses = kMaxWidth / kOrderStep + 1;
 
-__global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminParams m) {
+// The requests longest first (by classes of kOrderStep blocks), for the totals' pairs of chains.
+__device__ void order_requests(const MaxminParams &m) {
   __shared__ int s_count[kOrderClasses], s_next[kOrderClasses];
   const int tid = threadIdx.x;
   const int rows = m.p.rows;
@@ -914,6 +915,16 @@ __global__ __launch_bounds__(kSortThreads) void mm_order_kernel(const MaxminPara
   }
   __syncthreads();
   for (int r = tid; r < rows; r += kSortThreads) m.order[atomicAdd(&s_next[cls(r)], 1)] = r;
+}
+
+// One workgroup before the sort: the requests' order, then (with the default pins) every request's
+// base, then the budget's mode and the select's state (decide; its thread 0 finishes last).
+template <bool DEFAULT_PINS>
+__global__ __launch_bounds__(kSortThreads) void mm_plan_kernel(const MaxminParams m) {
+  order_requests(m);
+  if constexpr (DEFAULT_PINS)
+    for (int r = threadIdx.x; r < m.p.rows; r += kSortThreads) base_default(m, r);
+  decide<kSortThreads>(m.p);
 }
 
 // Two 16-wave sorting workgroups share a CU where their LDS allows it (sorts of up to 8192 blocks take
@@ -1398,14 +1409,18 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
     const bool staged = span <= kStaged;
     __syncthreads();  // the previous request's searches are done with s_tot
     if (staged) {
-      for (int i0 = threadIdx.x; i0 < span; i0 += 8 * kLevelThreads) {
-        double x[8];
+      // the whole bracket in one batch of loads (none under a condition), 6 or 24 a thread
+      auto stage = [&](auto batch) {
+        constexpr int B = decltype(batch)::value;
+        double x[B];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = pre[lo0 + min(i0 + u * kLevelThreads, span - 1)];  // no load under a condition
+        for (int u = 0; u < B; ++u) x[u] = pre[lo0 + min((int)threadIdx.x + u * kLevelThreads, span - 1)];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (i0 + u * kLevelThreads < span) s_tot[i0 + u * kLevelThreads] = x[u];
-      }
+        for (int u = 0; u < B; ++u)
+          if ((int)threadIdx.x + u * kLevelThreads < span) s_tot[threadIdx.x + u * kLevelThreads] = x[u];
+      };
+      if (span <= kStaged / 4) stage(std::integral_constant<int, kStaged / 4 / kLevelThreads>());
+      else stage(std::integral_constant<int, kStaged / kLevelThreads>());
     }
     __syncthreads();
 
@@ -1961,16 +1976,17 @@ __global__ __launch_bounds__(kThreads) void mm_keep_kernel(const MaxminParams m)
   const int words = (p.width + 31) / 32;
   for (int w = threadIdx.x; w < words; w += kThreads) s_kept[w] = 0u;
   __syncthreads();
-  for (int i0 = threadIdx.x; i0 < counts; i0 += 8 * kThreads) {  // eight loads in flight per thread
-    int b[8];
+  constexpr int kLoads = 8;  // loads in flight per thread
+  for (int i0 = threadIdx.x; i0 < counts; i0 += kLoads * kThreads) {
+    int b[kLoads];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kLoads; ++u) {
       const int i = i0 + u * kThreads;
       const int v = m.vals_out[row0 + min(i, counts - 1)];  // every load issued, none under a condition
       b[u] = i < counts ? v : -1;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kLoads; ++u)
       if (b[u] >= 0) atomicOr(&s_kept[b[u] >> 5], 1u << (b[u] & 31));
   }
   __syncthreads();
@@ -2335,14 +2351,14 @@ namespace alloc {
 int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
   Params &p = m.p;
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(alloc::kPrepThreads), 0, s, p);
-  hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const bool wide = width > alloc::kMaxWidth;
-  if (p.pinned == nullptr)
-    hipLaunchKernelGGL(alloc::mm_base_default_kernel, dim3((rows + alloc::kThreads - 1) / alloc::kThreads),
-                       dim3(alloc::kThreads), 0, s, m);
-  else if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);
-  else hipLaunchKernelGGL(alloc::mm_base_kernel<false>, dim3(rows), dim3(kWave), 0, s, m);
-  hipLaunchKernelGGL(alloc::mm_order_kernel, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
+  if (p.pinned == nullptr) {
+    hipLaunchKernelGGL(alloc::mm_plan_kernel<true>, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
+  } else {
+    hipLaunchKernelGGL(alloc::mm_plan_kernel<false>, dim3(1), dim3(alloc::kSortThreads), 0, s, m);
+    if (wide) hipLaunchKernelGGL(alloc::mm_base_kernel<true>, dim3(rows), dim3(kWave), 0, s, m);
+    else hipLaunchKernelGGL(alloc::mm_base_kernel<false>, dim3(rows), dim3(kWave), 0, s, m);
+  }
   int rc = check_hip(hipGetLastError(), "ekv_rank_maxmin launch");
   if (rc != EKV_OK) return rc;
   if (wide) {
