@@ -1364,13 +1364,17 @@ constexpr int kLevelThreads = 256;  // the second level-count pass's workgroups
 
 // The first kLevelBits steps of the bisection over counts summed at kLevels levels: [jl, jh] of
 // those levels, jh = jl + 1 (the same decisions: a level rises when its count fits the free blocks).
+// A count never falls as the level rises (each request's count is 0 until its need passes 1e-12,
+// then its position plus one, which only grows), so the steps end at jl = the number of levels
+// 0 < j < kLevels whose count fits, which the workgroup counts at once rather than in ten dependent
+// steps.  Contains barriers: every thread calls it.
+template <int NT>
 __device__ __forceinline__ void walk_levels(const int *s_level, long long free_blocks, int &jl, int &jh) {
-  jl = 0;
-  jh = kLevels;
-  for (int it = 0; it < kLevelBits; ++it) {
-    const int jm = (jl + jh) >> 1;
-    if ((long long)s_level[jm] <= free_blocks) jl = jm; else jh = jm;
-  }
+  __shared__ int s_fit[NT / kWave];
+  int fit = 0;
+  for (int j = threadIdx.x; j < kLevels; j += NT) fit += (j >= 1 && (long long)s_level[j] <= free_blocks) ? 1 : 0;
+  jl = block_sum<NT>(fit, s_fit);
+  jh = jl + 1;
 }
 
 // The second level-count pass: the next kLevelBits steps the same way.  Every workgroup repeats the
@@ -1392,7 +1396,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
   for (int j = threadIdx.x; j < kLevels; j += kLevelThreads) s_level[j] = m.level_count[j];
   __syncthreads();
   int jl, jh;
-  walk_levels(s_level, s->free_blocks, jl, jh);
+  walk_levels<kLevelThreads>(s_level, s->free_blocks, jl, jh);
   const double low = (double)jl / kLevels;
   constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
   int mine[kMine];
@@ -1500,12 +1504,12 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
   for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count[j];
   __syncthreads();
   int jl, jh;
-  walk_levels(s_level, free_blocks, jl, jh);
+  walk_levels<kBisectThreads>(s_level, free_blocks, jl, jh);
   __syncthreads();
   for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count2[j];
   __syncthreads();
   int jl2, jh2;
-  walk_levels(s_level, free_blocks, jl2, jh2);
+  walk_levels<kBisectThreads>(s_level, free_blocks, jl2, jh2);
   constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
   const double low1 = (double)jl / kLevels;
   double low = low1 + (double)jl2 * kSub, high = low1 + (double)jh2 * kSub;
@@ -1785,12 +1789,12 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const Max
   for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count[j];
   __syncthreads();
   int jl, jh;
-  walk_levels(s_level, free_blocks, jl, jh);
+  walk_levels<kBisectThreads>(s_level, free_blocks, jl, jh);
   __syncthreads();
   for (int j = tid; j < kLevels; j += kBisectThreads) s_level[j] = m.level_count2[j];
   __syncthreads();
   int jl2, jh2;
-  walk_levels(s_level, free_blocks, jl2, jh2);
+  walk_levels<kBisectThreads>(s_level, free_blocks, jl2, jh2);
   constexpr double kSub = 1.0 / ((double)kLevels * (double)kLevels);
   const double low1 = (double)jl / kLevels;
   double low = low1 + (double)jl2 * kSub, high = low1 + (double)jh2 * kSub;
