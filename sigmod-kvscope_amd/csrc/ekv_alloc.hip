@@ -1412,7 +1412,7 @@ __global__ __launch_bounds__(kLevelThreads) void mm_levels2_kernel(const MaxminP
     const int span = hi0 - lo0;
     const bool staged = span <= kStaged;
     __syncthreads();  // the previous request's searches are done with s_tot
-    if (staged) {
+    if (staged && span > 0) {
       // the whole bracket in one batch of loads (none under a condition), 6 or 24 a thread
       auto stage = [&](auto batch) {
         constexpr int B = decltype(batch)::value;
