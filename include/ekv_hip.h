@@ -373,7 +373,8 @@ int ekv_rank_uniform_ws(const float *scores, int64_t scores_stride, const int32_
  * may be NULL): budget, blocks of all rows, pinned blocks, status (1: the budget is below the
  * pinned blocks -- the reference raises ValueError -- and every block is kept), requests, free.
  * workspace: ekv_rank_sum_workspace(rows) bytes of device memory the call may overwrite (16 KB a
- * row of it lists the blocks left after the select's first digit).  rows at most 65535, width at most
+ * row of it lists the blocks left after the select's first digit).  rows at most 16777215 (the tie
+ * key holds the request in 16 bits up to 65536 requests, in up to 24 past them), width at most
  * 262144 (the first two passes stream the rows from memory; the later ones read the list, or the
  * rows again when it outgrows its room).
  */
@@ -389,7 +390,7 @@ int ekv_rank_sum(const double *scores, int64_t scores_stride, const int32_t *blo
  * the lowest retained share (pinned shares plus the kept open blocks, each request's open blocks
  * taken in stable descending share order) by the reference's 60-step bisection of the level, then
  * gives the leftover one block at a time to the request of the lowest (retained share, index).
- * rows <= 65535 (past 8192 requests the bisection keeps each request's state in the workspace),
+ * rows <= 16777215 (past 8192 requests the bisection keeps each request's state in the workspace),
  * width <= 262144 (requests up to 12288 blocks sort in LDS, wider ones in global memory, in a
  * second buffer the workspace includes; the level positions take 32 bits past 65535 blocks).
  * workspace:
@@ -416,7 +417,7 @@ int ekv_rank_maxmin(const double *scores, int64_t scores_stride, const int32_t *
  * past the row and in every row that takes no part.  summary (int64[6], may be NULL): budget, blocks
  * of the requests, pinned blocks, status, requests, free.  workspace:
  * ekv_controller_keep_workspace(objective, rows, width) bytes the call may overwrite.  rows at most
- * 65535, width at most 262144 (`maxmin` past 12288 blocks: rows x width below 2^31).
+ * 16777215, width at most 262144 (`maxmin` past 12288 blocks: rows x width below 2^31).
  */
 size_t ekv_controller_keep_workspace(int32_t objective, int32_t rows, int32_t width);
 int ekv_controller_keep(int32_t objective, const void *shares, int32_t shares_dtype, int64_t shares_stride,

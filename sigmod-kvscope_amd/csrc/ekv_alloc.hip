@@ -47,7 +47,7 @@ constexpr int kThreads = 256;
 constexpr int kMaxWidth = 12288;          // maxmin: a request sorted in one workgroup's LDS
 constexpr int kMaxMaxminWidth = 1 << 18;  // maxmin: positions in 16 bits up to 65535 blocks, 32 past it
 constexpr int kMaxSumWidth = 1 << 18;     // sum: the per-row loops stream the row; the tie key's block field
-constexpr int kMaxRows = 65535;  // the tie key holds the request in 16 bits
+constexpr int kMaxRows = (1 << 24) - 1;  // the tie key holds the request in 16 to 24 bits
 
 enum Mode : int { kSelect = 0, kKeepAll = 1, kKeepOpen = 2, kPinnedOnly = 3 };
 
@@ -95,6 +95,7 @@ struct Params {
   // over every block of the measured rows, from `ctl`, which also holds the request count
   double fraction;
   const struct CtlHeader *ctl;
+  int32_t tie_rbits;  // the request's bits in the tie key: 16, or as many as the request count needs
 };
 
 // Written by ctl_plan_kernel: the measured rows' blocks (freed ones included) and their count.
@@ -277,11 +278,18 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(const Params p) { deci
 __device__ __forceinline__ unsigned long long key_at(const Params &p, const RowStat &st, int r, int b) {
   return gain_key(weight_of(p, r) * share_of(p, st, r, b));
 }
-__device__ __forceinline__ unsigned long long tie_key(int r, int b) {
-  return ((unsigned long long)b << 16) | (unsigned long long)(0xFFFF - r);  // newer block, then earlier request
+__device__ __forceinline__ unsigned long long tie_key(const Params &p, int r, int b) {
+  const unsigned long long rmask = (1ull << p.tie_rbits) - 1ull;  // newer block, then earlier request
+  return ((unsigned long long)b << p.tie_rbits) | (rmask - (unsigned long long)r);
 }
-// the tie key's width: 16 bits of request below the block's bits (14 up to 16384 blocks, else 18)
-inline int tie_bits(int width) { return width <= (1 << 14) ? 30 : 34; }
+// the tie key's request bits: 16 up to 65536 requests, else as many as the last request's index needs
+inline int tie_request_bits(int rows) {
+  int bits = 16;
+  while (bits < 24 && rows > (1 << bits)) ++bits;
+  return bits;
+}
+// the tie key's width: the request's bits below the block's (14 up to 16384 blocks, else 18)
+inline int tie_bits(int width, int rbits) { return (width <= (1 << 14) ? 14 : 18) + rbits; }
 
 // The digit where the k_rem-th largest key lies, and the next pass's prefix, from the pass's
 // histogram: thread t holds the kBins / NT digits below kBins - (kBins / NT) t, in
@@ -459,7 +467,7 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(const Params p, int 
             unsigned long long k = 0ull;
             if (((run[i].inside & ~run[i].pinned) >> u) & 1u) {
               k = gain_key(weight[i] * share_value(st[i], run[i].score[u]));
-              counted = consider(k, tie_key(rr[i], b), digit);
+              counted = consider(k, tie_key(p, rr[i], b), digit);
             }
             count(counted, digit);
             if constexpr (cand_mode == 1) {  // list the counted blocks: one slot reservation (in LDS) per wave
@@ -472,7 +480,7 @@ __global__ __launch_bounds__(kHistThreads) void hist_kernel(const Params p, int 
                      __builtin_amdgcn_mbcnt_hi((uint32_t)(active >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)active, 0u));
                 if (counted && at < (unsigned int)room) {
                   p.cand[2 * (region + at)] = k;
-                  p.cand[2 * (region + at) + 1] = tie_key(rr[i], b);
+                  p.cand[2 * (region + at) + 1] = tie_key(p, rr[i], b);
                 }
               }
               if (b < p.width && !counted && rr[i] == r0 + i * G) {
@@ -527,7 +535,8 @@ __global__ __launch_bounds__(kHistThreads) void sum_keep_kernel(const Params p) 
     const unsigned long long *list = p.cand + 2 * region;
     for (int c = threadIdx.x; c < (int)listed; c += kHistThreads) {
       const unsigned long long key = list[2 * c], tk = list[2 * c + 1];
-      const int r = 0xFFFF - (int)(tk & 0xFFFFull), b = (int)(tk >> 16);
+      const unsigned long long rmask = (1ull << p.tie_rbits) - 1ull;
+      const int r = (int)(rmask - (tk & rmask)), b = (int)(tk >> p.tie_rbits);
       p.keep[(int64_t)r * p.keep_stride + b] = selected(key, tk);
     }
     return;
@@ -547,7 +556,7 @@ __global__ __launch_bounds__(kHistThreads) void sum_keep_kernel(const Params p) 
         if (error || b >= st.n || mode == kKeepAll || ((run.pinned >> u) & 1u)) k = 1;
         else if (mode == kKeepOpen) k = 1;
         else if (mode == kPinnedOnly) k = 0;
-        else k = selected(gain_key(weight * share_value(st, run.score[u])), tie_key(r, b));
+        else k = selected(gain_key(weight * share_value(st, run.score[u])), tie_key(p, r, b));
         krow[b] = k;
       }
     }
@@ -557,7 +566,7 @@ __global__ __launch_bounds__(kHistThreads) void sum_keep_kernel(const Params p) 
 // ---- maxmin --------------------------------------------------------------------------------
 constexpr int kBisectThreads = 1024;
 constexpr int kMaxMaxminRegRows = kBisectThreads * 8;  // at most 8 requests per bisection thread in registers
-constexpr int kMaxMaxminRows = 65535;                  // more than that many: the bisection state in memory
+constexpr int kMaxMaxminRows = (1 << 24) - 1;          // requests (past kMaxMaxminRegRows: the bisection state in memory)
 
 struct MaxminRow {
   double base;  // NumPy's sum of the pinned shares
@@ -1555,9 +1564,9 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
       f_mid[j] = count_at(j, mid, mid_pos[j]);
       local += f_mid[j];
     }
-    // the count (below 2^32) and the requests still changing, in one sum
-    const long long packed = block_sum<kBisectThreads>(local + (active << 32), s_red);
-    const long long total = packed & 0xffffffffll;
+    // the count (below 2^40) and the requests still changing (below 2^24), in one sum
+    const long long packed = block_sum<kBisectThreads>(local + (active << 40), s_red);
+    const long long total = packed & ((1ll << 40) - 1);
     const bool up = total <= free_blocks;
     if (up) low = mid; else high = mid;
 #pragma unroll
@@ -1572,7 +1581,7 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_kernel(const MaxminP
       }
     }
     ++it;
-    if ((packed >> 32) <= kWave) break;  // at most a wave's worth of requests can still change
+    if ((packed >> 40) <= kWave) break;  // at most a wave's worth of requests can still change
   }
   if (it < 60) {
     // the rest of the steps in wave 0 over the requests still changing, lane i taking the i-th; the
@@ -1834,8 +1843,8 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const Max
       m.b_pmid[r] = pos;
       local += f;
     }
-    const long long packed = block_sum<kBisectThreads>(local + (active << 32), s_red);
-    const long long total = packed & 0xffffffffll;
+    const long long packed = block_sum<kBisectThreads>(local + (active << 40), s_red);
+    const long long total = packed & ((1ll << 40) - 1);
     const bool up = total <= free_blocks;
     if (up) low = mid; else high = mid;
     for (int r = tid; r < rows; r += kBisectThreads) {
@@ -1848,7 +1857,7 @@ __global__ __launch_bounds__(kBisectThreads) void mm_bisect_mem_kernel(const Max
       }
     }
     ++it;
-    if ((packed >> 32) <= kWave) break;  // at most a wave's worth of requests can still change
+    if ((packed >> 40) <= kWave) break;  // at most a wave's worth of requests can still change
   }
   if (it < 60) {
     // the rest of the steps in wave 0 over the requests still changing, as in mm_bisect_kernel
@@ -2197,6 +2206,7 @@ namespace alloc {
 // The `sum` pipeline on prepared parameters (state and row statistics in place).
 int launch_sum(Params p, hipStream_t s) {
   const int rows = p.rows;
+  p.tie_rbits = tie_request_bits(rows);
   hipLaunchKernelGGL(alloc::prepare_kernel, dim3(rows), dim3(alloc::kPrepThreads), 0, s, p);
   hipLaunchKernelGGL(alloc::decide_kernel, dim3(1), dim3(alloc::kThreads), 0, s, p);
   const dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count()));
@@ -2218,7 +2228,7 @@ int launch_sum(Params p, hipStream_t s) {
   }
   // among the blocks at the threshold: newer block, earlier request (the tie key)
   static_assert(alloc::kMaxSumWidth <= (1 << 18), "the tie key's block field is at most 18 bits");
-  for (int top = tie_bits(p.width); top > 0; top -= alloc::kDigitBits) {
+  for (int top = tie_bits(p.width, p.tie_rbits); top > 0; top -= alloc::kDigitBits) {
     const int shift = std::max(top - alloc::kDigitBits, 0), bits = top - shift;
     hipLaunchKernelGGL(tied, grid, dim3(alloc::kHistThreads), 0, s, p, shift, bits, -1);
   }

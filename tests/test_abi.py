@@ -83,9 +83,11 @@ def test_shape_limits_are_refused_on_the_host():
     need = int(ekv_hip.load().ekv_rank_maxmin_workspace(8192, 262144))
     with pytest.raises(ValueError, match="workspace"):
         ekv_hip.call("ekv_rank_maxmin", P, 262144, P, 0, 0, 8192, 262144, 10, P, 262144, 0, P, need - 4096, 0)
-    # maxmin: more than 65535 requests
+    # sum and maxmin: 2^24 requests or more
     with pytest.raises(ValueError, match="rows"):
-        ekv_hip.call("ekv_rank_maxmin", P, 8, P, 0, 0, 65536, 8, 10, P, 8, 0, P, 1 << 30, 0)
+        ekv_hip.call("ekv_rank_maxmin", P, 8, P, 0, 0, 1 << 24, 8, 10, P, 8, 0, P, 1 << 30, 0)
+    with pytest.raises(ValueError, match="rows"):
+        ekv_hip.call("ekv_rank_sum", P, 8, P, 0, 0, 0, 1 << 24, 8, 10, P, 8, 0, P, 1 << 30, 0)
     with pytest.raises(ValueError, match="width"):
         ekv_hip.call("ekv_controller_keep", ekv_hip.OBJ_MAXMIN, P, ekv_hip.F64, wide, P, P, 0, 0, 0, 0, 4, wide,
                      4, 0, 0.5, P, wide, 0, P, 1 << 30, 0)

@@ -147,6 +147,47 @@ def test_sum_select_ending_at_the_first_digit():
         assert same(allocation.allocate(reqs, budget, "sum"), oa.allocate_sum(scores, pinned, [1.0] * 4, budget)), budget
 
 
+def test_sum_more_than_65536_requests():
+    # 70000 requests: the tie key's request field takes 17 bits; integer scores tie across requests
+    rng = np.random.default_rng(31)
+    rows, width = 70000, 6
+    scores = rng.integers(0, 3, size=(rows, width)).astype(np.float64)
+    sizes = rng.integers(1, width + 1, size=rows)
+    pinned = [oa.default_pins(int(n)) for n in sizes]
+    total = int(sizes.sum())
+    s_dev = torch.from_numpy(scores).cuda()
+    b_dev = torch.from_numpy(sizes.astype(np.int32)).cuda()
+    must = sum(int(p.sum()) for p in pinned)
+    for frac in (0.3, 0.6):
+        budget = must + int(frac * (total - must))
+        keep, summary = allocation.sum_keep(s_dev, b_dev, budget=budget)
+        got = keep.cpu().numpy()
+        want = oa.allocate_sum([scores[r, : sizes[r]] for r in range(rows)], pinned, [1.0] * rows, budget)
+        bad = sum(int((got[r, : sizes[r]].astype(bool) != want[r]).sum()) for r in range(rows))
+        print(f"sum over {rows} requests at {frac}: mismatched {bad}", flush=True)
+        assert bad == 0 and int(summary[4]) == rows
+
+
+def test_maxmin_more_than_65536_requests():
+    # 70000 requests: the bisection's state in memory, its summed count and active requests packed
+    rng = np.random.default_rng(32)
+    rows, width = 70000, 6
+    scores = rng.random((rows, width)) * rng.choice([1e-3, 1.0], size=(rows, 1))
+    sizes = rng.integers(1, width + 1, size=rows)
+    pinned = [oa.default_pins(int(n)) for n in sizes]
+    total = int(sizes.sum())
+    s_dev = torch.from_numpy(scores).cuda()
+    b_dev = torch.from_numpy(sizes.astype(np.int32)).cuda()
+    must = sum(int(p.sum()) for p in pinned)
+    budget = must + int(0.5 * (total - must))
+    keep, summary = allocation.maxmin_keep(s_dev, b_dev, budget=budget)
+    got = keep.cpu().numpy()
+    want = oa.allocate_maxmin([scores[r, : sizes[r]] for r in range(rows)], pinned, budget)
+    bad = sum(int((got[r, : sizes[r]].astype(bool) != want[r]).sum()) for r in range(rows))
+    print(f"maxmin over {rows} requests: mismatched {bad}", flush=True)
+    assert bad == 0 and int(summary[4]) == rows
+
+
 def test_sum_summary_flags_a_budget_below_the_pins():
     scores = torch.ones(2, 5, dtype=torch.float64, device="cuda")
     blocks = torch.tensor([5, 5], dtype=torch.int32, device="cuda")
