@@ -1151,217 +1151,254 @@ __global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const Maxmin
   }
 }
 
-// the running totals of the requests' sorted open shares (np.cumsum), in place, one float64 chain per
-// request added in order.  A dependent float64 add takes ~21 cycles here, so a chain's adds set the
-// time; what else the chain lane issues must fit beside them.  Per-element memory instructions from
-// a single lane do not: with a chain wave on every SIMD they queue in each CU's memory pipeline and
-// double the time.  So one wave runs kChainsPerWave chains, lane q the request order[kChainsPerWave w
-// + q] (the requests longest first, so a wave's chains have about the same length), each lane's loads
-// and stores being those of one instruction for all its chains.  The wave stages a chunk of each
-// request in LDS with coalesced loads (the next chunk's loads in flight meanwhile); a chain lane reads
-// two shares per 16-byte LDS read, a batch ahead of adding them, and leaves only each batch's last
-// total in LDS.  A level wave per chain (below) adds each batch of the chunk again from the total
-// before it (one lane a batch; the same float64 adds in the same order, so the same bits) and stores
-// the totals with whole-wave stores: a store per two elements from the chain lane had cost 19 µs of
-// its ~105.
+// The running totals of the requests' sorted open shares (np.cumsum: t_i = fl(t_{i-1} + x_i) from
+// t_{-1} = -0.0), in place, each request's by a wave in windows of kScanPer values a lane.  The
+// shares are at least 0 (or -0.0, or NaN), so the totals never fall.  While a total t lies in one
+// binade [2^E, 2^(E+1)), every float64 there is a multiple of its ulp u = 2^(E - 52), and as long as
+// t + x stays below 2^(E+1) the rounded sum is t plus x / u rounded to the nearest integer, times u:
+// x / u is exact (a scaling by a power of two) and, unless its fraction is exactly one half (a tie,
+// decided by the parity of t / u), rounds the same way whatever t is.  So a window's totals are
+// t + u * (inclusive prefix sums of those integers), an exact scan: every value up to the first
+// one that ties, leaves the binade or is not finite takes its total that way.  From that value on,
+// the next 64 values are added one at a time in order (a window stops where shares are about as
+// large as the total, which the values after it mostly are too), as are values while t is not a
+// positive normal float64 between 2^-960 and 2^1000 (-0.0 before the first value); a NaN total stays
+// NaN to the end.  The integers and their sums stay below 2^53 wherever they are used, so they are
+// exact in float64 too.  A long request of Dirichlet(0.1) shares takes ~11 windows of up to 1024
+// values and ~5 runs of 64 values added in order, against 8192 dependent adds of ~21 cycles for one
+// chain; a window is ~900 instructions of one wave.
 //
-// A level wave per chain places the levels j / kLevels (0 < j < kLevels) of the bisection's first
-// steps in each chunk's totals while the chain wave adds the next chunk: a request's count at a
-// level is its position among its totals shifted by 2r (np.searchsorted's left side, NaN above every
-// level), so the levels are placed in increasing order, those a chunk holds being those at or below
-// its last shifted total.  A lane takes a level: a binary search of the batches' last totals finds its batch,
-// whose totals the lane adds again from the batch before (the same float64 adds in the same order, so
-// the same bits) to find the position.  (A total per element in LDS would cost the chain lanes a
-// store per two elements, which slowed them by 15%; one level wave for both chains held them back at
-// the chunks that hold most levels.)  A level wave stores each position (level_pos) and adds the count
-// into the workgroup's counts in LDS, added into level_count once at the end, so the first walk of
-// the bisection needs no pass of its own.
+// Beside each request's scan wave, a level wave places the levels j / kLevels (0 < j < kLevels) of
+// the bisection's first steps in each chunk's totals while the scan wave takes the next chunk: a
+// request's count at a level is its position among its totals shifted by 2r (np.searchsorted's left
+// side, NaN above every level), so the levels are placed in increasing order, those a chunk holds
+// being those at or below its last shifted total, each by a binary search of the chunk's totals in
+// LDS.  The level wave also stores the chunk's totals with whole-wave stores.  It stores each
+// position (level_pos) and adds the count into the workgroup's counts in LDS, added into level_count
+// once at the end, so the first walk of the bisection needs no pass of its own.
 constexpr int kTotalsChunk = 1024;  // values per chunk and request: 16 per lane
-constexpr int kChainBatch = 16;     // values a chain lane reads from LDS a batch ahead of adding them
-constexpr int kChainsPerWave = 2;
-constexpr int kChunkPad = kTotalsChunk + 2;  // the requests' chunks a bank apart
-constexpr int kTotalsThreads = (1 + kChainsPerWave) * kWave;  // the chain wave, then a level wave per chain
-constexpr int kBatchEnds = kTotalsChunk / kChainBatch;  // last totals of a chunk's batches
+constexpr int kScanPer = 16;        // values a lane takes in a window
+constexpr int kTotalsReqs = 2;      // requests per workgroup: a scan wave and a level wave each
+constexpr int kTotalsThreads = 2 * kTotalsReqs * kWave;
+constexpr int kChunkSlots = kTotalsChunk + kTotalsChunk / 16;
+static_assert(kTotalsChunk == kWave * kScanPer, "a window of every lane's values covers a chunk");
+
+// a chunk's value e in LDS: one spare slot after every 16, so a lane's 16 values start 17 slots
+// after its neighbour's (two lanes a bank pair, not all of them)
+__device__ __forceinline__ int chunk_slot(int e) { return e + (e >> 4); }
+
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_ZERO = false>
+__device__ __forceinline__ double dpp_move_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const int lo = dpp_move<CTRL, ROW_MASK, BOUND_ZERO>((int)(uint32_t)b);
+  const int hi = dpp_move<CTRL, ROW_MASK, BOUND_ZERO>((int)(uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+// inclusive scan across the wave (wave_inclusive_scan's moves on both halves of a float64)
+__device__ __forceinline__ double wave_inclusive_scan_f64(double v) {
+  v += dpp_move_f64<0x111, 0xf, true>(v);
+  v += dpp_move_f64<0x112, 0xf, true>(v);
+  v += dpp_move_f64<0x114, 0xf, true>(v);
+  v += dpp_move_f64<0x118, 0xf, true>(v);
+  v += dpp_move_f64<0x142, 0xa>(v);
+  v += dpp_move_f64<0x143, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ double lane_f64(double v, int l) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// the totals of a chunk's first len values, in place in buf, from the total t before them; returns
+// the total after them.  One wave, every lane active.
+__device__ double scan_chunk(double *buf, int len, double t) {
+  const int lane = lane_id();
+  int pos = 0;
+  bool alone = false;
+  while (pos < len) {
+    const uint64_t tb = (uint64_t)__double_as_longlong(t);
+    const int eb = (int)((tb >> 52) & 0x7ff);  // t's biased exponent
+    if (t != t) {                               // NaN: every later total is NaN
+      for (int e = pos + lane; e < len; e += kWave) buf[chunk_slot(e)] = t;
+      return t;
+    }
+    if (alone || !(t > 0.0) || eb < 63 || eb > 2022) {
+      // -0.0, 0, below 2^-960 or above 2^1000, or after a window that stopped: the next kWave values
+      // added one at a time, lane k holding value pos + k (a window stops where shares are about as
+      // large as the total, which the values after it mostly are too)
+      const int run = min(len - pos, kWave);
+      const double x = buf[chunk_slot(pos + min(lane, run - 1))];
+      double mine = 0.0;
+      for (int k = 0; k < run; ++k) {
+        t += lane_f64(x, k);
+        if (lane == k) mine = t;
+      }
+      if (lane < run) buf[chunk_slot(pos + lane)] = mine;
+      pos += run;
+      alone = false;
+      continue;
+    }
+    const double u = __longlong_as_double((long long)((uint64_t)(eb - 52) << 52));     // 2^(E - 52)
+    const double inv = __longlong_as_double((long long)((uint64_t)(2098 - eb) << 52));  // 2^(52 - E)
+    const double room = 0x1p53 - t * inv;  // (2^(E+1) - t) / u, an integer
+    const int n = min(len - pos, kWave * kScanPer);
+    const int first = pos + lane * kScanPer;
+    double y[kScanPer], run[kScanPer];
+    bool fits[kScanPer];
+    double sum = 0.0;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+      const int e = first + k;
+      const double yy = buf[chunk_slot(min(e, len - 1))] * inv;  // every read issued, none under a condition
+      const bool in = e < pos + n && yy >= 0.0 && yy < 0x1p53;
+      const double r = __builtin_floor(yy), f = yy - r;
+      fits[k] = in && f != 0.5;
+      y[k] = yy;
+      sum += in ? r + (f > 0.5 ? 1.0 : 0.0) : 0.0;
+      run[k] = sum;  // this lane's inclusive prefix
+    }
+    // the lanes before this one: the scan of the sums moved one lane up (wave_shr:1), so a lane's own
+    // sum, which may hold values past its stop, never enters its prefix
+    const double before = wave_inclusive_scan_f64(dpp_move_f64<0x138, 0xf, true>(sum));
+    // the first value that cannot take the window: a tie, out of range, past the window, or one
+    // whose sum with the total before it reaches 2^(E+1)
+    int stop = kScanPer;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k) {
+      const double prior = before + (k > 0 ? run[k - 1] : 0.0);
+      if (stop == kScanPer && !(fits[k] && y[k] < room - prior)) stop = k;
+    }
+    const uint64_t stopped = __builtin_amdgcn_ballot_w64(stop < kScanPer);
+    const int sl = stopped ? __builtin_ctzll(stopped) : kWave;
+    const int taken = stopped ? sl * kScanPer + __builtin_amdgcn_readlane(stop, sl) : kWave * kScanPer;
+#pragma unroll
+    for (int k = 0; k < kScanPer; ++k)
+      if (lane * kScanPer + k < taken) buf[chunk_slot(first + k)] = t + (before + run[k]) * u;
+    if (taken > 0) {
+      const int last = taken - 1, kl = last % kScanPer;
+      double mine = 0.0;
+#pragma unroll
+      for (int k = 0; k < kScanPer; ++k)
+        if (k == kl) mine = before + run[k];
+      t = t + lane_f64(mine, last / kScanPer) * u;
+    }
+    pos += taken;
+    alone = taken < n;  // the value that stopped the window and those after it, one at a time
+  }
+  return t;
+}
 
 __global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminParams m) {
-  static_assert(kTotalsChunk % kWave == 0 && kTotalsChunk % (2 * kChainBatch) == 0, "whole steps per chunk");
   constexpr int kPer = kTotalsChunk / kWave;
-  constexpr int Q = kChainsPerWave;
-  // by chunk parity (the level wave reads one while the chain wave fills the other): a chunk's
-  // shares, and its batches' last totals
-  __shared__ __align__(16) double s_chunk[2][Q * kChunkPad];
-  __shared__ double s_ends[2][Q * kBatchEnds];
-  __shared__ int s_count[kLevels];  // the level wave's counts of the workgroup's requests
+  constexpr int Q = kTotalsReqs;
+  // by chunk parity (the level wave reads one while the scan wave fills the other): each request's
+  // chunk of shares, overwritten by their totals
+  __shared__ double s_chunk[2][Q][kChunkSlots];
+  __shared__ int s_count[kLevels];  // the level waves' counts of the workgroup's requests
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const bool chain_wave = wave == 0;
+  const bool scan_wave = wave < Q;
+  const int q = scan_wave ? wave : wave - Q;  // this wave's request in the workgroup
   for (int j = threadIdx.x; j < kLevels; j += kTotalsThreads) s_count[j] = 0;
   __syncthreads();
-  int req[Q], open[Q];
-  int longest = 0;
+  int longest = 0, req = -1, open = 0;
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int k = blockIdx.x * Q + q;
-    req[q] = k < m.p.rows ? m.order[k] : -1;
-    open[q] = req[q] >= 0 ? m.p.row_stat[req[q]].open : 0;
-    longest = max(longest, open[q]);
+  for (int i = 0; i < Q; ++i) {
+    const int k = blockIdx.x * Q + i;
+    const int r = k < m.p.rows ? m.order[k] : -1;
+    const int o = r >= 0 ? m.p.row_stat[r].open : 0;
+    longest = max(longest, o);
+    if (i == q) {
+      req = r;
+      open = o;
+    }
   }
   const int chunks = (longest + kTotalsChunk - 1) / kTotalsChunk;
-  const double *row[Q];
+  double *row = m.prefix + (int64_t)max(req, 0) * m.p.width;
+  // the scan wave: its request's next chunk in registers (loads at a clamped index, none under a
+  // condition; value 0 of request 0's row stands in for a missing request)
+  double v[kPer];
+  auto fetch = [&](int c0) {
 #pragma unroll
-  for (int q = 0; q < Q; ++q) row[q] = m.prefix + (int64_t)max(req[q], 0) * m.p.width;
-  // the chain wave: this lane's chain (lanes below Q), its request's row and length, and the chunk
-  // in registers
-  double v[Q][kPer];
-  if (chain_wave) {
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int i = j * kWave + lane;
-        v[q][j] = i < open[q] ? row[q][i] : 0.0;
-      }
-  }
-  // the level wave: per request, the next level to place, the total before the chunk, and the
-  // request's shift and base
-  int next[Q];
-  double shift[Q], base[Q], before[Q];
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    next[q] = 1;
-    before[q] = -0.0;
-    shift[q] = 2.0 * (double)max(req[q], 0);
-    base[q] = (!chain_wave && req[q] >= 0) ? m.mrow[req[q]].base : 0.0;
-  }
-  // -0.0 + x is x for every x, so the first total is the first share itself, as in np.cumsum
-  double acc = -0.0;
+    for (int j = 0; j < kPer; ++j) {
+      const int i = c0 + j * kWave + lane;
+      const double x = row[min(i, max(open - 1, 0))];
+      v[j] = i < open ? x : 0.0;
+    }
+  };
+  if (scan_wave) fetch(0);
+  int next = 1;  // the level wave: the next level to place
+  const double shift = 2.0 * (double)max(req, 0);
+  const double base = (!scan_wave && req >= 0) ? m.mrow[req].base : 0.0;
+  double t = -0.0;  // the scan wave: the total before the chunk
   for (int it = 0; it <= chunks; ++it) {
-    if (chain_wave && it < chunks) {
+    if (scan_wave && it < chunks) {
       const int c0 = it * kTotalsChunk;
-      double *buf = s_chunk[it & 1];
+      double *buf = s_chunk[it & 1][q];
 #pragma unroll
-      for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) buf[q * kChunkPad + j * kWave + lane] = v[q][j];
-      // the chain lanes read what every lane of the wave wrote
+      for (int j = 0; j < kPer; ++j) buf[chunk_slot(j * kWave + lane)] = v[j];
+      // the scan reads what every lane of the wave wrote
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int j = 0; j < kPer; ++j) {  // the next chunk
-          const int i = c0 + kTotalsChunk + j * kWave + lane;
-          v[q][j] = i < open[q] ? row[q][i] : 0.0;
-        }
-      const int steps = min(longest - c0, kTotalsChunk);  // positions every chain lane walks
-      if (lane < Q) {
-        // past the request's length the chain adds zeros (its total stays)
-        const double2 *pair = reinterpret_cast<const double2 *>(buf + lane * kChunkPad);
-        double *ends = s_ends[it & 1] + lane * kBatchEnds;
-        constexpr int kPairs = kChainBatch / 2;
-        auto read = [&](double2 (&x)[kPairs], int first) {  // a batch from `first`, or a dummy past the chunk
-          const int at = first < kTotalsChunk ? first / 2 : 0;
-#pragma unroll
-          for (int k = 0; k < kPairs; ++k) x[k] = pair[at + k];
-        };
-        auto add = [&](const double2 (&x)[kPairs], int first) {
-#pragma unroll
-          for (int k = 0; k < kPairs; ++k) {
-            acc += x[k].x;
-            acc += x[k].y;
-          }
-          ends[first / kChainBatch] = acc;
-        };
-        double2 xa[kPairs], xb[kPairs];
-        read(xa, 0);
-        for (int i = 0; i < steps; i += 2 * kChainBatch) {
-          read(xb, i + kChainBatch);
-          add(xa, i);
-          read(xa, i + 2 * kChainBatch);
-          add(xb, i + kChainBatch);
-        }
-      }
-    } else if (!chain_wave && it >= 1) {
-      // the previous chunk's totals: place every level at or below its last shifted total
+      fetch(c0 + kTotalsChunk);  // the next chunk, in flight during the scan
+      const int len = min(open - c0, kTotalsChunk);
+      if (len > 0) t = scan_chunk(buf, len, t);
+    } else if (!scan_wave && it >= 1) {
+      // the previous chunk's totals: store them, and place every level at or below its last shifted total
       const int c0 = (it - 1) * kTotalsChunk;
-      const double *buf = s_chunk[(it - 1) & 1];
+      const int len = min(open - c0, kTotalsChunk);
+      if (req >= 0 && len > 0) {
+        const double *tot = s_chunk[(it - 1) & 1][q];
+        {  // lane b stores values 16b .. 16b + 15
+          constexpr int kRun = kTotalsChunk / kWave;
+          const int e0 = lane * kRun;
+          double x[kRun];
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        const int len = min(open[q] - c0, kTotalsChunk);
-        if (q != wave - 1 || req[q] < 0 || len <= 0) continue;  // level wave q + 1 takes chain q
-        const double *share = buf + q * kChunkPad;
-        const double *ends = s_ends[(it - 1) & 1] + q * kBatchEnds;
-        const int nb = (len + kChainBatch - 1) / kChainBatch;  // past len a chain adds zeros: the last
-        const double last = ends[nb - 1] + shift[q];          // batch ends on the total at len - 1
-        {  // the totals: lane b adds batch b again from the total before it and stores those inside len
-          static_assert(kBatchEnds == kWave, "a lane per batch of a chunk");
-          const int b = lane;
-          double t = b > 0 ? ends[b - 1] : before[q];
-          double tot[kChainBatch];
+          for (int k = 0; k < kRun; ++k) x[k] = tot[chunk_slot(e0 + k)];
+          double *dst = row + c0 + e0;
+          if (e0 + kRun <= len) {
 #pragma unroll
-          for (int k = 0; k < kChainBatch; ++k) {
-            t += share[b * kChainBatch + k];
-            tot[k] = t;
-          }
-          double *dst = m.prefix + (int64_t)req[q] * m.p.width + c0 + b * kChainBatch;
-          if ((b + 1) * kChainBatch <= len) {
-#pragma unroll
-            for (int k = 0; k < kChainBatch; k += 2)
-              *reinterpret_cast<double2 *>(dst + k) = double2{tot[k], tot[k + 1]};
+            for (int k = 0; k < kRun; k += 2) *reinterpret_cast<double2 *>(dst + k) = double2{x[k], x[k + 1]};
           } else {
 #pragma unroll
-            for (int k = 0; k < kChainBatch; ++k)
-              if (b * kChainBatch + k < len) dst[k] = tot[k];
+            for (int k = 0; k < kRun; ++k)
+              if (e0 + k < len) dst[k] = x[k];
           }
         }
-        while (next[q] < kLevels) {
-          const int j = next[q] + lane;
-          const double need = (double)j / kLevels - base[q];
-          const double target = (need - 1e-12) + shift[q];
+        const double last = tot[chunk_slot(len - 1)] + shift;
+        while (next < kLevels) {
+          const int j = next + lane;
+          const double need = (double)j / kLevels - base;
+          const double target = (need - 1e-12) + shift;
           const bool here = j < kLevels && !(last < target);  // the lanes that hold one: a prefix of the wave
           if (here) {
-            int lo = 0, hi = nb - 1;  // the first batch whose last shifted total is not below the target
+            int lo = 0, hi = len - 1;  // the first total whose shifted value is not below the target
             while (lo < hi) {
               const int mid = (lo + hi) >> 1;
-              if (ends[mid] + shift[q] < target) lo = mid + 1;
+              if (tot[chunk_slot(mid)] + shift < target) lo = mid + 1;
               else hi = mid;
             }
-            // the batch's totals again, from the total before it: the first not below the target
-            double t = lo > 0 ? ends[lo - 1] : before[q];
-            int pos = kChainBatch - 1;
-            bool found = false;
-#pragma unroll
-            for (int k = 0; k < kChainBatch; ++k) {
-              t += share[lo * kChainBatch + k];
-              if (!found && !(t + shift[q] < target)) {
-                pos = k;
-                found = true;
-              }
-            }
-            pos += c0 + lo * kChainBatch;
-            set_pos(m, m.level_pos, req[q], j, pos);
-            const int count = need <= 1e-12 ? 0 : min(pos + 1, open[q]);
+            const int pos = c0 + lo;
+            set_pos(m, m.level_pos, req, j, pos);
+            const int count = need <= 1e-12 ? 0 : min(pos + 1, open);
             if (count > 0) atomicAdd(&s_count[j], count);
           }
           const int placed = __popcll(__ballot(here));
-          next[q] += placed;
+          next += placed;
           if (placed < kWave) break;
         }
-        before[q] = ends[kBatchEnds - 1];  // the total before the next chunk (this one was whole if it has one)
       }
     }
-    lds_barrier();  // a parity's totals are read before the chain wave refills it
+    lds_barrier();  // a parity's totals are read before the scan wave refills it
   }
-  if (!chain_wave) {  // the levels above every total: position `open`, count `open`
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      if (q != wave - 1 || req[q] < 0) continue;
-      for (int j = next[q] + lane; j < kLevels; j += kWave) {
-        set_pos(m, m.level_pos, req[q], j, open[q]);
-        const double need = (double)j / kLevels - base[q];
-        const int count = need <= 1e-12 ? 0 : open[q];
-        if (count > 0) atomicAdd(&s_count[j], count);
-      }
+  if (!scan_wave && req >= 0) {  // the levels above every total: position `open`, count `open`
+    for (int j = next + lane; j < kLevels; j += kWave) {
+      set_pos(m, m.level_pos, req, j, open);
+      const double need = (double)j / kLevels - base;
+      const int count = need <= 1e-12 ? 0 : open;
+      if (count > 0) atomicAdd(&s_count[j], count);
     }
   }
   __syncthreads();
@@ -2385,7 +2422,7 @@ int launch_maxmin(MaxminParams m, int rows, int width, hipStream_t s) {
     hipLaunchKernelGGL(alloc::mm_sort_kernel<12>, dim3(rows), dim3(alloc::kSortThreads), 0, s, m);
   rc = check_hip(hipGetLastError(), "ekv_rank_maxmin sort");
   if (rc != EKV_OK) return rc;
-  hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3((rows + alloc::kChainsPerWave - 1) / alloc::kChainsPerWave),
+  hipLaunchKernelGGL(alloc::mm_totals_kernel, dim3((rows + alloc::kTotalsReqs - 1) / alloc::kTotalsReqs),
                      dim3(alloc::kTotalsThreads), 0, s, m);
   const dim3 level_grid((unsigned)std::min<int64_t>(rows, (int64_t)cu_count() * 2));
   hipLaunchKernelGGL(alloc::mm_levels2_kernel, level_grid, dim3(alloc::kLevelThreads), 0, s, m);

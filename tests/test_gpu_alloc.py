@@ -199,6 +199,53 @@ def test_sum_summary_flags_a_budget_below_the_pins():
 
 # ---- maxmin ----------------------------------------------------------------------------------
 
+def test_maxmin_running_totals_are_numpy_cumsums_bit_for_bit():
+    # the running totals of each request's open shares sorted by share (np.cumsum) are read back from
+    # the workspace (the last rows x width float64 array before its 256-byte tail) and compared bit for
+    # bit: shares with full mantissas, whose sums round to ties about half the time while a share is
+    # within a binade of the total; coarse integer scores (many equal shares); exact binary fractions;
+    # shares across 300 decades; zero plateaus; lengths on both sides of the 1024-value chunks
+    rng = np.random.default_rng(33)
+    lengths = [1, 2, 3, 17, 1023, 1024, 1025, 1026, 2047, 2049, 3000, 4096, 5000, 8191, 8192, 8192,
+               6000, 7000, 8000, 300, 9000, 12288]
+    width = max(lengths)
+    rows = len(lengths)
+    scores = np.zeros((rows, width))
+    for r, n in enumerate(lengths):
+        kind = r % 6
+        if kind == 0:
+            x = rng.dirichlet(np.full(n, 0.1))
+        elif kind == 1:
+            x = rng.integers(1, 9, size=n).astype(np.float64)
+        elif kind == 2:
+            x = np.full(n, 0.25)
+        elif kind == 3:
+            x = rng.random(n) * 10.0 ** rng.uniform(-300, 0, size=n)
+        elif kind == 4:
+            x = rng.random(n)
+            x[rng.random(n) < 0.7] = 0.0
+        else:
+            x = rng.dirichlet(np.full(n, 10.0))
+        scores[r, :n] = x
+    need = allocation.maxmin_workspace_bytes(rows, width)
+    workspace = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    s_dev = torch.from_numpy(scores).cuda()
+    b_dev = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    total = sum(lengths)
+    must = sum(min(n, 2) for n in lengths)
+    allocation.maxmin_keep(s_dev, b_dev, budget=must + (total - must) // 2, workspace=workspace)
+    torch.cuda.synchronize()
+    raw = workspace.cpu().numpy()
+    cells = rows * width * 8
+    prefix = (-workspace.data_ptr()) % 256 + need - 256 - (cells + 255) // 256 * 256
+    for r, n in enumerate(lengths):
+        sh = oa.shares(scores[r, :n])
+        open_sh = sh[~oa.default_pins(n)]
+        want = np.cumsum(np.sort(open_sh)[::-1])
+        got = raw[prefix + r * width * 8: prefix + (r * width + len(want)) * 8].view(np.float64)
+        assert got.tobytes() == want.tobytes(), (n, r % 6, int(np.argmax(got != want)))
+
+
 @pytest.mark.parametrize("seed", range(40))
 def test_maxmin_random_requests(seed):
     rng = np.random.default_rng(seed)
