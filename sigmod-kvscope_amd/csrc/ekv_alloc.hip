@@ -1290,115 +1290,131 @@ __device__ double scan_chunk(double *buf, int len, double t) {
   return t;
 }
 
+// A request's scan wave and level wave hand its chunks over through kTotalsBufs LDS buffers and two
+// progress counters in LDS (chunks scanned, chunks placed), not a workgroup barrier per chunk, so the
+// scan runs up to kTotalsBufs - 1 chunks ahead of the placements (a request's first chunk holds most of
+// its levels).  The scan waits only for placements kTotalsBufs chunks back and the level wave only for
+// chunks already scanned, so neither waits on the other at once; each wait is also bounded by
+// kProgressSpins sleeps, which a run never reaches.
+constexpr int kTotalsBufs = 4;
+constexpr int kProgressSpins = 1 << 22;
+
+__device__ __forceinline__ void wait_progress(const int *counter, int target) {
+  for (int spin = 0; *(volatile const int *)counter < target && spin < kProgressSpins; ++spin)
+    __builtin_amdgcn_s_sleep(1);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+// every LDS access of the wave before it completes, then lane 0 raises the counter
+__device__ __forceinline__ void raise_progress(int *counter, int value) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (lane_id() == 0) *(volatile int *)counter = value;
+}
+
 __global__ __launch_bounds__(kTotalsThreads) void mm_totals_kernel(const MaxminParams m) {
   constexpr int kPer = kTotalsChunk / kWave;
   constexpr int Q = kTotalsReqs;
-  // by chunk parity (the level wave reads one while the scan wave fills the other): each request's
-  // chunk of shares, overwritten by their totals
-  __shared__ double s_chunk[2][Q][kChunkSlots];
+  // each request's chunks of shares in turn, overwritten by their totals
+  __shared__ double s_chunk[kTotalsBufs][Q][kChunkSlots];
   __shared__ int s_count[kLevels];  // the level waves' counts of the workgroup's requests
+  __shared__ int s_scanned[Q], s_placed[Q];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const bool scan_wave = wave < Q;
   const int q = scan_wave ? wave : wave - Q;  // this wave's request in the workgroup
   for (int j = threadIdx.x; j < kLevels; j += kTotalsThreads) s_count[j] = 0;
-  __syncthreads();
-  int longest = 0, req = -1, open = 0;
-#pragma unroll
-  for (int i = 0; i < Q; ++i) {
-    const int k = blockIdx.x * Q + i;
-    const int r = k < m.p.rows ? m.order[k] : -1;
-    const int o = r >= 0 ? m.p.row_stat[r].open : 0;
-    longest = max(longest, o);
-    if (i == q) {
-      req = r;
-      open = o;
-    }
+  if (threadIdx.x < Q) {
+    s_scanned[threadIdx.x] = 0;
+    s_placed[threadIdx.x] = 0;
   }
-  const int chunks = (longest + kTotalsChunk - 1) / kTotalsChunk;
+  __syncthreads();
+  const int k = blockIdx.x * Q + q;
+  const int req = k < m.p.rows ? m.order[k] : -1;
+  const int open = req >= 0 ? m.p.row_stat[req].open : 0;
+  const int chunks = (open + kTotalsChunk - 1) / kTotalsChunk;
   double *row = m.prefix + (int64_t)max(req, 0) * m.p.width;
-  // the scan wave: its request's next chunk in registers (loads at a clamped index, none under a
-  // condition; value 0 of request 0's row stands in for a missing request)
-  double v[kPer];
-  auto fetch = [&](int c0) {
+  if (scan_wave) {
+    // the request's next chunk in registers (loads at a clamped index, none under a condition;
+    // value 0 of request 0's row stands in for a missing request)
+    double v[kPer];
+    auto fetch = [&](int c0) {
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = c0 + j * kWave + lane;
-      const double x = row[min(i, max(open - 1, 0))];
-      v[j] = i < open ? x : 0.0;
-    }
-  };
-  if (scan_wave) fetch(0);
-  int next = 1;  // the level wave: the next level to place
-  const double shift = 2.0 * (double)max(req, 0);
-  const double base = (!scan_wave && req >= 0) ? m.mrow[req].base : 0.0;
-  double t = -0.0;  // the scan wave: the total before the chunk
-  for (int it = 0; it <= chunks; ++it) {
-    if (scan_wave && it < chunks) {
-      const int c0 = it * kTotalsChunk;
-      double *buf = s_chunk[it & 1][q];
+      for (int j = 0; j < kPer; ++j) {
+        const int i = c0 + j * kWave + lane;
+        const double x = row[min(i, max(open - 1, 0))];
+        v[j] = i < open ? x : 0.0;
+      }
+    };
+    fetch(0);
+    double t = -0.0;  // the total before the chunk
+    for (int c = 0; c < chunks; ++c) {
+      if (c >= kTotalsBufs) wait_progress(&s_placed[q], c - kTotalsBufs + 1);  // the buffer is free
+      double *buf = s_chunk[c % kTotalsBufs][q];
 #pragma unroll
       for (int j = 0; j < kPer; ++j) buf[chunk_slot(j * kWave + lane)] = v[j];
       // the scan reads what every lane of the wave wrote
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
-      fetch(c0 + kTotalsChunk);  // the next chunk, in flight during the scan
+      fetch((c + 1) * kTotalsChunk);  // the next chunk, in flight during the scan
+      t = scan_chunk(buf, min(open - c * kTotalsChunk, kTotalsChunk), t);
+      raise_progress(&s_scanned[q], c + 1);
+    }
+  } else {
+    int next = 1;  // the next level to place
+    const double shift = 2.0 * (double)max(req, 0);
+    const double base = req >= 0 ? m.mrow[req].base : 0.0;
+    for (int c = 0; c < chunks; ++c) {
+      // the chunk's totals: store them, and place every level at or below its last shifted total
+      wait_progress(&s_scanned[q], c + 1);
+      const int c0 = c * kTotalsChunk;
       const int len = min(open - c0, kTotalsChunk);
-      if (len > 0) t = scan_chunk(buf, len, t);
-    } else if (!scan_wave && it >= 1) {
-      // the previous chunk's totals: store them, and place every level at or below its last shifted total
-      const int c0 = (it - 1) * kTotalsChunk;
-      const int len = min(open - c0, kTotalsChunk);
-      if (req >= 0 && len > 0) {
-        const double *tot = s_chunk[(it - 1) & 1][q];
-        {  // lane b stores values 16b .. 16b + 15
-          constexpr int kRun = kTotalsChunk / kWave;
-          const int e0 = lane * kRun;
-          double x[kRun];
+      const double *tot = s_chunk[c % kTotalsBufs][q];
+      {  // lane b stores values 16b .. 16b + 15
+        constexpr int kRun = kTotalsChunk / kWave;
+        const int e0 = lane * kRun;
+        double x[kRun];
 #pragma unroll
-          for (int k = 0; k < kRun; ++k) x[k] = tot[chunk_slot(e0 + k)];
-          double *dst = row + c0 + e0;
-          if (e0 + kRun <= len) {
+        for (int i = 0; i < kRun; ++i) x[i] = tot[chunk_slot(e0 + i)];
+        double *dst = row + c0 + e0;
+        if (e0 + kRun <= len) {
 #pragma unroll
-            for (int k = 0; k < kRun; k += 2) *reinterpret_cast<double2 *>(dst + k) = double2{x[k], x[k + 1]};
-          } else {
+          for (int i = 0; i < kRun; i += 2) *reinterpret_cast<double2 *>(dst + i) = double2{x[i], x[i + 1]};
+        } else {
 #pragma unroll
-            for (int k = 0; k < kRun; ++k)
-              if (e0 + k < len) dst[k] = x[k];
-          }
-        }
-        const double last = tot[chunk_slot(len - 1)] + shift;
-        while (next < kLevels) {
-          const int j = next + lane;
-          const double need = (double)j / kLevels - base;
-          const double target = (need - 1e-12) + shift;
-          const bool here = j < kLevels && !(last < target);  // the lanes that hold one: a prefix of the wave
-          if (here) {
-            int lo = 0, hi = len - 1;  // the first total whose shifted value is not below the target
-            while (lo < hi) {
-              const int mid = (lo + hi) >> 1;
-              if (tot[chunk_slot(mid)] + shift < target) lo = mid + 1;
-              else hi = mid;
-            }
-            const int pos = c0 + lo;
-            set_pos(m, m.level_pos, req, j, pos);
-            const int count = need <= 1e-12 ? 0 : min(pos + 1, open);
-            if (count > 0) atomicAdd(&s_count[j], count);
-          }
-          const int placed = __popcll(__ballot(here));
-          next += placed;
-          if (placed < kWave) break;
+          for (int i = 0; i < kRun; ++i)
+            if (e0 + i < len) dst[i] = x[i];
         }
       }
+      const double last = tot[chunk_slot(len - 1)] + shift;
+      while (next < kLevels) {
+        const int j = next + lane;
+        const double need = (double)j / kLevels - base;
+        const double target = (need - 1e-12) + shift;
+        const bool here = j < kLevels && !(last < target);  // the lanes that hold one: a prefix of the wave
+        if (here) {
+          int lo = 0, hi = len - 1;  // the first total whose shifted value is not below the target
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (tot[chunk_slot(mid)] + shift < target) lo = mid + 1;
+            else hi = mid;
+          }
+          const int pos = c0 + lo;
+          set_pos(m, m.level_pos, req, j, pos);
+          const int count = need <= 1e-12 ? 0 : min(pos + 1, open);
+          if (count > 0) atomicAdd(&s_count[j], count);
+        }
+        const int placed = __popcll(__ballot(here));
+        next += placed;
+        if (placed < kWave) break;
+      }
+      raise_progress(&s_placed[q], c + 1);  // the chunk's buffer is free
     }
-    lds_barrier();  // a parity's totals are read before the scan wave refills it
-  }
-  if (!scan_wave && req >= 0) {  // the levels above every total: position `open`, count `open`
-    for (int j = next + lane; j < kLevels; j += kWave) {
-      set_pos(m, m.level_pos, req, j, open);
-      const double need = (double)j / kLevels - base;
-      const int count = need <= 1e-12 ? 0 : open;
-      if (count > 0) atomicAdd(&s_count[j], count);
+    if (req >= 0) {  // the levels above every total: position `open`, count `open`
+      for (int j = next + lane; j < kLevels; j += kWave) {
+        set_pos(m, m.level_pos, req, j, open);
+        const double need = (double)j / kLevels - base;
+        const int count = need <= 1e-12 ? 0 : open;
+        if (count > 0) atomicAdd(&s_count[j], count);
+      }
     }
   }
   __syncthreads();
