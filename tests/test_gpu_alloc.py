@@ -204,10 +204,11 @@ def test_maxmin_running_totals_are_numpy_cumsums_bit_for_bit():
     # the workspace (the last rows x width float64 array before its 256-byte tail) and compared bit for
     # bit: shares with full mantissas, whose sums round to ties about half the time while a share is
     # within a binade of the total; coarse integer scores (many equal shares); exact binary fractions;
-    # shares across 300 decades; zero plateaus; lengths on both sides of the 1024-value chunks
+    # shares across 300 decades; zero plateaus; lengths on both sides of the 1024-value chunks; a NaN
+    # score (every share NaN) and a +inf score (zero shares, then one NaN, which sorts last)
     rng = np.random.default_rng(33)
     lengths = [1, 2, 3, 17, 1023, 1024, 1025, 1026, 2047, 2049, 3000, 4096, 5000, 8191, 8192, 8192,
-               6000, 7000, 8000, 300, 9000, 12288]
+               6000, 7000, 8000, 300, 9000, 12288, 2500, 3100]
     width = max(lengths)
     rows = len(lengths)
     scores = np.zeros((rows, width))
@@ -226,6 +227,12 @@ def test_maxmin_running_totals_are_numpy_cumsums_bit_for_bit():
             x[rng.random(n) < 0.7] = 0.0
         else:
             x = rng.dirichlet(np.full(n, 10.0))
+        if r == len(lengths) - 2:
+            x = rng.random(n)
+            x[n // 3] = np.nan
+        elif r == len(lengths) - 1:
+            x = rng.random(n)
+            x[n // 2] = np.inf
         scores[r, :n] = x
     need = allocation.maxmin_workspace_bytes(rows, width)
     workspace = torch.zeros(need, dtype=torch.uint8, device="cuda")
@@ -239,11 +246,15 @@ def test_maxmin_running_totals_are_numpy_cumsums_bit_for_bit():
     cells = rows * width * 8
     prefix = (-workspace.data_ptr()) % 256 + need - 256 - (cells + 255) // 256 * 256
     for r, n in enumerate(lengths):
-        sh = oa.shares(scores[r, :n])
+        with np.errstate(invalid="ignore"):
+            sh = oa.shares(scores[r, :n])  # inf / inf is NaN
         open_sh = sh[~oa.default_pins(n)]
-        want = np.cumsum(np.sort(open_sh)[::-1])
+        nan = np.isnan(open_sh)
+        want = np.cumsum(np.concatenate([np.sort(open_sh[~nan])[::-1], open_sh[nan]]))
         got = raw[prefix + r * width * 8: prefix + (r * width + len(want)) * 8].view(np.float64)
-        assert got.tobytes() == want.tobytes(), (n, r % 6, int(np.argmax(got != want)))
+        assert np.array_equal(np.isnan(got), np.isnan(want)), (n, r)
+        fin = ~np.isnan(want)
+        assert got[fin].tobytes() == want[fin].tobytes(), (n, r % 6, int(np.argmax(got != want)))
 
 
 @pytest.mark.parametrize("seed", range(40))
