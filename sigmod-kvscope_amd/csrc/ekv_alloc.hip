@@ -1273,9 +1273,11 @@ __device__ double scan_chunk(double *buf, int len, double t) {
     const uint64_t stopped = __builtin_amdgcn_ballot_w64(stop < kScanPer);
     const int sl = stopped ? __builtin_ctzll(stopped) : kWave;
     const int taken = stopped ? sl * kScanPer + __builtin_amdgcn_readlane(stop, sl) : kWave * kScanPer;
+    // a value past the taken ones is written to the lane's spare slot (the one after values
+    // 16 lane .. 16 lane + 15, which no value maps to), so no store waits on a branch
 #pragma unroll
     for (int k = 0; k < kScanPer; ++k)
-      if (lane * kScanPer + k < taken) buf[chunk_slot(first + k)] = t + (before + run[k]) * u;
+      buf[lane * kScanPer + k < taken ? chunk_slot(first + k) : 17 * lane + 16] = t + (before + run[k]) * u;
     if (taken > 0) {
       const int last = taken - 1, kl = last % kScanPer;
       double mine = 0.0;
