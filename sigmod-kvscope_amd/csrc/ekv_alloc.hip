@@ -1164,9 +1164,9 @@ __global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const Maxmin
 // large as the total, which the values after it mostly are too), as are values while t is not a
 // positive normal float64 between 2^-960 and 2^1000 (-0.0 before the first value); a NaN total stays
 // NaN to the end.  The integers and their sums stay below 2^53 wherever they are used, so they are
-// exact in float64 too.  A long request of Dirichlet(0.1) shares takes ~11 windows of up to 1024
+// exact in float64 too.  A long request of Dirichlet(0.1) shares takes ~19 windows of up to 512
 // values and ~5 runs of 64 values added in order, against 8192 dependent adds of ~21 cycles for one
-// chain; a window is ~900 instructions of one wave.
+// chain.
 //
 // Beside each request's scan wave, a level wave places the levels j / kLevels (0 < j < kLevels) of
 // the bisection's first steps in each chunk's totals while the scan wave takes the next chunk: a
@@ -1177,11 +1177,11 @@ __global__ __launch_bounds__(kSortThreads) void mm_wide_sort_kernel(const Maxmin
 // position (level_pos) and adds the count into the workgroup's counts in LDS, added into level_count
 // once at the end, so the first walk of the bisection needs no pass of its own.
 constexpr int kTotalsChunk = 1024;  // values per chunk and request: 16 per lane
-constexpr int kScanPer = 16;        // values a lane takes in a window
+constexpr int kScanPer = 8;         // values a lane takes in a window (16: 6 us slower at 1024 x 8192)
 constexpr int kTotalsReqs = 2;      // requests per workgroup: a scan wave and a level wave each
 constexpr int kTotalsThreads = 2 * kTotalsReqs * kWave;
 constexpr int kChunkSlots = kTotalsChunk + kTotalsChunk / 16;
-static_assert(kTotalsChunk == kWave * kScanPer, "a window of every lane's values covers a chunk");
+static_assert(kTotalsChunk % (kWave * kScanPer) == 0, "whole windows per chunk");
 
 // a chunk's value e in LDS: one spare slot after every 16, so a lane's 16 values start 17 slots
 // after its neighbour's (two lanes a bank pair, not all of them)
